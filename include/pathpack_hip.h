@@ -1,0 +1,169 @@
+/*
+ * pathpack_hip.h -- C ABI of libpathpack_hip.so, the MI355X (gfx950) backend of PATHPACK.jl's multifrontal semiring
+ * LU path.
+ *
+ * The entry points replace what the reference computes on the CPU behind its public API (reference citations are
+ * file:line in AlgebraicJulia/PATHPACK.jl):
+ *
+ *   mlu(s, A; alg)        src/CPU/abstract_slu.jl:44-48      -> pp_symbolic + pp_factor
+ *   mstar(s, A; alg)      src/CPU/abstract_slu.jl:85-87      -> pp_symbolic + pp_factor + pp_star
+ *   Matrix(F)             src/CPU/abstract_slu.jl:10-14      -> pp_star
+ *   lmul!(F, B)           src/CPU/abstract_slu.jl:131-134    -> pp_lmul
+ *   rmul!(B, F)           src/CPU/abstract_slu.jl:142-145    -> pp_rmul
+ *   sgemx!(s, C, A, B)    src/CPU/dense/sgemx.jl:26-60       -> pp_sgemx           (dense kernel, device operands)
+ *   front LU + stars      ext/PATHPACKCUDAExt/batched/sgetrf.jl:11-120 -> pp_getrf_star_batched
+ *
+ * Conventions
+ *   - Matrices are column-major (Julia's layout).  A sparse matrix is CSC: colptr (n+1), rowval (nnz, 0-based,
+ *     sorted and unique within each column), nzval (nnz).  A[i, j] is the weight of the arc i -> j
+ *     (README.md:40-41).
+ *   - Indices and sizes are int64_t.  Element types: PP_F32 (float), PP_F64 (double), PP_I32 (int32_t, OrAnd only).
+ *   - Every function returns a pp_status; on failure pp_last_error(ctx) (or pp_last_error(NULL) for the functions
+ *     without a context) returns a message.  Nothing aborts and nothing throws across the ABI.  Sizes are
+ *     checked against free device memory before any work is launched (PP_ENOMEM).
+ *   - A pp_ctx owns one HIP stream on one device and every device buffer it allocates.  A context must not be
+ *     used by two threads at once; distinct contexts are independent.
+ *   - Host buffers passed in are borrowed for the duration of the call.
+ */
+#ifndef PATHPACK_HIP_H
+#define PATHPACK_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    PP_OK = 0,
+    PP_EINVAL = 1,        /* invalid argument (the reference's ArgumentError) */
+    PP_ENOMEM = 2,        /* not enough device memory; nothing was launched */
+    PP_EUNSUPPORTED = 3,  /* unsupported semiring / element type combination */
+    PP_EHIP = 4,          /* a HIP runtime call failed */
+    PP_ENODEV = 5         /* no usable GPU */
+} pp_status;
+
+/* Semirings (src/CPU/semiring/*.jl).  MinPlus/MaxPlus/MaxMin/MinMax/PlusProd take PP_F32 or PP_F64; OrAnd takes
+ * PP_I32. */
+typedef enum {
+    PP_MINPLUS = 0,   /* ([-Inf, Inf], min, +)   tropical.jl:15  */
+    PP_MAXPLUS = 1,   /* ([-Inf, Inf], max, +)   tropical.jl:31  */
+    PP_MAXMIN = 2,    /* ([-Inf, Inf], max, min) bottleneck.jl:31 */
+    PP_MINMAX = 3,    /* ([-Inf, Inf], min, max) bottleneck.jl:15 */
+    PP_PLUSPROD = 4,  /* ([0, Inf], +, *)        real.jl:16      */
+    PP_ORAND = 5      /* (2^n, |, &)             boolean.jl:31   */
+} pp_semiring;
+
+typedef enum { PP_F32 = 0, PP_F64 = 1, PP_I32 = 2 } pp_dtype;
+
+/* Orderings for pp_symbolic (the reference's `alg` keyword, abstract_slu.jl:44). */
+typedef enum {
+    PP_ORDER_ND = 0,       /* nested dissection (default) */
+    PP_ORDER_NATURAL = 1,  /* identity */
+    PP_ORDER_GIVEN = 2     /* the permutation passed in `perm` (perm[new] = old, 0-based) */
+} pp_ordering;
+
+typedef struct pp_ctx pp_ctx;
+typedef struct pp_sym pp_sym;
+typedef struct pp_fac pp_fac;
+
+/* ===== context ===== */
+
+/* Open a context on HIP device `device` (creates its stream).  Replaces nothing in the reference: Julia's threads
+ * need no handle. */
+pp_status pp_init(pp_ctx **ctx, int device);
+pp_status pp_destroy(pp_ctx *ctx);
+/* Message of the last failure on ctx; with ctx == NULL, of the calling thread's last context-free call. */
+const char *pp_last_error(const pp_ctx *ctx);
+/* Wait for all work queued on the context's stream. */
+pp_status pp_synchronize(pp_ctx *ctx);
+/* The context's HIP stream (hipStream_t) as an opaque pointer, for callers that order their own work after it. */
+pp_status pp_stream(pp_ctx *ctx, void **stream);
+
+/* ===== symbolic analysis (host only; no GPU needed) ===== */
+
+/* Order the symmetrized pattern of A, build the postordered supernodal elimination tree and the separators.
+ * Replaces ssymbolic(A; alg) (src/CPU/chordal_ssymbolic.jl:26-57) and the CliqueTrees calls behind it.
+ * ordering: pp_ordering; amalgamate: merge small fronts into their parents (1) or keep fundamental supernodes (0);
+ * perm: used when ordering == PP_ORDER_GIVEN, else may be NULL. */
+pp_status pp_symbolic(int64_t n, const int64_t *colptr, const int64_t *rowval, int ordering, int amalgamate,
+                      const int64_t *perm, pp_sym **sym);
+/* The symbolic structure for a given permutation (perm[new] = old) and partition of the permuted vertices into
+ * fronts (Rptr, nf + 1 entries, fronts in postorder), e.g. a structure the reference computed
+ * (docs/site_factors.jl:136-160 writes one).  Separators are derived. */
+pp_status pp_symbolic_given(int64_t n, const int64_t *colptr, const int64_t *rowval, const int64_t *perm, int64_t nf,
+                            const int64_t *Rptr, pp_sym **sym);
+/* Sizes: vertices, fronts, total separator length, largest front (nn + na). */
+pp_status pp_sym_size(const pp_sym *sym, int64_t *n, int64_t *nf, int64_t *nstgt, int64_t *maxfront);
+/* Copy out the structure (0-based): perm (n), Rptr (nf+1), Sptr (nf+1), Stgt (nstgt), parent (nf, -1 = root).
+ * Any pointer may be NULL. */
+pp_status pp_sym_export(const pp_sym *sym, int64_t *perm, int64_t *Rptr, int64_t *Sptr, int64_t *Stgt,
+                        int64_t *parent);
+/* Work counts in semiring multiply-adds, stats[0..9]: factor, star, one right-hand side, nnz(L) of the exact
+ * (fundamental-supernode) structure; the same four of the executed (amalgamated) structure; seconds spent in the
+ * ordering and in the whole analysis. */
+pp_status pp_sym_stats(const pp_sym *sym, double *stats);
+pp_status pp_sym_destroy(pp_sym *sym);
+
+/* ===== numeric factorization (device) ===== */
+
+/* mlu: upload the values of A (nzval, host, in the CSC order given to pp_symbolic) and factorize on the device,
+ * A* = U* L*.  Replaces copyto!(F, A) + lu!(F) (src/CPU/chordal_slu.jl:116-328, src/CPU/chordal/sgetrf.jl:3-290).
+ * The factor stays on the device; the symbolic object must outlive it. */
+pp_status pp_factor(pp_ctx *ctx, const pp_sym *sym, int semiring, int dtype, const void *nzval, pp_fac **fac);
+/* Same, with nzval already in device memory. */
+pp_status pp_factor_device(pp_ctx *ctx, const pp_sym *sym, int semiring, int dtype, const void *d_nzval,
+                           pp_fac **fac);
+/* Copy the factor to the host in the reference's layout (CliqueTrees' FChordalTriangular storage):
+ * LD/UD: diagonal blocks (sum nn^2; LD holds L (strict lower) + U, UD's upper triangle holds U),
+ * LL: na x nn blocks of L (sum nn*na), UL: nn x na blocks of U.  Pointers may be NULL. */
+pp_status pp_fac_export(pp_ctx *ctx, const pp_fac *fac, void *LD, void *UD, void *LL, void *UL);
+pp_status pp_fac_destroy(pp_fac *fac);
+
+/* ===== star and solves (device) ===== */
+
+/* Matrix(F): the full star A* (n x n, column-major, ldc >= n, original labels) into `out`: a device pointer when
+ * out_on_device != 0, else a host pointer (copied back through pinned staging).  Replaces sgetri!(F, C)
+ * (src/CPU/chordal_slu.jl:501-513 -> chordal/sgetri.jl:13-31, utils.jl:261-505). */
+pp_status pp_star(pp_ctx *ctx, const pp_fac *fac, void *out, int64_t ldc, int out_on_device);
+/* lmul!(F, B): B (n x nrhs, column-major, ldb >= n) <- A* B, the least solution of X = A X (+) B.
+ * B is a device pointer when on_device != 0, else a host pointer.  (abstract_slu.jl:131-134) */
+pp_status pp_lmul(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int64_t nrhs, int on_device);
+/* rmul!(B, F): B (nrhs x n, column-major, ldb >= nrhs) <- B A*, the least solution of X = X A (+) B.
+ * (abstract_slu.jl:142-145) */
+pp_status pp_rmul(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int64_t nrhs, int on_device);
+
+/* ===== dense kernels (device operands) ===== */
+
+/* C <- C (+) A (x) B over the semiring; A m x k, B k x n, C m x n, column-major device pointers.
+ * (src/CPU/dense/sgemx.jl:26-60, the reference GPU's sgemx_gpu! ext/PATHPACKCUDAExt/dense/sgemx.jl) */
+pp_status pp_sgemx(pp_ctx *ctx, int semiring, int dtype, int64_t m, int64_t n, int64_t k, const void *A, int64_t lda,
+                   const void *B, int64_t ldb, void *C, int64_t ldc);
+/* For each of `batch` dense nb x nb fronts (column-major, back to back, nb <= 64): A <- L + U (in place, no
+ * pivoting, dense/sgetrf.jl:151-175), TU <- U* and TL <- L* (unit lower), as the reference's fused front diagonal
+ * kernel (ext/PATHPACKCUDAExt/batched/sgetrf.jl:11-120).  Device pointers; TL or TU may be NULL. */
+pp_status pp_getrf_star_batched(pp_ctx *ctx, int semiring, int dtype, int64_t nb, int64_t batch, void *A, void *TL,
+                                void *TU);
+
+/* ===== device buffers ===== */
+
+pp_status pp_buffer_alloc(pp_ctx *ctx, size_t bytes, void **dptr);
+pp_status pp_buffer_free(pp_ctx *ctx, void *dptr);
+pp_status pp_upload(pp_ctx *ctx, void *dst_device, const void *src_host, size_t bytes);
+pp_status pp_download(pp_ctx *ctx, void *dst_host, const void *src_device, size_t bytes);
+
+/* ===== measurement ===== */
+
+/* Per-phase device time of the last pp_factor / pp_star / pp_lmul / pp_rmul on ctx, in seconds (HIP events on the
+ * context's stream): t[0] factor total, t[1] star U* sweep, t[2] star L* sweep, t[3] star relabel, t[4] solve,
+ * t[5] host-side setup of the last call, t[6] the dominant sweep kernel's summed duration, t[7] its launch count.
+ * Timing adds synchronization: enable with pp_set_timing(ctx, 1). */
+pp_status pp_set_timing(pp_ctx *ctx, int on);
+pp_status pp_get_timing(const pp_ctx *ctx, double *t);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PATHPACK_HIP_H */

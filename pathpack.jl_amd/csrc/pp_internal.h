@@ -1,0 +1,147 @@
+// pp_internal.h -- device plans for the factorization and the sweeps (internal).
+//
+// Factorization plan.  Every frontal matrix F_f (nj x nj, nj = nn + na, column-major, local order res(f) then
+// sep(f)) has a fixed place in one arena.  Fronts are grouped by height in the front tree (leaves 0); a height level
+// runs: extend-add of the children's update blocks F_c[nn_c:, nn_c:] into the parents (one workgroup per parent,
+// children one after another), then the partial LU of the fronts' first nn pivots.  Fronts with nj <= SMALL_NJ are
+// factorized by one workgroup in LDS; larger fronts take blocked steps of NB pivots: a panel kernel (LU of the
+// NB x NB diagonal block in LDS + triangular solves of the row and column panels) and a batched semiring GEMM on
+// the trailing block.  Afterwards the factor values are copied into the reference's storage layout and into
+// per-panel packs for the sweeps.
+//
+// Sweep plan.  Each front's residual is cut into panels of at most PANEL_W columns.  A panel p of front f covers
+// the permuted columns [c0, c0 + w); its "extension" E_p is the rest of the residual after the panel followed by
+// sep(f), i.e. the frontal-matrix local indices lo_ext .. nj-1 with lo_ext = c0 - Rptr[f] + w.  Packs:
+//   Dpack[p]: the panel's w x w diagonal block of F (L strict lower, U upper with diagonal), at i + j*w
+//   Upack[p]: U[c_j, E_t] at t*w + j          Lpack[p]: L[E_t, c_j] at t*w + j
+// A forward sweep visits panels leaves to root (each panel after its front's previous panel and after all
+// panels of its children), a backward sweep root to leaves.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "pp_symbolic.h"
+
+namespace pp {
+
+constexpr int SMALL_NJ = 64;   // fronts up to this size are factorized in one workgroup's LDS
+constexpr int NB = 32;         // pivot block of the blocked front factorization
+constexpr int PANEL_W = 32;    // widest sweep panel
+constexpr int SWEEP_ROWS = 256;  // rows of X per sweep workgroup (one per thread)
+constexpr int NCLASS = 6;      // sweep width classes 1, 2, 4, 8, 16, 32
+
+inline int width_class(int w) {
+    int c = 0;
+    while ((1 << c) < w) c++;
+    return c;
+}
+
+struct FactorPlan {
+    i64 nf = 0;
+    std::vector<int32_t> nn, na, nj;
+    std::vector<i64> Foff;           // arena offset of each front
+    i64 arena = 0;                   // elements
+    std::vector<int32_t> relpos;     // Sptr-aligned: local index of sep(f)[k] in bag(parent(f))
+    std::vector<i64> Sptr32;         // copy of Sptr (offsets into relpos)
+    std::vector<int32_t> chptr, chidx;   // children (CSR)
+    std::vector<i64> entry_pos;      // arena position of each stored entry of A
+    // schedule
+    struct Step {
+        i64 panel_off, panel_cnt;    // (front, chunk) pairs in ftask
+        i64 schur_off, schur_cnt;    // (front, ti, tj) triples in stask
+    };
+    struct Level {
+        i64 asm_off, asm_cnt;        // fronts with children, in flist
+        i64 small_off, small_cnt;    // fronts with nj <= SMALL_NJ, in flist
+        std::vector<Step> steps;     // blocked steps for the large fronts
+    };
+    std::vector<Level> levels;
+    std::vector<int32_t> flist;      // front lists of all levels
+    std::vector<int32_t> ftask;      // (front, step offset, chunk) per panel task: 3 ints
+    std::vector<int32_t> stask;      // (front, step offset, ti, tj) per Schur task: 4 ints
+    i64 max_nj = 0;
+};
+
+struct SweepPlan {
+    i64 np = 0;
+    // per panel
+    std::vector<int32_t> front, c0, w, e, lo_ext;
+    std::vector<i64> eoff, poff, doff;
+    std::vector<int32_t> rowA_lo, rowA_hi, rowB_lo, rowB_hi;   // rows of the star sweeps
+    std::vector<int32_t> Eidx;       // extension column indices (permuted labels)
+    i64 npack = 0, ndpack = 0;
+    struct List {
+        int cls;                     // width class
+        i64 off, cnt;                // panel ids in plist
+        i64 tA_off, tB_off;          // tile prefix sums (cnt + 1 each) for the star's row ranges
+    };
+    std::vector<List> fwd, bwd;      // in execution order
+    std::vector<int32_t> plist;
+    std::vector<int32_t> tiles;      // prefix sums of row tiles, per list: star forward / star backward
+    i64 max_e = 0;
+};
+
+std::string build_factor_plan(const Symbolic &S, FactorPlan &P);
+std::string build_sweep_plan(const Symbolic &S, const FactorPlan &F, SweepPlan &P);
+
+// Device copies of the plans.
+struct DevPlan {
+    // factor
+    int32_t *nn = nullptr, *na = nullptr, *nj = nullptr, *relpos = nullptr, *chptr = nullptr, *chidx = nullptr;
+    i64 *Foff = nullptr, *Sptr = nullptr, *entry_pos = nullptr;
+    int32_t *flist = nullptr, *ftask = nullptr, *stask = nullptr;
+    i64 *Dptr = nullptr, *Lptr = nullptr, *Rptr = nullptr;
+    // sweeps
+    int32_t *p_front = nullptr, *p_c0 = nullptr, *p_w = nullptr, *p_e = nullptr, *p_lo = nullptr;
+    i64 *p_eoff = nullptr, *p_poff = nullptr, *p_doff = nullptr;
+    int32_t *p_rowA_lo = nullptr, *p_rowA_hi = nullptr, *p_rowB_lo = nullptr, *p_rowB_hi = nullptr;
+    int32_t *Eidx = nullptr, *plist = nullptr, *tiles = nullptr;
+    // permutation
+    i64 *perm = nullptr, *invp = nullptr;
+    std::vector<void *> owned;
+};
+
+}  // namespace pp
+
+// Opaque handles of the C ABI.
+struct pp_sym {
+    pp::Symbolic S;
+    pp::FactorPlan *fplan = nullptr;
+    pp::SweepPlan *splan = nullptr;
+    ~pp_sym();
+};
+
+struct pp_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    int timing = 0;
+    double t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    hipEvent_t ev[8] = {};
+    void *staging = nullptr;        // pinned host staging for host outputs
+    size_t staging_bytes = 0;
+};
+
+struct pp_fac {
+    pp_ctx *ctx = nullptr;
+    const pp_sym *sym = nullptr;
+    int semiring = 0, dtype = 0;
+    pp::DevPlan plan;
+    void *LD = nullptr, *LL = nullptr, *UL = nullptr;     // reference layout
+    void *Dpack = nullptr, *Upack = nullptr, *Lpack = nullptr;
+    ~pp_fac();
+};
+
+namespace pp {
+// Numeric drivers (pp_device.hip).  Return "" or an error message.
+std::string device_factor(pp_ctx *ctx, pp_fac *fac, const void *d_nzval);
+std::string device_star(pp_ctx *ctx, const pp_fac *fac, void *d_out, i64 ldc);
+std::string device_rmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs);
+std::string device_lmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs);
+std::string device_sgemx(pp_ctx *ctx, int sr, int dt, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B,
+                         i64 ldb, void *C, i64 ldc);
+std::string device_getrf_star_batched(pp_ctx *ctx, int sr, int dt, i64 nb, i64 batch, void *A, void *TL, void *TU);
+}  // namespace pp

@@ -1,0 +1,846 @@
+// pp_kernels.h -- gfx950 kernels and the numeric drivers of the multifrontal semiring LU (templates).
+//
+// Included once per semiring/element type by the pp_inst_*.hip translation units, which instantiate the drivers.
+//
+// Reference behaviour (file:line in AlgebraicJulia/PATHPACK.jl):
+//   factorization     src/CPU/chordal/sgetrf.jl:35-290, src/CPU/dense/sgetrf.jl:151-175
+//   star              src/CPU/chordal/sgetri.jl:13-31 (X <- U*, X <- X L*), src/CPU/utils.jl:261-505 (relabel)
+//   solves            src/CPU/chordal_slu.jl:337-377, src/CPU/chordal/sgetrs.jl:29-51, src/CPU/chordal/strsx.jl
+//   dense GEMM        src/CPU/dense/sgemx.jl:606-635
+//   front LU + stars  ext/PATHPACKCUDAExt/batched/sgetrf.jl:11-120
+// The plans these kernels run are described in pp_internal.h.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+
+#include "pp_internal.h"
+#include "pp_semiring.h"
+
+namespace pp {
+
+#define HIPCHK(x)                                                                  \
+    do {                                                                           \
+        hipError_t e_ = (x);                                                       \
+        if (e_ != hipSuccess) return std::string(#x ": ") + hipGetErrorString(e_); \
+    } while (0)
+
+#define LAUNCHCHK()                                                                            \
+    do {                                                                                       \
+        hipError_t e_ = hipGetLastError();                                                     \
+        if (e_ != hipSuccess) return std::string("kernel launch: ") + hipGetErrorString(e_);   \
+    } while (0)
+
+constexpr int NT = 256;
+
+static inline unsigned grid1(i64 work, int per = NT) {
+    i64 g = (work + per - 1) / per;
+    return (unsigned)std::max<i64>(1, std::min<i64>(g, 1 << 20));
+}
+
+// ===== elementwise =====
+
+template <class T> __global__ void k_fill(T *__restrict__ p, i64 n, T v) {
+    for (i64 i = blockIdx.x * (i64)NT + threadIdx.x; i < n; i += (i64)gridDim.x * NT) p[i] = v;
+}
+
+template <class T>
+__global__ void k_scatter_entries(T *__restrict__ F, const i64 *__restrict__ pos, const T *__restrict__ val, i64 nnz) {
+    for (i64 i = blockIdx.x * (i64)NT + threadIdx.x; i < nnz; i += (i64)gridDim.x * NT) F[pos[i]] = val[i];
+}
+
+// X <- I in the semiring (the start of X <- U*)
+template <class S> __global__ void k_identity(typename S::value_type *__restrict__ X, i64 n) {
+    typedef typename S::value_type T;
+    for (i64 col = blockIdx.x; col < n; col += gridDim.x) {
+        T *x = X + col * n;
+        for (i64 i = threadIdx.x; i < n; i += NT) x[i] = i == col ? S::one() : S::zero();
+    }
+}
+
+// ===== extend-add: F_f <- F_f (+) inj M_c inj^T for every child c (sgetrf_send!, chordal/sgetrf.jl:257-290) =====
+
+template <class S>
+__global__ __launch_bounds__(NT) void k_assemble(typename S::value_type *__restrict__ F, const i64 *__restrict__ Foff,
+                                                 const int32_t *__restrict__ nn, const int32_t *__restrict__ na,
+                                                 const int32_t *__restrict__ nj, const i64 *__restrict__ Sptr,
+                                                 const int32_t *__restrict__ relpos, const int32_t *__restrict__ chptr,
+                                                 const int32_t *__restrict__ chidx, const int32_t *__restrict__ list) {
+    typedef typename S::value_type T;
+    const int f = list[blockIdx.x];
+    T *Ff = F + Foff[f];
+    const int ldf = nj[f];
+    for (int q = chptr[f]; q < chptr[f + 1]; q++) {
+        const int c = chidx[q];
+        const int nc = na[c], ldc = nj[c], off = nn[c];
+        const T *M = F + Foff[c] + off + (i64)off * ldc;
+        const int32_t *rp = relpos + Sptr[c];
+        const int cnt = nc * nc;
+        for (int e = threadIdx.x; e < cnt; e += NT) {
+            const int v = e % nc, w = e / nc;
+            T *dst = Ff + rp[v] + (i64)rp[w] * ldf;
+            *dst = S::plus(*dst, M[v + (i64)w * ldc]);
+        }
+        __syncthreads();
+    }
+}
+
+// ===== dense LU of an n x n block in LDS (ld = lda), first p pivots (dense/sgetrf.jl:151-175) =====
+
+template <class S>
+__device__ inline void lds_lu(typename S::value_type *A, int n, int lda, int p) {
+    for (int i = 0; i < p; i++) {
+        if (!S::integral) {
+            const typename S::value_type s = S::star(A[i + i * lda]);
+            for (int k = i + 1 + threadIdx.x; k < n; k += NT) A[k + i * lda] = S::prod(A[k + i * lda], s);
+            __syncthreads();
+        }
+        const int m = n - i - 1;
+        for (int e = threadIdx.x; e < m * m; e += NT) {
+            const int k = i + 1 + e % m, j = i + 1 + e / m;
+            A[k + j * lda] = S::muladd(A[k + i * lda], A[i + j * lda], A[k + j * lda]);
+        }
+        __syncthreads();
+    }
+}
+
+// fronts with nj <= SMALL_NJ: the whole partial LU (nn pivots of the nj x nj front) in one workgroup
+template <class S>
+__global__ __launch_bounds__(NT) void k_front_small(typename S::value_type *__restrict__ F, const i64 *__restrict__ Foff,
+                                                    const int32_t *__restrict__ nn, const int32_t *__restrict__ nj,
+                                                    const int32_t *__restrict__ list) {
+    typedef typename S::value_type T;
+    __shared__ T A[SMALL_NJ * SMALL_NJ];
+    const int f = list[blockIdx.x];
+    const int n = nj[f], p = nn[f];
+    T *G = F + Foff[f];
+    for (int e = threadIdx.x; e < n * n; e += NT) A[e] = G[e];
+    __syncthreads();
+    lds_lu<S>(A, n, n, p);
+    for (int e = threadIdx.x; e < n * n; e += NT) G[e] = A[e];
+}
+
+// large fronts, step at pivot `off`: LU of the b x b diagonal block (redundantly in every chunk), then the chunk's
+// rows of the column panel (L <- L U_kk*, right upper non-unit) and columns of the row panel (U <- L_kk* U, left
+// lower unit).
+template <class S>
+__global__ __launch_bounds__(NT) void k_front_panel(typename S::value_type *__restrict__ F, const i64 *__restrict__ Foff,
+                                                    const int32_t *__restrict__ nn, const int32_t *__restrict__ nj,
+                                                    const int32_t *__restrict__ tasks) {
+    typedef typename S::value_type T;
+    constexpr int LD = NB + 1;
+    __shared__ T D[NB * LD];
+    const int32_t *t = tasks + 3 * (i64)blockIdx.x;
+    const int f = t[0], off = t[1], chunk = t[2];
+    const int n = nj[f];
+    const int b = min(NB, nn[f] - off);
+    const int m0 = off + b;
+    T *A = F + Foff[f];
+    for (int e = threadIdx.x; e < b * b; e += NT) {
+        const int i = e % b, j = e / b;
+        D[i + j * LD] = A[(off + i) + (i64)(off + j) * n];
+    }
+    __syncthreads();
+    lds_lu<S>(D, b, LD, b);
+    if (chunk == 0)
+        for (int e = threadIdx.x; e < b * b; e += NT) {
+            const int i = e % b, j = e / b;
+            A[(off + i) + (i64)(off + j) * n] = D[i + j * LD];
+        }
+    const int r = m0 + chunk * NT + threadIdx.x;
+    if (r < n) {
+        // row r of the column panel
+        T x[NB];
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+            if (j < b) x[j] = A[r + (i64)(off + j) * n];
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            if (j < b) {
+                T acc = x[j];
+#pragma unroll
+                for (int i = 0; i < j; i++) acc = S::muladd(x[i], D[i + j * LD], acc);
+                if (!S::integral) acc = S::prod(acc, S::star(D[j + j * LD]));
+                x[j] = acc;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+            if (j < b) A[r + (i64)(off + j) * n] = x[j];
+        // column r of the row panel
+        T y[NB];
+#pragma unroll
+        for (int i = 0; i < NB; i++)
+            if (i < b) y[i] = A[(off + i) + (i64)r * n];
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            if (i < b) {
+                T acc = y[i];
+#pragma unroll
+                for (int k = 0; k < i; k++) acc = S::muladd(D[i + k * LD], y[k], acc);
+                y[i] = acc;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NB; i++)
+            if (i < b) A[(off + i) + (i64)r * n] = y[i];
+    }
+}
+
+// ===== semiring GEMM tile: C[64 x 64] <- C (+) A[64 x k] (x) B[k x 64], column-major operands =====
+
+constexpr int GT = 64, GK = 32;
+
+template <class S>
+__device__ inline void gemm_tile(typename S::value_type *__restrict__ C, i64 ldc, const typename S::value_type *__restrict__ A,
+                                 i64 lda, const typename S::value_type *__restrict__ B, i64 ldb, int m, int n, int k) {
+    typedef typename S::value_type T;
+    __shared__ T As[GK][GT + 4];
+    __shared__ T Bs[GK][GT + 4];
+    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    T acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = tx * 4 + i, c = ty * 4 + j;
+            acc[i][j] = (r < m && c < n) ? C[r + c * ldc] : S::zero();
+        }
+    for (int k0 = 0; k0 < k; k0 += GK) {
+        const int kc = min(GK, k - k0);
+        __syncthreads();
+        for (int e = threadIdx.x; e < GK * GT; e += NT) {
+            const int r = e % GT, kk = e / GT;
+            As[kk][r] = (kk < kc && r < m) ? A[r + (i64)(k0 + kk) * lda] : S::zero();
+        }
+        for (int e = threadIdx.x; e < GK * GT; e += NT) {
+            const int kk = e % GK, c = e / GK;
+            Bs[kk][c] = (kk < kc && c < n) ? B[(k0 + kk) + (i64)c * ldb] : S::zero();
+        }
+        __syncthreads();
+        for (int kk = 0; kk < kc; kk++) {
+            T a[4], bb[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) a[i] = As[kk][tx * 4 + i];
+#pragma unroll
+            for (int j = 0; j < 4; j++) bb[j] = Bs[kk][ty * 4 + j];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = S::muladd(a[i], bb[j], acc[i][j]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = tx * 4 + i, c = ty * 4 + j;
+            if (r < m && c < n) C[r + c * ldc] = acc[i][j];
+        }
+}
+
+// Schur update of the large fronts: F22 <- F22 (+) L_panel (x) U_panel (sgemx_mt!, chordal/sgetrf.jl:146)
+template <class S>
+__global__ __launch_bounds__(NT) void k_front_schur(typename S::value_type *__restrict__ F, const i64 *__restrict__ Foff,
+                                                    const int32_t *__restrict__ nn, const int32_t *__restrict__ nj,
+                                                    const int32_t *__restrict__ tasks) {
+    typedef typename S::value_type T;
+    const int32_t *t = tasks + 4 * (i64)blockIdx.x;
+    const int f = t[0], off = t[1], ti = t[2], tj = t[3];
+    const int n = nj[f];
+    const int b = min(NB, nn[f] - off);
+    const int m0 = off + b;
+    const int r0 = m0 + ti * GT, c0 = m0 + tj * GT;
+    T *A = F + Foff[f];
+    gemm_tile<S>(A + r0 + (i64)c0 * n, n, A + r0 + (i64)off * n, n, A + off + (i64)c0 * n, n, min(GT, n - r0),
+                 min(GT, n - c0), b);
+}
+
+template <class S>
+__global__ __launch_bounds__(NT) void k_gemm(typename S::value_type *__restrict__ C, i64 ldc,
+                                             const typename S::value_type *__restrict__ A, i64 lda,
+                                             const typename S::value_type *__restrict__ B, i64 ldb, i64 m, i64 n, i64 k) {
+    const i64 r0 = (i64)blockIdx.x * GT, c0 = (i64)blockIdx.y * GT;
+    gemm_tile<S>(C + r0 + c0 * ldc, ldc, A + r0, lda, B + c0 * ldb, ldb, (int)min<i64>(GT, m - r0),
+                 (int)min<i64>(GT, n - c0), (int)k);
+}
+
+// ===== factor extraction: the reference layout and the sweep packs =====
+
+// LD (nn x nn at Dptr), LL (na x nn at Lptr), UL (nn x na at Lptr), one workgroup per front
+template <class T>
+__global__ __launch_bounds__(NT) void k_extract_ref(const T *__restrict__ F, const i64 *__restrict__ Foff,
+                                                   const int32_t *__restrict__ nn, const int32_t *__restrict__ nj,
+                                                   const i64 *__restrict__ Dptr, const i64 *__restrict__ Lptr,
+                                                   T *__restrict__ LD, T *__restrict__ LL, T *__restrict__ UL) {
+    const int f = blockIdx.x;
+    const int a = nn[f], n = nj[f], c = n - a;
+    const T *G = F + Foff[f];
+    for (int e = threadIdx.x; e < a * a; e += NT) LD[Dptr[f] + e] = G[(e % a) + (i64)(e / a) * n];
+    for (int e = threadIdx.x; e < a * c; e += NT) {
+        const int r = e % c, col = e / c;   // LL[r, col] = F[a + r, col]
+        LL[Lptr[f] + e] = G[(a + r) + (i64)col * n];
+    }
+    for (int e = threadIdx.x; e < a * c; e += NT) {
+        const int r = e % a, col = e / a;   // UL[r, col] = F[r, a + col]
+        UL[Lptr[f] + e] = G[r + (i64)(a + col) * n];
+    }
+}
+
+// Dpack / Upack / Lpack of every panel, one workgroup per panel
+template <class T>
+__global__ __launch_bounds__(NT) void k_build_packs(const T *__restrict__ F, const i64 *__restrict__ Foff,
+                                                   const int32_t *__restrict__ nj, const i64 *__restrict__ Rptr,
+                                                   const int32_t *__restrict__ p_front, const int32_t *__restrict__ p_c0,
+                                                   const int32_t *__restrict__ p_w, const int32_t *__restrict__ p_e,
+                                                   const int32_t *__restrict__ p_lo, const i64 *__restrict__ p_poff,
+                                                   const i64 *__restrict__ p_doff, T *__restrict__ Dpack,
+                                                   T *__restrict__ Upack, T *__restrict__ Lpack) {
+    const int p = blockIdx.x;
+    const int f = p_front[p], w = p_w[p], e = p_e[p], lo = p_lo[p];
+    const int n = nj[f];
+    const int lj0 = p_c0[p] - (int)Rptr[f];
+    const T *G = F + Foff[f];
+    for (int q = threadIdx.x; q < w * w; q += NT) {
+        const int i = q % w, j = q / w;
+        Dpack[p_doff[p] + q] = G[(lj0 + i) + (i64)(lj0 + j) * n];
+    }
+    for (int q = threadIdx.x; q < w * e; q += NT) {
+        const int j = q % w, t = q / w;   // element (j, t) at t*w + j
+        Upack[p_poff[p] + q] = G[(lj0 + j) + (i64)(lo + t) * n];
+        Lpack[p_poff[p] + q] = G[(lo + t) + (i64)(lj0 + j) * n];
+    }
+}
+
+// ===== sweeps over the rows of X (X column-major, ld rows) =====
+//
+// Forward (leaves to root), one panel with columns c_0..c_{w-1}:
+//   x_j <- (x_j (+) sum_{i<j} x_i (x) D(i,j)) (x) star(D(j,j))?,   then   X[:, E_t] <- X[:, E_t] (+) sum_j x_j (x) P(j,t)
+// Backward (root to leaves):
+//   x_j <- x_j (+) sum_t X[:, E_t] (x) Q(t,j),   then   x_j <- (x_j (+) sum_{i>j} x_i (x) D(i,j)) (x) star(D(j,j))?
+// DMODE 0 reads the panel block as stored (U upper for forward with star, L strict lower for backward, unit);
+// DMODE 1 reads it transposed (L^T for forward, unit; U^T for backward with star), which is how lmul! runs on the
+// transposed right-hand sides.  One thread per row; the column indices and pack values are wave-uniform.
+
+struct SweepArgs {
+    const int32_t *plist, *tiles;   // tiles: prefix sums of row tiles (null: uniform [0, nrows))
+    int32_t np, nrows;
+    const int32_t *p_c0, *p_w, *p_e, *row_lo, *row_hi;
+    const i64 *p_eoff, *p_poff, *p_doff;
+    const int32_t *Eidx;
+};
+
+__device__ inline void locate(const SweepArgs &a, int &pi, int &tile) {
+    const int bid = blockIdx.x;
+    if (a.tiles) {
+        int lo = 0, hi = a.np;   // largest lo with tiles[lo] <= bid
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (a.tiles[mid] <= bid) lo = mid;
+            else hi = mid;
+        }
+        pi = lo;
+        tile = bid - a.tiles[lo];
+    } else {
+        pi = bid % a.np;
+        tile = bid / a.np;
+    }
+}
+
+template <class S, int W, int DMODE>
+__global__ __launch_bounds__(NT) void k_sweep_fwd(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
+                                                  const typename S::value_type *__restrict__ Dpack,
+                                                  const typename S::value_type *__restrict__ P) {
+    typedef typename S::value_type T;
+    int pi, tile;
+    locate(a, pi, tile);
+    const int p = a.plist[pi];
+    const int lo = a.tiles ? a.row_lo[p] : 0, hi = a.tiles ? a.row_hi[p] : a.nrows;
+    const int r = lo + tile * NT + threadIdx.x;
+    if (r >= hi) return;
+    const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
+    const T *D = Dpack + a.p_doff[p];
+    const T *Pp = P + a.p_poff[p];
+    const int32_t *E = a.Eidx + a.p_eoff[p];
+    T x[W];
+#pragma unroll
+    for (int j = 0; j < W; j++)
+        if (j < w) x[j] = X[(i64)(c0 + j) * ld + r];
+#pragma unroll
+    for (int j = 0; j < W; j++) {
+        if (j < w) {
+            T acc = x[j];
+#pragma unroll
+            for (int i = 0; i < j; i++) acc = S::muladd(x[i], DMODE == 0 ? D[i + j * w] : D[j + i * w], acc);
+            if (DMODE == 0 && !S::integral) acc = S::prod(acc, S::star(D[j + j * w]));
+            x[j] = acc;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < W; j++)
+        if (j < w) X[(i64)(c0 + j) * ld + r] = x[j];
+    int t = 0;
+    for (; t + 4 <= e; t += 4) {
+        T *y0 = X + (i64)E[t] * ld, *y1 = X + (i64)E[t + 1] * ld, *y2 = X + (i64)E[t + 2] * ld, *y3 = X + (i64)E[t + 3] * ld;
+        T v0 = y0[r], v1 = y1[r], v2 = y2[r], v3 = y3[r];
+        const T *q = Pp + (i64)t * w;
+#pragma unroll
+        for (int j = 0; j < W; j++)
+            if (j < w) {
+                v0 = S::muladd(x[j], q[j], v0);
+                v1 = S::muladd(x[j], q[w + j], v1);
+                v2 = S::muladd(x[j], q[2 * w + j], v2);
+                v3 = S::muladd(x[j], q[3 * w + j], v3);
+            }
+        y0[r] = v0;
+        y1[r] = v1;
+        y2[r] = v2;
+        y3[r] = v3;
+    }
+    for (; t < e; t++) {
+        T *y = X + (i64)E[t] * ld;
+        T v = y[r];
+        const T *q = Pp + (i64)t * w;
+#pragma unroll
+        for (int j = 0; j < W; j++)
+            if (j < w) v = S::muladd(x[j], q[j], v);
+        y[r] = v;
+    }
+}
+
+template <class S, int W, int DMODE>
+__global__ __launch_bounds__(NT) void k_sweep_bwd(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
+                                                  const typename S::value_type *__restrict__ Dpack,
+                                                  const typename S::value_type *__restrict__ Q) {
+    typedef typename S::value_type T;
+    int pi, tile;
+    locate(a, pi, tile);
+    const int p = a.plist[pi];
+    const int lo = a.tiles ? a.row_lo[p] : 0, hi = a.tiles ? a.row_hi[p] : a.nrows;
+    const int r = lo + tile * NT + threadIdx.x;
+    if (r >= hi) return;
+    const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
+    const T *D = Dpack + a.p_doff[p];
+    const T *Qp = Q + a.p_poff[p];
+    const int32_t *E = a.Eidx + a.p_eoff[p];
+    T acc[W];
+#pragma unroll
+    for (int j = 0; j < W; j++)
+        if (j < w) acc[j] = X[(i64)(c0 + j) * ld + r];
+    int t = 0;
+    for (; t + 4 <= e; t += 4) {
+        const T v0 = X[(i64)E[t] * ld + r], v1 = X[(i64)E[t + 1] * ld + r], v2 = X[(i64)E[t + 2] * ld + r],
+                v3 = X[(i64)E[t + 3] * ld + r];
+        const T *q = Qp + (i64)t * w;
+#pragma unroll
+        for (int j = 0; j < W; j++)
+            if (j < w) {
+                T s = acc[j];
+                s = S::muladd(v0, q[j], s);
+                s = S::muladd(v1, q[w + j], s);
+                s = S::muladd(v2, q[2 * w + j], s);
+                s = S::muladd(v3, q[3 * w + j], s);
+                acc[j] = s;
+            }
+    }
+    for (; t < e; t++) {
+        const T v = X[(i64)E[t] * ld + r];
+        const T *q = Qp + (i64)t * w;
+#pragma unroll
+        for (int j = 0; j < W; j++)
+            if (j < w) acc[j] = S::muladd(v, q[j], acc[j]);
+    }
+#pragma unroll
+    for (int j = W - 1; j >= 0; j--) {
+        if (j < w) {
+            T s = acc[j];
+#pragma unroll
+            for (int i = j + 1; i < W; i++)
+                if (i < w) s = S::muladd(acc[i], DMODE == 0 ? D[i + j * w] : D[j + i * w], s);
+            if (DMODE == 1 && !S::integral) s = S::prod(s, S::star(D[j + j * w]));
+            acc[j] = s;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < W; j++)
+        if (j < w) X[(i64)(c0 + j) * ld + r] = acc[j];
+}
+
+// ===== relabel and permutations =====
+
+// C[i, j] = X[invp[i], invp[j]]  (C <- P^-1 X Q^-1, permuterowscols!, utils.jl:261-505): one workgroup per column
+template <class T>
+__global__ __launch_bounds__(NT) void k_relabel(const T *__restrict__ X, i64 n, T *__restrict__ C, i64 ldc,
+                                               const i64 *__restrict__ invp) {
+    const i64 j = blockIdx.x;
+    const T *src = X + invp[j] * n;
+    T *dst = C + j * ldc;
+    for (i64 i = threadIdx.x; i < n; i += NT) dst[i] = src[invp[i]];
+}
+
+// rmul!: Y[:, invp[c]] = B[:, c] (dir 0) or B[:, c] = Y[:, invp[c]] (dir 1); B nrhs x n (ldb), Y nrhs x n (nrhs)
+template <class T>
+__global__ __launch_bounds__(NT) void k_permute_cols(T *__restrict__ B, i64 ldb, T *__restrict__ Y, i64 n, i64 nrhs,
+                                                    const i64 *__restrict__ invp, int dir) {
+    for (i64 c = blockIdx.x; c < n; c += gridDim.x) {
+        T *b = B + c * ldb;
+        T *y = Y + invp[c] * nrhs;
+        for (i64 r = threadIdx.x; r < nrhs; r += NT) {
+            if (dir == 0) y[r] = b[r];
+            else b[r] = y[r];
+        }
+    }
+}
+
+// lmul!: Y[r, invp[c]] = B[c, r] (dir 0) or back (dir 1); B n x nrhs (ldb), Y nrhs x n (ld nrhs); 32 x 32 tiles
+template <class T>
+__global__ __launch_bounds__(NT) void k_transpose_perm(T *__restrict__ B, i64 ldb, T *__restrict__ Y, i64 n, i64 nrhs,
+                                                      const i64 *__restrict__ invp, int dir) {
+    __shared__ T tile[32][33];
+    const i64 c0 = (i64)blockIdx.x * 32, r0 = (i64)blockIdx.y * 32;
+    const int tx = threadIdx.x % 32, ty = threadIdx.x / 32;   // 8 rows of 32
+    if (dir == 0) {
+        for (int k = ty; k < 32; k += 8) {
+            const i64 c = c0 + tx, r = r0 + k;
+            if (c < n && r < nrhs) tile[k][tx] = B[c + r * ldb];
+        }
+        __syncthreads();
+        for (int k = ty; k < 32; k += 8) {
+            const i64 c = c0 + k, r = r0 + tx;
+            if (c < n && r < nrhs) Y[r + invp[c] * nrhs] = tile[tx][k];
+        }
+    } else {
+        for (int k = ty; k < 32; k += 8) {
+            const i64 c = c0 + k, r = r0 + tx;
+            if (c < n && r < nrhs) tile[tx][k] = Y[r + invp[c] * nrhs];
+        }
+        __syncthreads();
+        for (int k = ty; k < 32; k += 8) {
+            const i64 c = c0 + tx, r = r0 + k;
+            if (c < n && r < nrhs) B[c + r * ldb] = tile[k][tx];
+        }
+    }
+}
+
+// ===== batched getrf + star of dense fronts (nb <= 64), one workgroup per front =====
+
+template <class S>
+__global__ __launch_bounds__(NT) void k_getrf_star(typename S::value_type *__restrict__ Aall,
+                                                   typename S::value_type *__restrict__ TLall,
+                                                   typename S::value_type *__restrict__ TUall, int nb) {
+    typedef typename S::value_type T;
+    constexpr int LD = 65;
+    __shared__ T A[64 * LD];
+    __shared__ T X[64 * LD];
+    const i64 base = (i64)blockIdx.x * nb * nb;
+    T *G = Aall + base;
+    for (int e = threadIdx.x; e < nb * nb; e += NT) A[(e % nb) + (e / nb) * LD] = G[e];
+    __syncthreads();
+    lds_lu<S>(A, nb, LD, nb);
+    for (int e = threadIdx.x; e < nb * nb; e += NT) G[e] = A[(e % nb) + (e / nb) * LD];
+    // TU = U*: row r: X[r, j] = (X[r, j] (+) sum_{k<j} X[r, k] U[k, j]) (x) U[j, j]*, from X = I
+    if (TUall) {
+        const int r = threadIdx.x;
+        if (r < nb) {
+            T *x = X + r;   // row r at stride LD
+            for (int j = 0; j < nb; j++) x[j * LD] = j == r ? S::one() : S::zero();
+            for (int j = 0; j < nb; j++) {
+                T part = S::zero();
+                for (int k = 0; k < j; k++) part = S::muladd(x[k * LD], A[k + j * LD], part);
+                T acc = S::plus(x[j * LD], part);
+                if (!S::integral) acc = S::prod(acc, S::star(A[j + j * LD]));
+                x[j * LD] = acc;
+            }
+        }
+        __syncthreads();
+        T *TU = TUall + base;
+        for (int e = threadIdx.x; e < nb * nb; e += NT) TU[e] = X[(e % nb) + (e / nb) * LD];
+        __syncthreads();
+    }
+    // TL = L*: column c: X[i, c] = X[i, c] (+) sum_{k<i} L[i, k] X[k, c], from X = I
+    if (TLall) {
+        const int c = threadIdx.x;
+        if (c < nb) {
+            T *x = X + c * LD;   // column c
+            for (int i = 0; i < nb; i++) x[i] = i == c ? S::one() : S::zero();
+            for (int i = 0; i < nb; i++) {
+                T part = S::zero();
+                for (int k = 0; k < i; k++) part = S::muladd(A[i + k * LD], x[k], part);
+                x[i] = S::plus(x[i], part);
+            }
+        }
+        __syncthreads();
+        T *TL = TLall + base;
+        for (int e = threadIdx.x; e < nb * nb; e += NT) TL[e] = X[(e % nb) + (e / nb) * LD];
+    }
+}
+
+// ===== drivers =====
+
+struct Timer {
+    pp_ctx *ctx;
+    int slot;
+    Timer(pp_ctx *c, int s) : ctx(c), slot(s) {
+        if (ctx->timing) hipEventRecord(ctx->ev[0], ctx->stream);
+    }
+    void stop() {
+        if (!ctx->timing) return;
+        hipEventRecord(ctx->ev[1], ctx->stream);
+        hipEventSynchronize(ctx->ev[1]);
+        float ms = 0;
+        hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[1]);
+        ctx->t[slot] = ms * 1e-3;
+    }
+};
+
+template <class S> struct FactorRun {
+    pp_ctx *ctx;
+    pp_fac *fac;
+    const void *nz;
+    std::string err;
+    void operator()() { err = run(); }
+    std::string run() {
+        typedef typename S::value_type T;
+        const FactorPlan &P = *fac->sym->fplan;
+        const SweepPlan &W = *fac->sym->splan;
+        const DevPlan &d = fac->plan;
+        hipStream_t st = ctx->stream;
+        Timer tm(ctx, 0);
+        T *F = nullptr;
+        HIPCHK(hipMallocAsync((void **)&F, std::max<i64>(1, P.arena) * sizeof(T), st));
+        k_fill<T><<<grid1(P.arena), NT, 0, st>>>(F, P.arena, S::zero());
+        LAUNCHCHK();
+        if (fac->sym->S.nnz > 0)
+            k_scatter_entries<T><<<grid1(fac->sym->S.nnz), NT, 0, st>>>(F, d.entry_pos, (const T *)nz, fac->sym->S.nnz);
+        LAUNCHCHK();
+        for (const auto &L : P.levels) {
+            if (L.asm_cnt)
+                k_assemble<S><<<(unsigned)L.asm_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.na, d.nj, d.Sptr, d.relpos, d.chptr,
+                                                                 d.chidx, d.flist + L.asm_off);
+            if (L.small_cnt)
+                k_front_small<S><<<(unsigned)L.small_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.flist + L.small_off);
+            for (const auto &s : L.steps) {
+                if (s.panel_cnt)
+                    k_front_panel<S><<<(unsigned)s.panel_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.ftask + 3 * s.panel_off);
+                if (s.schur_cnt)
+                    k_front_schur<S><<<(unsigned)s.schur_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.stask + 4 * s.schur_off);
+            }
+            LAUNCHCHK();
+        }
+        const i64 nf = P.nf;
+        if (nf > 0)
+            k_extract_ref<T><<<(unsigned)nf, NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.Dptr, d.Lptr, (T *)fac->LD,
+                                                          (T *)fac->LL, (T *)fac->UL);
+        if (W.np > 0)
+            k_build_packs<T><<<(unsigned)W.np, NT, 0, st>>>(F, d.Foff, d.nj, d.Rptr, d.p_front, d.p_c0, d.p_w, d.p_e,
+                                                            d.p_lo, d.p_poff, d.p_doff, (T *)fac->Dpack,
+                                                            (T *)fac->Upack, (T *)fac->Lpack);
+        LAUNCHCHK();
+        HIPCHK(hipFreeAsync(F, st));
+        tm.stop();
+        return "";
+    }
+};
+
+template <class S, int W>
+static void launch_sweep(bool fwd, int dmode, typename S::value_type *X, i64 ld, const SweepArgs &a, unsigned grid,
+                         const void *Dpack, const void *pack, hipStream_t st) {
+    typedef typename S::value_type T;
+    if (fwd) {
+        if (dmode == 0) k_sweep_fwd<S, W, 0><<<grid, NT, 0, st>>>(X, ld, a, (const T *)Dpack, (const T *)pack);
+        else k_sweep_fwd<S, W, 1><<<grid, NT, 0, st>>>(X, ld, a, (const T *)Dpack, (const T *)pack);
+    } else {
+        if (dmode == 0) k_sweep_bwd<S, W, 0><<<grid, NT, 0, st>>>(X, ld, a, (const T *)Dpack, (const T *)pack);
+        else k_sweep_bwd<S, W, 1><<<grid, NT, 0, st>>>(X, ld, a, (const T *)Dpack, (const T *)pack);
+    }
+}
+
+// Run the forward or backward lists of the sweep plan over X.  star_rows: use each panel's own row range of the
+// star (tiles from the plan); otherwise rows [0, nrows) for every panel.
+template <class S>
+static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmode, typename S::value_type *X, i64 ld,
+                              bool star_rows, i64 nrows, const void *pack) {
+    const SweepPlan &W = *fac->sym->splan;
+    const DevPlan &d = fac->plan;
+    hipStream_t st = ctx->stream;
+    const auto &lists = fwd ? W.fwd : W.bwd;
+    const i64 ntile = (nrows + NT - 1) / NT;
+    for (const auto &li : lists) {
+        SweepArgs a;
+        a.plist = d.plist + li.off;
+        a.np = (int32_t)li.cnt;
+        a.nrows = (int32_t)nrows;
+        a.p_c0 = d.p_c0;
+        a.p_w = d.p_w;
+        a.p_e = d.p_e;
+        a.p_eoff = d.p_eoff;
+        a.p_poff = d.p_poff;
+        a.p_doff = d.p_doff;
+        a.Eidx = d.Eidx;
+        unsigned grid;
+        if (star_rows) {
+            const i64 toff = fwd ? li.tA_off : li.tB_off;
+            a.tiles = d.tiles + toff;
+            a.row_lo = fwd ? d.p_rowA_lo : d.p_rowB_lo;
+            a.row_hi = fwd ? d.p_rowA_hi : d.p_rowB_hi;
+            const i64 total = W.tiles[toff + li.cnt];
+            if (total == 0) continue;
+            grid = (unsigned)total;
+        } else {
+            a.tiles = nullptr;
+            a.row_lo = a.row_hi = nullptr;
+            if (ntile == 0) continue;
+            grid = (unsigned)(li.cnt * ntile);
+        }
+        switch (li.cls) {
+        case 0: launch_sweep<S, 1>(fwd, dmode, X, ld, a, grid, fac->Dpack, pack, st); break;
+        case 1: launch_sweep<S, 2>(fwd, dmode, X, ld, a, grid, fac->Dpack, pack, st); break;
+        case 2: launch_sweep<S, 4>(fwd, dmode, X, ld, a, grid, fac->Dpack, pack, st); break;
+        case 3: launch_sweep<S, 8>(fwd, dmode, X, ld, a, grid, fac->Dpack, pack, st); break;
+        case 4: launch_sweep<S, 16>(fwd, dmode, X, ld, a, grid, fac->Dpack, pack, st); break;
+        default: launch_sweep<S, 32>(fwd, dmode, X, ld, a, grid, fac->Dpack, pack, st); break;
+        }
+        LAUNCHCHK();
+    }
+    return "";
+}
+
+template <class S> struct StarRun {
+    pp_ctx *ctx;
+    const pp_fac *fac;
+    void *out;
+    i64 ldc;
+    std::string err;
+    void operator()() { err = run(); }
+    std::string run() {
+        typedef typename S::value_type T;
+        const i64 n = fac->sym->S.n;
+        hipStream_t st = ctx->stream;
+        T *X = nullptr;
+        HIPCHK(hipMallocAsync((void **)&X, std::max<i64>(1, n * n) * sizeof(T), st));
+        Timer t1(ctx, 1);
+        if (n > 0) k_identity<S><<<(unsigned)std::min<i64>(n, 65536), NT, 0, st>>>(X, n);
+        LAUNCHCHK();
+        std::string e = run_sweeps<S>(ctx, fac, true, 0, X, n, true, n, fac->Upack);
+        if (!e.empty()) return e;
+        t1.stop();
+        Timer t2(ctx, 2);
+        e = run_sweeps<S>(ctx, fac, false, 0, X, n, true, n, fac->Lpack);
+        if (!e.empty()) return e;
+        t2.stop();
+        Timer t3(ctx, 3);
+        if (n > 0) k_relabel<T><<<(unsigned)n, NT, 0, st>>>(X, n, (T *)out, ldc, fac->plan.invp);
+        LAUNCHCHK();
+        t3.stop();
+        HIPCHK(hipFreeAsync(X, st));
+        return "";
+    }
+};
+
+template <class S> struct SolveRun {
+    pp_ctx *ctx;
+    const pp_fac *fac;
+    void *B;
+    i64 ldb, nrhs;
+    bool left;
+    std::string err;
+    void operator()() { err = run(); }
+    std::string run() {
+        typedef typename S::value_type T;
+        const i64 n = fac->sym->S.n;
+        hipStream_t st = ctx->stream;
+        if (n == 0 || nrhs == 0) return "";
+        T *Y = nullptr;
+        HIPCHK(hipMallocAsync((void **)&Y, n * nrhs * sizeof(T), st));
+        Timer tm(ctx, 4);
+        std::string e;
+        if (!left) {
+            // rmul!: B (nrhs x n) <- B A*: U forward, then L backward (chordal/sgetrs.jl:29-51)
+            k_permute_cols<T><<<(unsigned)std::min<i64>(n, 65536), NT, 0, st>>>((T *)B, ldb, Y, n, nrhs, fac->plan.invp, 0);
+            LAUNCHCHK();
+            e = run_sweeps<S>(ctx, fac, true, 0, Y, nrhs, false, nrhs, fac->Upack);
+            if (e.empty()) e = run_sweeps<S>(ctx, fac, false, 0, Y, nrhs, false, nrhs, fac->Lpack);
+            if (!e.empty()) return e;
+            k_permute_cols<T><<<(unsigned)std::min<i64>(n, 65536), NT, 0, st>>>((T *)B, ldb, Y, n, nrhs, fac->plan.invp, 1);
+        } else {
+            // lmul!: B (n x nrhs) <- A* B: L forward, then U backward, run on B^T
+            dim3 g((unsigned)((n + 31) / 32), (unsigned)((nrhs + 31) / 32));
+            k_transpose_perm<T><<<g, NT, 0, st>>>((T *)B, ldb, Y, n, nrhs, fac->plan.invp, 0);
+            LAUNCHCHK();
+            e = run_sweeps<S>(ctx, fac, true, 1, Y, nrhs, false, nrhs, fac->Lpack);
+            if (e.empty()) e = run_sweeps<S>(ctx, fac, false, 1, Y, nrhs, false, nrhs, fac->Upack);
+            if (!e.empty()) return e;
+            k_transpose_perm<T><<<g, NT, 0, st>>>((T *)B, ldb, Y, n, nrhs, fac->plan.invp, 1);
+        }
+        LAUNCHCHK();
+        tm.stop();
+        HIPCHK(hipFreeAsync(Y, st));
+        return "";
+    }
+};
+
+template <class S> struct GemmRun {
+    pp_ctx *ctx;
+    i64 m, n, k;
+    const void *A;
+    i64 lda;
+    const void *B;
+    i64 ldb;
+    void *C;
+    i64 ldc;
+    std::string err;
+    void operator()() { err = run(); }
+    std::string run() {
+        typedef typename S::value_type T;
+        if (m == 0 || n == 0) return "";
+        dim3 g((unsigned)((m + GT - 1) / GT), (unsigned)((n + GT - 1) / GT));
+        k_gemm<S><<<g, NT, 0, ctx->stream>>>((T *)C, ldc, (const T *)A, lda, (const T *)B, ldb, m, n, k);
+        LAUNCHCHK();
+        return "";
+    }
+};
+
+template <class S> struct GetrfStarRun {
+    pp_ctx *ctx;
+    i64 nb, batch;
+    void *A, *TL, *TU;
+    std::string err;
+    void operator()() { err = run(); }
+    std::string run() {
+        typedef typename S::value_type T;
+        if (batch == 0) return "";
+        k_getrf_star<S><<<(unsigned)batch, NT, 0, ctx->stream>>>((T *)A, (T *)TL, (T *)TU, (int)nb);
+        LAUNCHCHK();
+        return "";
+    }
+};
+
+template <class S> std::string factor_impl(pp_ctx *ctx, pp_fac *fac, const void *nz) {
+    FactorRun<S> r{ctx, fac, nz};
+    r();
+    return r.err;
+}
+template <class S> std::string star_impl(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc) {
+    StarRun<S> r{ctx, fac, out, ldc};
+    r();
+    return r.err;
+}
+template <class S> std::string solve_impl(pp_ctx *ctx, const pp_fac *fac, void *B, i64 ldb, i64 nrhs, bool left) {
+    SolveRun<S> r{ctx, fac, B, ldb, nrhs, left};
+    r();
+    return r.err;
+}
+template <class S>
+std::string gemm_impl(pp_ctx *ctx, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B, i64 ldb, void *C, i64 ldc) {
+    GemmRun<S> r{ctx, m, n, k, A, lda, B, ldb, C, ldc};
+    r();
+    return r.err;
+}
+template <class S> std::string getrf_impl(pp_ctx *ctx, i64 nb, i64 batch, void *A, void *TL, void *TU) {
+    GetrfStarRun<S> r{ctx, nb, batch, A, TL, TU};
+    r();
+    return r.err;
+}
+
+}  // namespace pp

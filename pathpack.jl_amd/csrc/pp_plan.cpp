@@ -1,0 +1,218 @@
+// pp_plan.cpp -- host construction of the device plans (see pp_internal.h).
+#include <algorithm>
+
+#include "pp_internal.h"
+
+namespace pp {
+
+std::string build_factor_plan(const Symbolic &S, FactorPlan &P) {
+    const i64 nf = S.nf;
+    P.nf = nf;
+    P.nn.resize(nf);
+    P.na.resize(nf);
+    P.nj.resize(nf);
+    P.Foff.resize(nf + 1);
+    P.Foff[0] = 0;
+    P.max_nj = 0;
+    for (i64 f = 0; f < nf; f++) {
+        i64 nn = S.Rptr[f + 1] - S.Rptr[f], na = S.Sptr[f + 1] - S.Sptr[f];
+        if (nn + na > (i64)0x7fffffff / 2) return "front too large";
+        P.nn[f] = (int32_t)nn;
+        P.na[f] = (int32_t)na;
+        P.nj[f] = (int32_t)(nn + na);
+        P.Foff[f + 1] = P.Foff[f] + (nn + na) * (nn + na);
+        P.max_nj = std::max(P.max_nj, nn + na);
+    }
+    P.arena = P.Foff[nf];
+    P.Sptr32 = S.Sptr;
+    // positions of each separator in its parent's bag
+    P.relpos.assign(S.Stgt.size(), 0);
+    for (i64 f = 0; f < nf; f++) {
+        i64 p = S.parent[f];
+        if (p < 0) continue;
+        const i64 *b = S.Stgt.data() + S.Sptr[p], *e = S.Stgt.data() + S.Sptr[p + 1];
+        for (i64 q = S.Sptr[f]; q < S.Sptr[f + 1]; q++) {
+            i64 v = S.Stgt[q];
+            if (v >= S.Rptr[p] && v < S.Rptr[p + 1]) {
+                P.relpos[q] = (int32_t)(v - S.Rptr[p]);
+            } else {
+                const i64 *r = std::lower_bound(b, e, v);
+                if (r == e || *r != v) return "separator not contained in the parent's bag";
+                P.relpos[q] = (int32_t)((S.Rptr[p + 1] - S.Rptr[p]) + (r - b));
+            }
+        }
+    }
+    // children
+    P.chptr.assign(nf + 1, 0);
+    for (i64 f = 0; f < nf; f++)
+        if (S.parent[f] >= 0) P.chptr[S.parent[f] + 1]++;
+    for (i64 f = 0; f < nf; f++) P.chptr[f + 1] += P.chptr[f];
+    P.chidx.assign(P.chptr[nf], 0);
+    {
+        std::vector<int32_t> pos(P.chptr.begin(), P.chptr.end() - 1);
+        for (i64 f = 0; f < nf; f++)
+            if (S.parent[f] >= 0) P.chidx[pos[S.parent[f]]++] = (int32_t)f;
+    }
+    // entries of A
+    P.entry_pos.resize(S.nnz);
+    for (i64 p = 0; p < S.nnz; p++) {
+        i64 f = S.entry_front[p];
+        P.entry_pos[p] = P.Foff[f] + S.entry_row[p] + (i64)S.entry_col[p] * P.nj[f];
+    }
+    // heights
+    std::vector<i64> h(nf, 0);
+    i64 H = 0;
+    for (i64 f = 0; f < nf; f++) {
+        if (S.parent[f] >= 0) h[S.parent[f]] = std::max(h[S.parent[f]], h[f] + 1);
+        H = std::max(H, h[f] + 1);
+    }
+    std::vector<std::vector<int32_t>> byh(H);
+    for (i64 f = 0; f < nf; f++) byh[h[f]].push_back((int32_t)f);
+    P.levels.clear();
+    P.flist.clear();
+    P.ftask.clear();
+    P.stask.clear();
+    for (i64 l = 0; l < H; l++) {
+        FactorPlan::Level L;
+        L.asm_off = (i64)P.flist.size();
+        for (int32_t f : byh[l])
+            if (P.chptr[f + 1] > P.chptr[f]) P.flist.push_back(f);
+        L.asm_cnt = (i64)P.flist.size() - L.asm_off;
+        L.small_off = (i64)P.flist.size();
+        for (int32_t f : byh[l])
+            if (P.nj[f] <= SMALL_NJ) P.flist.push_back(f);
+        L.small_cnt = (i64)P.flist.size() - L.small_off;
+        i64 maxsteps = 0;
+        for (int32_t f : byh[l])
+            if (P.nj[f] > SMALL_NJ) maxsteps = std::max<i64>(maxsteps, (P.nn[f] + NB - 1) / NB);
+        for (i64 s = 0; s < maxsteps; s++) {
+            FactorPlan::Step st;
+            st.panel_off = (i64)P.ftask.size() / 3;
+            st.schur_off = (i64)P.stask.size() / 4;
+            for (int32_t f : byh[l]) {
+                if (P.nj[f] <= SMALL_NJ || s * NB >= P.nn[f]) continue;
+                i64 off = s * NB, b = std::min<i64>(NB, P.nn[f] - off), m = P.nj[f] - off - b;
+                i64 chunks = std::max<i64>(1, (m + 255) / 256);
+                for (i64 c = 0; c < chunks; c++) {
+                    P.ftask.push_back(f);
+                    P.ftask.push_back((int32_t)off);
+                    P.ftask.push_back((int32_t)c);
+                }
+                i64 T = (m + 63) / 64;
+                for (i64 ti = 0; ti < T; ti++)
+                    for (i64 tj = 0; tj < T; tj++) {
+                        P.stask.push_back(f);
+                        P.stask.push_back((int32_t)off);
+                        P.stask.push_back((int32_t)ti);
+                        P.stask.push_back((int32_t)tj);
+                    }
+            }
+            st.panel_cnt = (i64)P.ftask.size() / 3 - st.panel_off;
+            st.schur_cnt = (i64)P.stask.size() / 4 - st.schur_off;
+            L.steps.push_back(st);
+        }
+        P.levels.push_back(std::move(L));
+    }
+    return "";
+}
+
+std::string build_sweep_plan(const Symbolic &S, const FactorPlan &F, SweepPlan &P) {
+    const i64 nf = S.nf;
+    // panels
+    std::vector<i64> first(nf), last(nf);
+    P.np = 0;
+    P.front.clear();
+    P.c0.clear();
+    P.w.clear();
+    P.e.clear();
+    P.lo_ext.clear();
+    P.eoff.clear();
+    P.poff.clear();
+    P.doff.clear();
+    P.Eidx.clear();
+    P.npack = 0;
+    P.ndpack = 0;
+    P.max_e = 0;
+    std::vector<i64> root(nf);
+    for (i64 f = nf - 1; f >= 0; f--) root[f] = S.parent[f] >= 0 ? root[S.parent[f]] : f;
+    for (i64 f = 0; f < nf; f++) {
+        const i64 Rp = S.Rptr[f], nn = F.nn[f], nj = F.nj[f];
+        first[f] = P.np;
+        for (i64 k = 0; k * PANEL_W < nn; k++) {
+            const i64 c0 = Rp + k * PANEL_W, w = std::min<i64>(PANEL_W, nn - k * PANEL_W);
+            const i64 lo = k * PANEL_W + w, e = nj - lo;
+            P.front.push_back((int32_t)f);
+            P.c0.push_back((int32_t)c0);
+            P.w.push_back((int32_t)w);
+            P.e.push_back((int32_t)e);
+            P.lo_ext.push_back((int32_t)lo);
+            P.eoff.push_back((i64)P.Eidx.size());
+            for (i64 v = c0 + w; v < Rp + nn; v++) P.Eidx.push_back((int32_t)v);
+            for (i64 q = S.Sptr[f]; q < S.Sptr[f + 1]; q++) P.Eidx.push_back((int32_t)S.Stgt[q]);
+            P.poff.push_back(P.npack);
+            P.npack += w * e;
+            P.doff.push_back(P.ndpack);
+            P.ndpack += w * w;
+            P.rowA_lo.push_back((int32_t)S.Rptr[S.fdsc[f]]);
+            P.rowA_hi.push_back((int32_t)(c0 + w));
+            P.rowB_lo.push_back((int32_t)S.Rptr[S.fdsc[root[f]]]);
+            P.rowB_hi.push_back((int32_t)S.Rptr[root[f] + 1]);
+            P.max_e = std::max(P.max_e, e);
+            P.np++;
+        }
+        last[f] = P.np - 1;
+    }
+    // forward levels (leaves to root) and backward levels (root to leaves)
+    std::vector<i64> lvA(P.np, 0), lvB(P.np, 0);
+    std::vector<i64> endA(nf, -1);
+    for (i64 f = 0; f < nf; f++) {
+        i64 base = 0;
+        for (i64 q = F.chptr[f]; q < F.chptr[f + 1]; q++) base = std::max(base, endA[F.chidx[q]] + 1);
+        for (i64 p = first[f]; p <= last[f]; p++) lvA[p] = base + (p - first[f]);
+        endA[f] = lvA[last[f]];
+    }
+    std::vector<i64> endB(nf, -1);   // level of the front's first panel (the last one visited)
+    for (i64 f = nf - 1; f >= 0; f--) {
+        i64 base = S.parent[f] >= 0 ? endB[S.parent[f]] + 1 : 0;
+        for (i64 p = last[f]; p >= first[f]; p--) lvB[p] = base + (last[f] - p);
+        endB[f] = lvB[first[f]];
+    }
+    auto make_lists = [&](const std::vector<i64> &lv, std::vector<SweepPlan::List> &out) {
+        i64 L = 0;
+        for (i64 p = 0; p < P.np; p++) L = std::max(L, lv[p] + 1);
+        std::vector<std::vector<int32_t>> buckets(L * NCLASS);
+        for (i64 p = 0; p < P.np; p++) buckets[lv[p] * NCLASS + width_class(P.w[p])].push_back((int32_t)p);
+        for (i64 b = 0; b < (i64)buckets.size(); b++) {
+            if (buckets[b].empty()) continue;
+            SweepPlan::List li;
+            li.cls = (int)(b % NCLASS);
+            li.off = (i64)P.plist.size();
+            li.cnt = (i64)buckets[b].size();
+            P.plist.insert(P.plist.end(), buckets[b].begin(), buckets[b].end());
+            li.tA_off = (i64)P.tiles.size();
+            int32_t acc = 0;
+            P.tiles.push_back(0);
+            for (int32_t p : buckets[b]) {
+                acc += (P.rowA_hi[p] - P.rowA_lo[p] + SWEEP_ROWS - 1) / SWEEP_ROWS;
+                P.tiles.push_back(acc);
+            }
+            li.tB_off = (i64)P.tiles.size();
+            acc = 0;
+            P.tiles.push_back(0);
+            for (int32_t p : buckets[b]) {
+                acc += (P.rowB_hi[p] - P.rowB_lo[p] + SWEEP_ROWS - 1) / SWEEP_ROWS;
+                P.tiles.push_back(acc);
+            }
+            out.push_back(li);
+        }
+    };
+    P.plist.clear();
+    P.tiles.clear();
+    P.fwd.clear();
+    P.bwd.clear();
+    make_lists(lvA, P.fwd);
+    make_lists(lvB, P.bwd);
+    return "";
+}
+
+}  // namespace pp

@@ -1,0 +1,654 @@
+// pp_symbolic.cpp -- host symbolic analysis: ordering, elimination tree, supernodes, separators.
+//
+// Replaces the CliqueTrees.jl calls of the reference (src/CPU/chordal_ssymbolic.jl:26-184: cliquetree,
+// symmetric, ChordalSymbolic).  See pp_symbolic.h for what is computed and how it differs.
+#include "pp_symbolic.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+#include <numeric>
+
+namespace pp {
+
+namespace {
+
+struct Adj {
+    i64 n = 0;
+    std::vector<i64> xadj;
+    std::vector<i32> adj;
+};
+
+// Symmetric pattern of A without the diagonal, neighbours sorted.
+std::string symmetrize(i64 n, const i64 *colptr, const i64 *rowval, Adj &G) {
+    if (n < 0 || n > (i64)0x7fffffff) return "n out of range";
+    if (colptr[0] != 0) return "colptr[0] must be 0";
+    for (i64 j = 0; j < n; j++) {
+        if (colptr[j + 1] < colptr[j]) return "colptr must be nondecreasing";
+        for (i64 p = colptr[j]; p < colptr[j + 1]; p++) {
+            if (rowval[p] < 0 || rowval[p] >= n) return "row index out of range";
+            if (p > colptr[j] && rowval[p] <= rowval[p - 1]) return "row indices must be sorted and unique in each column";
+        }
+    }
+    std::vector<i64> deg(n + 1, 0);
+    for (i64 j = 0; j < n; j++)
+        for (i64 p = colptr[j]; p < colptr[j + 1]; p++) {
+            i64 i = rowval[p];
+            if (i == j) continue;
+            deg[i]++;
+            deg[j]++;
+        }
+    G.n = n;
+    G.xadj.assign(n + 1, 0);
+    for (i64 v = 0; v < n; v++) G.xadj[v + 1] = G.xadj[v] + deg[v];
+    G.adj.assign(G.xadj[n], 0);
+    std::vector<i64> pos(G.xadj.begin(), G.xadj.end() - 1);
+    for (i64 j = 0; j < n; j++)
+        for (i64 p = colptr[j]; p < colptr[j + 1]; p++) {
+            i64 i = rowval[p];
+            if (i == j) continue;
+            G.adj[pos[i]++] = (i32)j;
+            G.adj[pos[j]++] = (i32)i;
+        }
+    // sort and deduplicate each list
+    std::vector<i64> nx(n + 1, 0);
+    i64 w = 0;
+    for (i64 v = 0; v < n; v++) {
+        i32 *b = G.adj.data() + G.xadj[v], *e = G.adj.data() + G.xadj[v + 1];
+        std::sort(b, e);
+        i64 start = w;
+        for (i32 *q = b; q < e; q++)
+            if (q == b || *q != q[-1]) G.adj[w++] = *q;
+        nx[v] = start;
+    }
+    nx[n] = w;
+    G.xadj = nx;
+    G.adj.resize(w);
+    return "";
+}
+
+// ===== nested dissection on level structures =====
+//
+// A work item is a vertex subset (all vertices v with part[v] == id) that owns the output positions
+// [hi - size, hi).  A connected item is split by one level of a breadth-first level structure rooted at a
+// pseudo-peripheral vertex (George & Liu, "Computer Solution of Large Sparse Positive Definite Systems", 1981):
+// the level with the fewest vertices among those leaving at least 30% of the item on each side.  The separator
+// takes the last positions; the two sides recurse.  Small items are ordered by minimum degree.
+
+struct ND {
+    const Adj &G;
+    int leaf;
+    std::vector<i32> part;
+    std::vector<i32> level, queue;
+    std::vector<i64> order;   // order[k] = vertex eliminated k-th
+    i32 next_id = 1;
+
+    ND(const Adj &g, int leaf_) : G(g), leaf(std::max(2, std::min(leaf_, 64))), part(g.n, 0), level(g.n, -1),
+                                   queue(g.n), order(g.n, -1) {}
+
+    // BFS inside item id from root; returns the number of levels; fills queue[0..cnt) and level[]
+    int bfs(i32 id, i32 root, i64 &cnt, std::vector<i64> &lptr) {
+        lptr.clear();
+        cnt = 0;
+        queue[cnt++] = root;
+        level[root] = 0;
+        i64 head = 0;
+        int nlev;
+        lptr.push_back(0);
+        while (head < cnt) {
+            i32 v = queue[head++];
+            for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) {
+                i32 u = G.adj[p];
+                if (part[u] != id || level[u] >= 0) continue;
+                level[u] = level[v] + 1;
+                queue[cnt++] = u;
+            }
+        }
+        // level pointers (BFS visits levels in order)
+        for (i64 k = 1; k < cnt; k++)
+            if (level[queue[k]] != level[queue[k - 1]]) lptr.push_back(k);
+        lptr.push_back(cnt);
+        nlev = (int)lptr.size() - 1;
+        return nlev;
+    }
+
+    void clear_levels(i64 cnt) {
+        for (i64 k = 0; k < cnt; k++) level[queue[k]] = -1;
+    }
+
+    i64 degree_in(i32 v, i32 id) const {
+        i64 d = 0;
+        for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) d += part[G.adj[p]] == id;
+        return d;
+    }
+
+    // minimum degree on a small item (at most 64 vertices): explicit elimination graph in bit masks
+    void md_leaf(const std::vector<i32> &V, i64 lo) {
+        const int m = (int)V.size();
+        std::vector<uint64_t> mask(m, 0);
+        // local index lookup through level[] (free at this point)
+        for (int a = 0; a < m; a++) level[V[a]] = a;
+        i32 id = part[V[0]];
+        for (int a = 0; a < m; a++)
+            for (i64 p = G.xadj[V[a]]; p < G.xadj[V[a] + 1]; p++) {
+                i32 u = G.adj[p];
+                if (part[u] == id) mask[a] |= uint64_t(1) << level[u];
+            }
+        for (int a = 0; a < m; a++) level[V[a]] = -1;
+        uint64_t alive = m == 64 ? ~uint64_t(0) : ((uint64_t(1) << m) - 1);
+        for (int k = 0; k < m; k++) {
+            int best = -1, bd = 1 << 30;
+            for (int a = 0; a < m; a++)
+                if (alive >> a & 1) {
+                    int d = __builtin_popcountll(mask[a] & alive);
+                    if (d < bd) { bd = d; best = a; }
+                }
+            uint64_t nb = mask[best] & alive & ~(uint64_t(1) << best);
+            for (int a = 0; a < m; a++)
+                if (nb >> a & 1) mask[a] |= nb & ~(uint64_t(1) << a);
+            alive &= ~(uint64_t(1) << best);
+            order[lo + k] = V[best];
+        }
+    }
+
+    void run() {
+        struct Item { std::vector<i32> V; i64 hi; };
+        std::vector<Item> stack;
+        {
+            Item all;
+            all.V.resize(G.n);
+            std::iota(all.V.begin(), all.V.end(), 0);
+            all.hi = G.n;
+            stack.push_back(std::move(all));
+        }
+        std::vector<i64> lptr;
+        while (!stack.empty()) {
+            Item it = std::move(stack.back());
+            stack.pop_back();
+            const i64 sz = (i64)it.V.size();
+            if (sz == 0) continue;
+            const i32 id = next_id++;
+            for (i32 v : it.V) part[v] = id;
+            const i64 lo = it.hi - sz;
+            if (sz <= leaf) {
+                md_leaf(it.V, lo);
+                continue;
+            }
+            // connected components of the item
+            i64 cnt;
+            i32 root = it.V[0];
+            {
+                i64 bd = 1LL << 60;
+                for (i32 v : it.V) {
+                    i64 d = degree_in(v, id);
+                    if (d < bd) { bd = d; root = v; }
+                }
+            }
+            int nlev = bfs(id, root, cnt, lptr);
+            if (cnt < sz) {
+                // disconnected: every component becomes an item of its own
+                clear_levels(cnt);
+                std::vector<std::vector<i32>> comps;
+                std::vector<i64> lp2;
+                for (i32 v : it.V) {
+                    if (part[v] != id) continue;
+                    i64 c2;
+                    bfs(id, v, c2, lp2);
+                    comps.emplace_back(queue.begin(), queue.begin() + c2);
+                    clear_levels(c2);
+                    for (i32 u : comps.back()) part[u] = -id;
+                }
+                i64 hi = it.hi;
+                for (auto &c : comps) {
+                    for (i32 u : c) part[u] = id;
+                    i64 csz = (i64)c.size();
+                    stack.push_back({std::move(c), hi});
+                    hi -= csz;
+                }
+                continue;
+            }
+            // pseudo-peripheral root
+            for (int iter = 0; iter < 8; iter++) {
+                i32 best = -1;
+                i64 bd = 1LL << 60;
+                for (i64 k = lptr[nlev - 1]; k < lptr[nlev]; k++) {
+                    i32 v = queue[k];
+                    i64 d = degree_in(v, id);
+                    if (d < bd) { bd = d; best = v; }
+                }
+                clear_levels(cnt);
+                std::vector<i64> lptr2;
+                i64 cnt2;
+                int nlev2 = bfs(id, best, cnt2, lptr2);
+                if (nlev2 > nlev) {
+                    nlev = nlev2;
+                    lptr = lptr2;
+                    root = best;
+                } else {
+                    clear_levels(cnt2);
+                    nlev = bfs(id, root, cnt, lptr);
+                    break;
+                }
+            }
+            if (nlev < 3) {
+                // too shallow to dissect: minimum degree would be too slow on a large item; natural order
+                for (i64 k = 0; k < cnt; k++) order[lo + k] = queue[k];
+                clear_levels(cnt);
+                continue;
+            }
+            // the separator level
+            int sl = -1;
+            i64 ssz = 1LL << 60, sbal = 1LL << 60;
+            const i64 minside = (i64)(0.3 * (double)sz);
+            for (int k = 1; k + 1 < nlev; k++) {
+                i64 a = lptr[k], s = lptr[k + 1] - lptr[k], b = sz - a - s;
+                if (a < minside || b < minside) continue;
+                i64 bal = a > b ? a - b : b - a;
+                if (s < ssz || (s == ssz && bal < sbal)) { ssz = s; sbal = bal; sl = k; }
+            }
+            if (sl < 0) {
+                for (int k = 1; k + 1 < nlev; k++)
+                    if (lptr[k + 1] * 2 >= sz) { sl = k; break; }
+                if (sl < 0) sl = nlev / 2;
+            }
+            // sides: A = levels < sl, B = levels > sl, S = level sl; then drop separator vertices that touch only
+            // one side (a minimal separator)
+            const i32 idA = next_id++, idB = next_id++, idS = next_id++;
+            for (i64 k = 0; k < cnt; k++) {
+                i32 v = queue[k];
+                part[v] = level[v] < sl ? idA : (level[v] > sl ? idB : idS);
+            }
+            clear_levels(cnt);
+            std::vector<i32> S;
+            for (i64 k = lptr[sl]; k < lptr[sl + 1]; k++) S.push_back(queue[k]);
+            std::vector<i32> keep;
+            for (i32 v : S) {
+                bool ta = false, tb = false;
+                for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) {
+                    i32 u = G.adj[p];
+                    ta |= part[u] == idA;
+                    tb |= part[u] == idB;
+                }
+                if (!tb) part[v] = idA;
+                else if (!ta) part[v] = idB;
+                else keep.push_back(v);
+            }
+            std::vector<i32> A, B;
+            for (i32 v : it.V) {
+                if (part[v] == idA) A.push_back(v);
+                else if (part[v] == idB) B.push_back(v);
+            }
+            const i64 ns = (i64)keep.size();
+            for (i64 k = 0; k < ns; k++) order[it.hi - ns + k] = keep[k];
+            const i64 na = (i64)A.size();
+            stack.push_back({std::move(B), it.hi - ns});
+            stack.push_back({std::move(A), lo + na});
+        }
+    }
+};
+
+// ===== elimination tree and postorder (Liu 1986, path compression) =====
+
+void etree_postorder(const Adj &G, const std::vector<i64> &perm, std::vector<i64> &post_perm) {
+    const i64 n = G.n;
+    std::vector<i64> invp(n);
+    for (i64 k = 0; k < n; k++) invp[perm[k]] = k;
+    std::vector<i64> parent(n, -1), anc(n, -1);
+    for (i64 j = 0; j < n; j++) {
+        i64 v = perm[j];
+        for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) {
+            i64 i = invp[G.adj[p]];
+            if (i >= j) continue;
+            i64 r = i;
+            while (anc[r] != -1 && anc[r] != j) {
+                i64 t = anc[r];
+                anc[r] = j;
+                r = t;
+            }
+            if (anc[r] == -1) {
+                anc[r] = j;
+                parent[r] = j;
+            }
+        }
+    }
+    // children lists in increasing order, then an iterative DFS from the roots
+    std::vector<i64> head(n, -1), next(n, -1);
+    for (i64 j = n - 1; j >= 0; j--)
+        if (parent[j] >= 0) {
+            next[j] = head[parent[j]];
+            head[parent[j]] = j;
+        }
+    post_perm.clear();
+    post_perm.reserve(n);
+    std::vector<i64> stack;
+    for (i64 r = 0; r < n; r++) {
+        if (parent[r] != -1) continue;
+        stack.push_back(r);
+        while (!stack.empty()) {
+            i64 v = stack.back();
+            if (head[v] >= 0) {
+                i64 c = head[v];
+                head[v] = next[c];
+                stack.push_back(c);
+            } else {
+                stack.pop_back();
+                post_perm.push_back(perm[v]);
+            }
+        }
+    }
+}
+
+// ===== supernodal symbolic factorization for (perm, Rptr) =====
+//
+// sep(f) = (adj(res(f)) and the separators of f's children) restricted to vertices after res(f); parent(f) is the
+// front holding min sep(f).  Fronts must be in a postorder of the resulting tree.
+std::string supernodal(const Adj &G, const std::vector<i64> &perm, const std::vector<i64> &Rptr,
+                       std::vector<i64> &Sptr, std::vector<i32> &Stgt, std::vector<i64> &parent) {
+    const i64 n = G.n, nf = (i64)Rptr.size() - 1;
+    std::vector<i64> invp(n), idx(n);
+    for (i64 k = 0; k < n; k++) invp[perm[k]] = k;
+    for (i64 f = 0; f < nf; f++)
+        for (i64 v = Rptr[f]; v < Rptr[f + 1]; v++) idx[v] = f;
+    std::vector<i64> mark(n, -1), chead(nf, -1), cnext(nf, -1), ctail(nf, -1);
+    Sptr.assign(nf + 1, 0);
+    Stgt.clear();
+    parent.assign(nf, -1);
+    std::vector<i32> buf;
+    for (i64 f = 0; f < nf; f++) {
+        const i64 r0 = Rptr[f], r1 = Rptr[f + 1];
+        buf.clear();
+        for (i64 v = r0; v < r1; v++) {
+            i64 ov = perm[v];
+            for (i64 p = G.xadj[ov]; p < G.xadj[ov + 1]; p++) {
+                i64 u = invp[G.adj[p]];
+                if (u >= r1 && mark[u] != f) {
+                    mark[u] = f;
+                    buf.push_back((i32)u);
+                }
+            }
+        }
+        for (i64 c = chead[f]; c >= 0; c = cnext[c])
+            for (i64 q = Sptr[c]; q < Sptr[c + 1]; q++) {
+                i64 u = Stgt[q];
+                if (u < r0) return "front structure is not a postorder of its tree";
+                if (u >= r1 && mark[u] != f) {
+                    mark[u] = f;
+                    buf.push_back((i32)u);
+                }
+            }
+        std::sort(buf.begin(), buf.end());
+        Stgt.insert(Stgt.end(), buf.begin(), buf.end());
+        Sptr[f + 1] = (i64)Stgt.size();
+        if (!buf.empty()) {
+            i64 p = idx[buf[0]];
+            parent[f] = p;
+            if (ctail[p] < 0) chead[p] = f;
+            else cnext[ctail[p]] = f;
+            ctail[p] = f;
+        }
+    }
+    return "";
+}
+
+double now() {
+    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+// Work counts of a structure (the formulas of the reference's per-front costs): factor sum nn^3/3 + nn^2 na +
+// nn na^2; star n * sum nn (na + (nn-1)/2) for X <- X L* plus sum |subtree(f)| nn (na + (nn-1)/2) for X <- U*;
+// one right-hand side 2 sum nn (na + (nn-1)/2).
+void work_counts(i64 n, const std::vector<i64> &Rptr, const std::vector<i64> &Sptr, const std::vector<i64> &parent,
+                 double &factor, double &star, double &rhs, double &nnzL) {
+    const i64 nf = (i64)Rptr.size() - 1;
+    std::vector<i64> fdsc(nf);
+    for (i64 f = 0; f < nf; f++) fdsc[f] = f;
+    for (i64 f = 0; f < nf; f++)
+        if (parent[f] >= 0) fdsc[parent[f]] = std::min(fdsc[parent[f]], fdsc[f]);
+    factor = star = rhs = nnzL = 0;
+    for (i64 f = 0; f < nf; f++) {
+        double nn = (double)(Rptr[f + 1] - Rptr[f]), na = (double)(Sptr[f + 1] - Sptr[f]);
+        double per = nn * (na + (nn - 1) / 2);
+        double sub = (double)(Rptr[f + 1] - Rptr[fdsc[f]]);
+        factor += nn * nn * nn / 3 + nn * nn * na + nn * na * na;
+        star += (double)n * per + sub * per;
+        rhs += 2 * per;
+        nnzL += per;
+    }
+}
+
+std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, std::vector<i64> perm,
+                   std::vector<i64> Rptr, Symbolic &out) {
+    std::vector<i64> Sptr, parent;
+    std::vector<i32> Stgt;
+    std::string err = supernodal(G, perm, Rptr, Sptr, Stgt, parent);
+    if (!err.empty()) return err;
+    const i64 nf = (i64)Rptr.size() - 1;
+    out.n = n;
+    out.perm = std::move(perm);
+    out.invp.assign(n, 0);
+    for (i64 k = 0; k < n; k++) out.invp[out.perm[k]] = k;
+    out.nf = nf;
+    out.Rptr = std::move(Rptr);
+    out.Sptr = std::move(Sptr);
+    out.Stgt.assign(Stgt.begin(), Stgt.end());
+    out.parent = std::move(parent);
+    out.fdsc.resize(nf);
+    for (i64 f = 0; f < nf; f++) out.fdsc[f] = f;
+    for (i64 f = 0; f < nf; f++)
+        if (out.parent[f] >= 0) out.fdsc[out.parent[f]] = std::min(out.fdsc[out.parent[f]], out.fdsc[f]);
+    out.Dptr.assign(nf + 1, 0);
+    out.Lptr.assign(nf + 1, 0);
+    for (i64 f = 0; f < nf; f++) {
+        i64 nn = out.Rptr[f + 1] - out.Rptr[f], na = out.Sptr[f + 1] - out.Sptr[f];
+        out.Dptr[f + 1] = out.Dptr[f] + nn * nn;
+        out.Lptr[f + 1] = out.Lptr[f] + nn * na;
+    }
+    // where each stored entry lands: front of min(i, j), local positions in its bag
+    std::vector<i64> idx(n);
+    for (i64 f = 0; f < nf; f++)
+        for (i64 v = out.Rptr[f]; v < out.Rptr[f + 1]; v++) idx[v] = f;
+    out.nnz = colptr[n];
+    out.entry_front.resize(out.nnz);
+    out.entry_row.resize(out.nnz);
+    out.entry_col.resize(out.nnz);
+    auto local = [&](i64 f, i64 v) -> i64 {
+        const i64 r0 = out.Rptr[f], r1 = out.Rptr[f + 1];
+        if (v >= r0 && v < r1) return v - r0;
+        const i64 *b = out.Stgt.data() + out.Sptr[f], *e = out.Stgt.data() + out.Sptr[f + 1];
+        const i64 *q = std::lower_bound(b, e, v);
+        if (q == e || *q != v) return -1;
+        return (r1 - r0) + (q - b);
+    };
+    for (i64 c = 0; c < n; c++)
+        for (i64 p = colptr[c]; p < colptr[c + 1]; p++) {
+            i64 i = out.invp[rowval[p]], j = out.invp[c];
+            i64 f = idx[std::min(i, j)];
+            i64 li = local(f, i), lj = local(f, j);
+            if (li < 0 || lj < 0) return "an entry of A falls outside the structure";
+            out.entry_front[p] = f;
+            out.entry_row[p] = (i32)li;
+            out.entry_col[p] = (i32)lj;
+        }
+    work_counts(n, out.Rptr, out.Sptr, out.parent, out.madds_factor, out.madds_star, out.madds_rhs, out.nnzL);
+    return "";
+}
+
+}  // namespace
+
+std::string analyze_given(i64 n, const i64 *colptr, const i64 *rowval, const i64 *perm, i64 nf, const i64 *Rptr,
+                          Symbolic &out) {
+    double t0 = now();
+    Adj G;
+    std::string err = symmetrize(n, colptr, rowval, G);
+    if (!err.empty()) return err;
+    std::vector<i64> p(perm, perm + n), R(Rptr, Rptr + nf + 1);
+    std::vector<char> seen(n, 0);
+    for (i64 k = 0; k < n; k++) {
+        if (p[k] < 0 || p[k] >= n || seen[p[k]]) return "perm is not a permutation";
+        seen[p[k]] = 1;
+    }
+    if (R[0] != 0 || R[nf] != n) return "Rptr must run from 0 to n";
+    for (i64 f = 0; f < nf; f++)
+        if (R[f + 1] <= R[f]) return "fronts must be nonempty";
+    err = finish(G, n, colptr, rowval, p, R, out);
+    if (!err.empty()) return err;
+    out.madds_factor_alg = out.madds_factor;
+    out.madds_star_alg = out.madds_star;
+    out.madds_rhs_alg = out.madds_rhs;
+    out.nnzL_alg = out.nnzL;
+    out.seconds_total = now() - t0;
+    return "";
+}
+
+std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOptions &opts, const i64 *given_perm,
+                    Symbolic &out) {
+    double t0 = now();
+    Adj G;
+    std::string err = symmetrize(n, colptr, rowval, G);
+    if (!err.empty()) return err;
+    // 1. fill-reducing order
+    std::vector<i64> perm0(n);
+    if (opts.ordering == 0) {
+        ND nd(G, opts.nd_leaf);
+        nd.run();
+        perm0 = nd.order;
+    } else if (opts.ordering == 1) {
+        std::iota(perm0.begin(), perm0.end(), 0);
+    } else {
+        if (!given_perm) return "no permutation given";
+        std::vector<char> seen(n, 0);
+        for (i64 k = 0; k < n; k++) {
+            if (given_perm[k] < 0 || given_perm[k] >= n || seen[given_perm[k]]) return "perm is not a permutation";
+            seen[given_perm[k]] = 1;
+            perm0[k] = given_perm[k];
+        }
+    }
+    out.seconds_order = now() - t0;
+    // 2. postordered elimination tree
+    std::vector<i64> perm1;
+    etree_postorder(G, perm0, perm1);
+    // 3. column structures, then fundamental supernodes
+    std::vector<i64> Rcol(n + 1);
+    std::iota(Rcol.begin(), Rcol.end(), 0);
+    std::vector<i64> Scol, pcol;
+    std::vector<i32> Tcol;
+    err = supernodal(G, perm1, Rcol, Scol, Tcol, pcol);
+    if (!err.empty()) return err;
+    std::vector<i32> Tfree;
+    Tcol.swap(Tfree);   // column structures are no longer needed: only counts and the tree
+    std::vector<i64> nchild(n, 0);
+    for (i64 j = 0; j < n; j++)
+        if (pcol[j] >= 0) nchild[pcol[j]]++;
+    std::vector<i64> R1;
+    R1.push_back(0);
+    for (i64 j = 1; j < n; j++) {
+        i64 ccp = Scol[j] - Scol[j - 1], ccj = Scol[j + 1] - Scol[j];
+        bool cont = pcol[j - 1] == j && nchild[j] == 1 && ccj == ccp - 1;
+        if (!cont) R1.push_back(j);
+    }
+    R1.push_back(n);
+    std::vector<i64> S1, par1;
+    std::vector<i32> T1;
+    err = supernodal(G, perm1, R1, S1, T1, par1);
+    if (!err.empty()) return err;
+    const i64 ns = (i64)R1.size() - 1;
+    {
+        double f, s, r, l;
+        work_counts(n, R1, S1, par1, f, s, r, l);
+        out.madds_factor_alg = f;
+        out.madds_star_alg = s;
+        out.madds_rhs_alg = r;
+        out.nnzL_alg = l;
+    }
+    if (!opts.amalgamate) {
+        err = finish(G, n, colptr, rowval, perm1, R1, out);
+        out.seconds_total = now() - t0;
+        return err;
+    }
+    // 4. relaxed amalgamation: merge a child front into its parent when the merged front's share of explicit
+    //    zeros stays below a size-dependent bound (the rule of CHOLMOD's relaxed supernodes, Ashcraft & Grimes
+    //    1989); the merged front has the parent's separator.
+    std::vector<i64> mnn(ns), mna(ns), rep(ns);
+    std::vector<double> mtrue(ns);
+    for (i64 s = 0; s < ns; s++) {
+        i64 nn = R1[s + 1] - R1[s], na = S1[s + 1] - S1[s];
+        mnn[s] = nn;
+        mna[s] = na;
+        mtrue[s] = (double)nn * (nn - 1) / 2 + (double)nn * na;
+        rep[s] = s;
+    }
+    auto find = [&](i64 s) {
+        while (rep[s] != s) {
+            rep[s] = rep[rep[s]];
+            s = rep[s];
+        }
+        return s;
+    };
+    std::vector<std::vector<i64>> kids(ns);
+    for (i64 s = 0; s < ns; s++)
+        if (par1[s] >= 0) kids[par1[s]].push_back(s);
+    for (i64 p = 0; p < ns; p++) {
+        // children with few columns first: they gain the most
+        std::vector<i64> cs = kids[p];
+        std::stable_sort(cs.begin(), cs.end(), [&](i64 a, i64 b) { return mnn[find(a)] < mnn[find(b)]; });
+        for (i64 c : cs) {
+            i64 rc = find(c), rp = find(p);
+            i64 nn = mnn[rp] + mnn[rc], na = mna[rp];
+            if (nn > opts.max_front_cols) continue;
+            double dense = (double)nn * (nn - 1) / 2 + (double)nn * na;
+            double z = dense > 0 ? 1.0 - (mtrue[rp] + mtrue[rc]) / dense : 0.0;
+            bool merge;
+            if (nn <= opts.relax_small) merge = true;
+            else if (nn <= opts.relax_cols[0]) merge = z < opts.relax_z[0];
+            else if (nn <= opts.relax_cols[1]) merge = z < opts.relax_z[1];
+            else merge = z < opts.relax_z[2];
+            if (!merge) continue;
+            rep[rc] = rp;
+            mnn[rp] = nn;
+            mtrue[rp] += mtrue[rc];
+        }
+    }
+    // 5. renumber: postorder of the merged tree; a merged front lists its members' columns in the members'
+    //    (post)order, so the new order is still a topological order of the elimination tree
+    std::vector<i64> root(ns);
+    for (i64 s = 0; s < ns; s++) root[s] = find(s);
+    std::vector<std::vector<i64>> members(ns), mkids(ns);
+    for (i64 s = 0; s < ns; s++) members[root[s]].push_back(s);
+    std::vector<char> is_root(ns, 0);
+    for (i64 s = 0; s < ns; s++)
+        if (root[s] == s) {
+            is_root[s] = 1;
+            // parent of a merged front: the merged front of its top member's parent
+            i64 top = members[s].back();
+            if (par1[top] >= 0) mkids[root[par1[top]]].push_back(s);
+        }
+    std::vector<i64> perm2, R2;
+    perm2.reserve(n);
+    R2.push_back(0);
+    std::vector<std::pair<i64, size_t>> stack;
+    for (i64 s = 0; s < ns; s++) {
+        if (!is_root[s]) continue;
+        i64 top = members[s].back();
+        if (par1[top] >= 0) continue;
+        stack.push_back({s, 0});
+        while (!stack.empty()) {
+            auto &tp = stack.back();
+            i64 m = tp.first;
+            if (tp.second < mkids[m].size()) {
+                i64 c = mkids[m][tp.second++];
+                stack.push_back({c, 0});
+            } else {
+                for (i64 mem : members[m])
+                    for (i64 v = R1[mem]; v < R1[mem + 1]; v++) perm2.push_back(perm1[v]);
+                R2.push_back((i64)perm2.size());
+                stack.pop_back();
+            }
+        }
+    }
+    if ((i64)perm2.size() != n) return "internal error: amalgamation lost vertices";
+    err = finish(G, n, colptr, rowval, perm2, R2, out);
+    out.seconds_total = now() - t0;
+    return err;
+}
+
+}  // namespace pp

@@ -1,0 +1,63 @@
+// pp_symbolic.h -- host symbolic analysis of the multifrontal semiring LU (internal header).
+//
+// The reference delegates this step to CliqueTrees.jl (cliquetree(symmetric(graph); alg), ChordalSymbolic,
+// src/CPU/chordal_ssymbolic.jl:26-184): a fill-reducing order, the elimination tree and the supernodes ("fronts")
+// with their separators.  This is an independent implementation of the same objects:
+//   * the pattern is symmetrized (the reference orders symmetric(graph), chordal_ssymbolic.jl:67);
+//   * the order is nested dissection on level structures, with minimum degree on the leaves;
+//   * the elimination tree is postordered, fundamental supernodes are found from the column counts, and small
+//     fronts are merged into their parents (relaxed amalgamation: explicit semiring zeros in exchange for wider
+//     fronts);
+//   * separators are computed by the supernodal symbolic factorization, so a structure given from outside (a
+//     permutation plus a partition into fronts, e.g. the reference's own) yields the same separators.
+// Unlike the reference, strongly connected components are not split into separate blocks: the whole pattern is
+// one block, and the block triangular structure is absorbed into the fronts (same star, more fill on DAG-like
+// inputs).
+#pragma once
+#include <cstdint>
+#include <string>
+#include <vector>
+
+namespace pp {
+
+typedef int64_t i64;
+typedef int32_t i32;
+
+struct SymOptions {
+    int ordering = 0;          // 0 = nested dissection, 1 = natural (identity), 2 = given permutation
+    int amalgamate = 1;        // relaxed amalgamation on/off
+    int nd_leaf = 32;          // subgraphs of at most this many vertices are ordered by minimum degree
+    int relax_small = 4;       // fronts of at most this many columns always merge
+    double relax_z[3] = {0.8, 0.1, 0.05};   // zero fraction allowed at <= 16, <= 48, > 48 columns
+    int relax_cols[2] = {16, 48};
+    int max_front_cols = 1 << 30;
+};
+
+struct Symbolic {
+    i64 n = 0;
+    std::vector<i64> perm, invp;        // perm[new] = old, invp[old] = new
+    i64 nf = 0;
+    std::vector<i64> Rptr, Sptr, Stgt;  // res(f) = [Rptr[f], Rptr[f+1]), sep(f) = Stgt[Sptr[f]..Sptr[f+1]) ascending
+    std::vector<i64> parent;            // parent front, -1 for roots
+    std::vector<i64> fdsc;              // first descendant front of each front
+    std::vector<i64> Dptr, Lptr;        // running sums of nn^2 and nn*na
+    // the input pattern: where each stored entry of A lands in the frontal matrices
+    i64 nnz = 0;
+    std::vector<i64> entry_front;       // front owning entry p (the front of min(new row, new col))
+    std::vector<i32> entry_row, entry_col;   // local row / column of entry p in that front's bag (res then sep)
+    // work counts (semiring multiply-adds) of the exact structure, before amalgamation, and of the executed one
+    double madds_factor_alg = 0, madds_star_alg = 0, madds_rhs_alg = 0, nnzL_alg = 0;
+    double madds_factor = 0, madds_star = 0, madds_rhs = 0, nnzL = 0;
+    double seconds_order = 0, seconds_total = 0;
+};
+
+// Build the symbolic structure of the CSC pattern (colptr, rowval) of an n x n matrix.  Returns "" on success,
+// otherwise an error message.  `given_perm` is used when opts.ordering == 2.
+std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOptions &opts, const i64 *given_perm,
+                    Symbolic &out);
+
+// The symbolic structure for a given permutation and partition into fronts (Rptr, fronts in postorder).
+std::string analyze_given(i64 n, const i64 *colptr, const i64 *rowval, const i64 *perm, i64 nf, const i64 *Rptr,
+                          Symbolic &out);
+
+}  // namespace pp

@@ -1,0 +1,407 @@
+"""pathpack_hip: PATHPACK.jl's multifrontal semiring LU on one MI355X.
+
+The host-side mirror of the reference's CPU API (src/CPU/abstract_slu.jl), over the C ABI of libpathpack_hip.so:
+
+    F = mlu(MinPlus(), A)        # abstract_slu.jl:44-58   ordering + symbolic on the host, factorization on the GPU
+    C = Matrix(F)                # abstract_slu.jl:10-14   the full star A* (n x n, original labels)
+    D = mstar(MinPlus(), A)      # abstract_slu.jl:81-87   Matrix(mlu(s, A))
+    lmul_(F, B)                  # lmul!(F, B), :131-134    B <- A* B  (columns of the star)
+    rmul_(B, F)                  # rmul!(B, F), :142-145    B <- B A*  (rows of the star)
+
+Python has no ``!`` in names, so ``lmul!``/``rmul!`` are ``lmul_``/``rmul_`` (the in-place convention of torch).
+``A`` is a square sparse matrix (scipy.sparse, or ``(n, colptr, rowval, nzval)``, or a ``workloads.Graph``) with
+``A[i, j]`` the weight of the arc i -> j, or a dense numpy array (one dense front, as the reference's DenseSLU).  The
+element type follows the values, as ``ChordalSLU{Sem, T}`` does: float32 / float64, int32 for OrAnd.  Host arrays
+come back as numpy arrays; ``device=True`` keeps results in HBM as torch tensors.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+
+import numpy as np
+
+from . import _lib
+from ._lib import (PathpackArgumentError, PathpackDeviceError, PathpackError, PathpackMemoryError,
+                   PathpackUnsupportedError, check, lib)
+
+__all__ = [
+    "AbstractSemiring", "MinPlus", "MaxPlus", "MaxMin", "MinMax", "PlusProd", "OrAnd",
+    "szero", "sone", "mlu", "mstar", "lmul_", "rmul_", "Matrix", "Factorization", "Symbolic", "symbolic",
+    "Context", "context", "PathpackError", "PathpackArgumentError", "PathpackMemoryError",
+    "PathpackUnsupportedError", "PathpackDeviceError",
+]
+
+F32, F64, I32 = 0, 1, 2
+
+
+# ===== semirings (src/CPU/semiring/*.jl) =====
+
+class AbstractSemiring:
+    id = -1
+    name = ""
+    integral = False
+
+    def __repr__(self):
+        return f"{self.name}()"
+
+    def __eq__(self, other):
+        return type(self) is type(other)
+
+    def __hash__(self):
+        return hash(self.id)
+
+
+class MinPlus(AbstractSemiring):
+    """([-Inf, Inf], min, +): shortest paths (tropical.jl:15)."""
+    id, name = 0, "MinPlus"
+
+
+class MaxPlus(AbstractSemiring):
+    """([-Inf, Inf], max, +): longest paths (tropical.jl:31)."""
+    id, name = 1, "MaxPlus"
+
+
+class MaxMin(AbstractSemiring):
+    """([-Inf, Inf], max, min): widest paths (bottleneck.jl:31)."""
+    id, name, integral = 2, "MaxMin", True
+
+
+class MinMax(AbstractSemiring):
+    """([-Inf, Inf], min, max): minimax paths (bottleneck.jl:15)."""
+    id, name, integral = 3, "MinMax", True
+
+
+class PlusProd(AbstractSemiring):
+    """([0, Inf], +, *): walk sums (I - A)^-1 (real.jl:16)."""
+    id, name = 4, "PlusProd"
+
+
+class OrAnd(AbstractSemiring):
+    """(2^n, |, &) on int32 bit sets: label reachability (boolean.jl:31)."""
+    id, name, integral = 5, "OrAnd", True
+
+
+def szero(s: AbstractSemiring, dtype):
+    """The semiring zero as a value of ``dtype`` (szero, semiring.jl:54-59)."""
+    dtype = np.dtype(dtype)
+    if isinstance(s, OrAnd):
+        return dtype.type(0)
+    return dtype.type({0: np.inf, 1: -np.inf, 2: -np.inf, 3: np.inf, 4: 0.0}[s.id])
+
+
+def sone(s: AbstractSemiring, dtype):
+    """The semiring one as a value of ``dtype`` (sone, semiring.jl:61-66)."""
+    dtype = np.dtype(dtype)
+    if isinstance(s, OrAnd):
+        return dtype.type(np.iinfo(dtype).max)
+    return dtype.type({0: 0.0, 1: 0.0, 2: np.inf, 3: -np.inf, 4: 1.0}[s.id])
+
+
+def _dtype_code(dtype) -> int:
+    dtype = np.dtype(dtype)
+    if dtype == np.float32:
+        return F32
+    if dtype == np.float64:
+        return F64
+    if dtype == np.int32:
+        return I32
+    raise PathpackUnsupportedError(_lib.PP_EUNSUPPORTED, f"element type {dtype} is not supported")
+
+
+def _p(a: np.ndarray):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+# ===== device context =====
+
+class Context:
+    """One HIP stream on one device (pp_ctx)."""
+
+    def __init__(self, device: int = 0):
+        h = ctypes.c_void_p()
+        check(lib().pp_init(ctypes.byref(h), int(device)))
+        self.handle = h
+        self.device = int(device)
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h is not None and h.value:
+            lib().pp_destroy(h)
+            self.handle = None
+
+    def check(self, status: int):
+        check(status, self.handle)
+
+    def synchronize(self):
+        self.check(lib().pp_synchronize(self.handle))
+
+    def set_timing(self, on: bool):
+        self.check(lib().pp_set_timing(self.handle, 1 if on else 0))
+
+    def timing(self) -> np.ndarray:
+        t = (ctypes.c_double * 8)()
+        self.check(lib().pp_get_timing(self.handle, t))
+        return np.array(t[:])
+
+
+_contexts: dict[int, Context] = {}
+_ctx_lock = threading.Lock()
+
+
+def context(device: int = 0) -> Context:
+    """The shared context of a device (created on first use)."""
+    with _ctx_lock:
+        if device not in _contexts:
+            _contexts[device] = Context(device)
+        return _contexts[device]
+
+
+# ===== sparse input =====
+
+def _as_csc(A):
+    """(n, colptr int64, rowval int64, nzval) of a square sparse matrix, canonical (sorted, no duplicates)."""
+    if hasattr(A, "colptr") and hasattr(A, "rowval"):
+        return int(A.n), np.ascontiguousarray(A.colptr, np.int64), np.ascontiguousarray(A.rowval, np.int64), \
+            np.ascontiguousarray(A.nzval)
+    if isinstance(A, tuple) and len(A) == 4:
+        n, cp, rv, nz = A
+        return int(n), np.ascontiguousarray(cp, np.int64), np.ascontiguousarray(rv, np.int64), np.ascontiguousarray(nz)
+    try:
+        import scipy.sparse as sp
+    except ImportError:  # pragma: no cover
+        sp = None
+    if sp is not None and sp.issparse(A):
+        if A.shape[0] != A.shape[1]:
+            raise PathpackArgumentError(_lib.PP_EINVAL, "the matrix must be square")
+        M = sp.csc_matrix(A, copy=True)
+        M.sort_indices()
+        cp = M.indptr.astype(np.int64)
+        rv = M.indices.astype(np.int64)
+        dup = (np.diff(rv) == 0) & (np.repeat(np.arange(M.shape[1]), np.diff(cp))[1:] ==
+                                    np.repeat(np.arange(M.shape[1]), np.diff(cp))[:-1])
+        if dup.any():
+            raise PathpackArgumentError(_lib.PP_EINVAL, "duplicate entries: combine parallel arcs with the semiring's "
+                                                        "(+) before the call")
+        return int(M.shape[0]), cp, rv, np.ascontiguousarray(M.data)
+    raise PathpackArgumentError(_lib.PP_EINVAL, f"unsupported matrix type {type(A)}")
+
+
+# ===== symbolic analysis =====
+
+class Symbolic:
+    """Ordering, supernodal elimination tree and separators of a pattern (pp_sym; ssymbolic,
+    chordal_ssymbolic.jl:26-57).  Host only."""
+
+    def __init__(self, handle: ctypes.c_void_p, n: int, nnz: int):
+        self.handle = handle
+        self.n = n
+        self.nnz = nnz
+        nn = ctypes.c_int64()
+        nf = ctypes.c_int64()
+        ns = ctypes.c_int64()
+        mf = ctypes.c_int64()
+        check(lib().pp_sym_size(handle, ctypes.byref(nn), ctypes.byref(nf), ctypes.byref(ns), ctypes.byref(mf)))
+        self.nf = nf.value
+        self.nstgt = ns.value
+        self.maxfront = mf.value
+        self._export = None
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h is not None and h.value:
+            lib().pp_sym_destroy(h)
+            self.handle = None
+
+    def export(self) -> dict:
+        """perm (new -> old), Rptr, Sptr, Stgt, parent, all 0-based."""
+        if self._export is None:
+            perm = np.empty(self.n, np.int64)
+            R = np.empty(self.nf + 1, np.int64)
+            S = np.empty(self.nf + 1, np.int64)
+            T = np.empty(max(1, self.nstgt), np.int64)
+            P = np.empty(max(1, self.nf), np.int64)
+            check(lib().pp_sym_export(self.handle, _p(perm), _p(R), _p(S), _p(T), _p(P)))
+            self._export = {"perm": perm, "Rptr": R, "Sptr": S, "Stgt": T[:self.nstgt], "parent": P[:self.nf]}
+        return self._export
+
+    def stats(self) -> dict:
+        st = (ctypes.c_double * 10)()
+        check(lib().pp_sym_stats(self.handle, st))
+        keys = ["madds_factor_alg", "madds_star_alg", "madds_rhs_alg", "nnzL_alg", "madds_factor", "madds_star",
+                "madds_rhs", "nnzL", "seconds_order", "seconds_total"]
+        return dict(zip(keys, st[:]))
+
+
+_ALGS = {None: 0, "nd": 0, "ND": 0, "natural": 1}
+
+
+def symbolic(A, alg=None, amalgamate: bool = True) -> Symbolic:
+    """Symbolic analysis of the pattern of A.  ``alg``: None / "nd" (nested dissection), "natural", or a permutation
+    (0-based, perm[new] = old) -- the reference's ``alg`` keyword (abstract_slu.jl:44)."""
+    n, cp, rv, _ = _as_csc(A)
+    h = ctypes.c_void_p()
+    if isinstance(alg, (str, type(None))):
+        if alg not in _ALGS:
+            raise PathpackArgumentError(_lib.PP_EINVAL, f"unknown ordering {alg!r}")
+        check(lib().pp_symbolic(n, _p(cp), _p(rv), _ALGS[alg], 1 if amalgamate else 0, None, ctypes.byref(h)))
+    else:
+        perm = np.ascontiguousarray(alg, np.int64)
+        if perm.shape != (n,):
+            raise PathpackArgumentError(_lib.PP_EINVAL, "the permutation must have n entries")
+        check(lib().pp_symbolic(n, _p(cp), _p(rv), 2, 1 if amalgamate else 0, _p(perm), ctypes.byref(h)))
+    return Symbolic(h, n, int(cp[-1]))
+
+
+def symbolic_given(A, perm, Rptr) -> Symbolic:
+    """The structure for a given permutation and partition into fronts (e.g. the reference's own)."""
+    n, cp, rv, _ = _as_csc(A)
+    perm = np.ascontiguousarray(perm, np.int64)
+    Rptr = np.ascontiguousarray(Rptr, np.int64)
+    h = ctypes.c_void_p()
+    check(lib().pp_symbolic_given(n, _p(cp), _p(rv), _p(perm), Rptr.size - 1, _p(Rptr), ctypes.byref(h)))
+    return Symbolic(h, n, int(cp[-1]))
+
+
+# ===== factorization =====
+
+class Factorization:
+    """A* = U* L* on the device (pp_fac; the reference's ChordalSLU, chordal_slu.jl:1-26)."""
+
+    def __init__(self, s: AbstractSemiring, sym: Symbolic, dtype, handle, ctx: Context):
+        self.s = s
+        self.sym = sym
+        self.dtype = np.dtype(dtype)
+        self.handle = handle
+        self.ctx = ctx
+        self.n = sym.n
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h is not None and h.value:
+            lib().pp_fac_destroy(h)
+            self.handle = None
+
+    @property
+    def shape(self):
+        return (self.n, self.n)
+
+    @property
+    def perm(self) -> np.ndarray:
+        return self.sym.export()["perm"]
+
+    def export(self) -> dict:
+        """The factor in the reference's storage layout: LD/UD (diagonal blocks), LL (na x nn), UL (nn x na)."""
+        e = self.sym.export()
+        nn = np.diff(e["Rptr"])
+        na = np.diff(e["Sptr"])
+        nD = int((nn * nn).sum())
+        nL = int((nn * na).sum())
+        LD = np.empty(max(1, nD), self.dtype)
+        UD = np.empty(max(1, nD), self.dtype)
+        LL = np.empty(max(1, nL), self.dtype)
+        UL = np.empty(max(1, nL), self.dtype)
+        self.ctx.check(lib().pp_fac_export(self.ctx.handle, self.handle, _p(LD), _p(UD), _p(LL), _p(UL)))
+        return {"LD": LD[:nD], "UD": UD[:nD], "LL": LL[:nL], "UL": UL[:nL]}
+
+
+def _factor(s: AbstractSemiring, sym: Symbolic, nzval, ctx: Context) -> Factorization:
+    dt = _dtype_code(nzval.dtype)
+    if (dt == I32) != isinstance(s, OrAnd):
+        raise PathpackUnsupportedError(_lib.PP_EUNSUPPORTED, f"{s.name} does not support {nzval.dtype}")
+    h = ctypes.c_void_p()
+    nz = np.ascontiguousarray(nzval)
+    ctx.check(lib().pp_factor(ctx.handle, sym.handle, s.id, dt, _p(nz), ctypes.byref(h)))
+    return Factorization(s, sym, nz.dtype, h, ctx)
+
+
+def mlu(s: AbstractSemiring, A, alg=None, amalgamate: bool = True, device: int = 0, sym: Symbolic | None = None):
+    """Factorize the star of A over the semiring s: A* = U* L* (mlu, abstract_slu.jl:44-58).  A dense numpy A is one
+    dense front in its natural order (the reference's DenseSLU path, abstract_slu.jl:65-68)."""
+    ctx = context(device)
+    if isinstance(A, np.ndarray):
+        if A.ndim != 2 or A.shape[0] != A.shape[1]:
+            raise PathpackArgumentError(_lib.PP_EINVAL, "the matrix must be square")
+        n = A.shape[0]
+        cp = np.arange(0, n * n + 1, n, dtype=np.int64)
+        rv = np.tile(np.arange(n, dtype=np.int64), n)
+        nz = np.asfortranarray(A).ravel(order="F")
+        csc = (n, cp, rv, nz)
+        if sym is None:
+            sym = symbolic_given(csc, np.arange(n), np.array([0, n]) if n > 0 else np.array([0]))
+        return _factor(s, sym, nz, ctx)
+    n, cp, rv, nz = _as_csc(A)
+    if sym is None:
+        sym = symbolic((n, cp, rv, nz), alg=alg, amalgamate=amalgamate)
+    return _factor(s, sym, nz, ctx)
+
+
+def Matrix(F: Factorization, device: bool = False, out=None):
+    """The full star A* of a factorization (Matrix(F), abstract_slu.jl:10-14), n x n in the original labels.
+    ``device=True`` returns a torch tensor in HBM holding A* column-major, i.e. a tensor T with T[j, i] = A*[i, j]
+    (its transpose T.T is the star with Julia's indexing)."""
+    n = F.n
+    if device or (out is not None and not isinstance(out, np.ndarray)):
+        import torch
+
+        if out is None:
+            out = torch.empty((n, n), dtype=getattr(torch, str(F.dtype)), device=f"cuda:{F.ctx.device}")
+        if not out.is_contiguous() or tuple(out.shape) != (n, n):
+            raise PathpackArgumentError(_lib.PP_EINVAL, "out must be a contiguous n x n tensor")
+        F.ctx.check(lib().pp_star(F.ctx.handle, F.handle, ctypes.c_void_p(out.data_ptr()), n, 1))
+        return out
+    C = out if out is not None else np.empty((n, n), dtype=F.dtype, order="F")
+    if not C.flags.f_contiguous or C.shape != (n, n) or C.dtype != F.dtype:
+        raise PathpackArgumentError(_lib.PP_EINVAL, "out must be a Fortran-ordered n x n array of the factor's type")
+    F.ctx.check(lib().pp_star(F.ctx.handle, F.handle, _p(C), n, 0))
+    return C
+
+
+def mstar(s: AbstractSemiring, A, alg=None, amalgamate: bool = True, device: bool = False):
+    """The star A* = I (+) A (+) A^2 (+) ... as a dense matrix (mstar, abstract_slu.jl:81-87)."""
+    return Matrix(mlu(s, A, alg=alg, amalgamate=amalgamate), device=device)
+
+
+def _solve(F: Factorization, B, left: bool):
+    name = "lmul_" if left else "rmul_"
+    fn = lib().pp_lmul if left else lib().pp_rmul
+    if isinstance(B, np.ndarray):
+        if B.dtype != F.dtype:
+            raise PathpackArgumentError(_lib.PP_EINVAL, f"{name}: B must have the factor's element type {F.dtype}")
+        vec = B.ndim == 1
+        if vec and not left:
+            raise PathpackArgumentError(_lib.PP_EINVAL, "rmul_: B must be a matrix")
+        M = B.reshape(-1, 1) if vec else B
+        if left and M.shape[0] != F.n or (not left and M.shape[1] != F.n):
+            raise PathpackArgumentError(_lib.PP_EINVAL, f"{name}: B has the wrong size")
+        W = np.asfortranarray(M)
+        nrhs = W.shape[1] if left else W.shape[0]
+        ld = max(1, W.shape[0])
+        F.ctx.check(fn(F.ctx.handle, F.handle, _p(W), ld, nrhs, 0))
+        if W is not M:
+            M[...] = W
+        return B
+    import torch
+
+    if not isinstance(B, torch.Tensor) or not B.is_cuda:
+        raise PathpackArgumentError(_lib.PP_EINVAL, f"{name}: B must be a numpy array or a cuda tensor")
+    # a cuda tensor holds B column-major when B.T is contiguous (the layout Julia uses)
+    if B.dim() != 2 or not B.T.is_contiguous():
+        raise PathpackArgumentError(_lib.PP_EINVAL, f"{name}: a device B must be 2-D with B.T contiguous")
+    rows, cols = B.shape
+    if left and rows != F.n or (not left and cols != F.n):
+        raise PathpackArgumentError(_lib.PP_EINVAL, f"{name}: B has the wrong size")
+    nrhs = cols if left else rows
+    F.ctx.check(fn(F.ctx.handle, F.handle, ctypes.c_void_p(B.data_ptr()), max(1, rows), nrhs, 1))
+    return B
+
+
+def lmul_(F: Factorization, B):
+    """lmul!(F, B): B <- A* B, the least solution of X = A X (+) B (abstract_slu.jl:131-134)."""
+    return _solve(F, B, True)
+
+
+def rmul_(B, F: Factorization):
+    """rmul!(B, F): B <- B A*, the least solution of X = X A (+) B (abstract_slu.jl:142-145)."""
+    return _solve(F, B, False)
