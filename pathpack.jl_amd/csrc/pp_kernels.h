@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <type_traits>
 
 #include "pp_internal.h"
 #include "pp_semiring.h"
@@ -323,6 +324,23 @@ __global__ __launch_bounds__(NT) void k_build_packs(const T *__restrict__ F, con
 // DMODE 1 reads it transposed (L^T for forward, unit; U^T for backward with star), which is how lmul! runs on the
 // transposed right-hand sides.  One thread per row; the column indices and pack values are wave-uniform.
 
+// X[addr] <- X[addr] (+) v by compare-and-swap on the bit pattern; returns at once when (+) leaves the value
+// unchanged (the common case for min / max / or).  Exact and order-independent for the idempotent semirings.
+template <class S> __device__ inline void atomic_plus(typename S::value_type *addr, typename S::value_type v) {
+    typedef typename S::value_type T;
+    typedef typename std::conditional<sizeof(T) == 8, unsigned long long, unsigned int>::type U;
+    U *a = reinterpret_cast<U *>(addr);
+    U old = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    while (true) {
+        const T nv = S::plus(__builtin_bit_cast(T, old), v);
+        const U nb = __builtin_bit_cast(U, nv);
+        if (nb == old) return;
+        const U prev = atomicCAS(a, old, nb);
+        if (prev == old) return;
+        old = prev;
+    }
+}
+
 struct SweepArgs {
     const int32_t *plist, *tiles;   // tiles: prefix sums of row tiles (null: uniform [0, nrows))
     int32_t np, nrows;
@@ -348,7 +366,7 @@ __device__ inline void locate(const SweepArgs &a, int &pi, int &tile) {
     }
 }
 
-template <class S, int W, int DMODE>
+template <class S, int W, int DMODE, bool ATOMIC>
 __global__ __launch_bounds__(NT) void k_sweep_fwd(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
                                                   const typename S::value_type *__restrict__ Dpack,
                                                   const typename S::value_type *__restrict__ P) {
@@ -380,6 +398,18 @@ __global__ __launch_bounds__(NT) void k_sweep_fwd(typename S::value_type *__rest
 #pragma unroll
     for (int j = 0; j < W; j++)
         if (j < w) X[(i64)(c0 + j) * ld + r] = x[j];
+    if (ATOMIC) {
+        // several panels of one level may target the same columns of the same rows (solves): (+) atomically
+        for (int t = 0; t < e; t++) {
+            const T *q = Pp + (i64)t * w;
+            T v = S::zero();
+#pragma unroll
+            for (int j = 0; j < W; j++)
+                if (j < w) v = S::muladd(x[j], q[j], v);
+            atomic_plus<S>(X + (i64)E[t] * ld + r, v);
+        }
+        return;
+    }
     int t = 0;
     for (; t + 4 <= e; t += 4) {
         T *y0 = X + (i64)E[t] * ld, *y1 = X + (i64)E[t + 1] * ld, *y2 = X + (i64)E[t + 2] * ld, *y3 = X + (i64)E[t + 3] * ld;
@@ -644,15 +674,21 @@ template <class S> struct FactorRun {
 };
 
 template <class S, int W>
-static void launch_sweep(bool fwd, int dmode, typename S::value_type *X, i64 ld, const SweepArgs &a, unsigned grid,
-                         const void *Dpack, const void *pack, hipStream_t st) {
+static void launch_sweep(bool fwd, int dmode, bool atomic, typename S::value_type *X, i64 ld, const SweepArgs &a,
+                         unsigned grid, const void *Dpack, const void *pack, hipStream_t st) {
     typedef typename S::value_type T;
+    const T *D = (const T *)Dpack, *Pk = (const T *)pack;
     if (fwd) {
-        if (dmode == 0) k_sweep_fwd<S, W, 0><<<grid, NT, 0, st>>>(X, ld, a, (const T *)Dpack, (const T *)pack);
-        else k_sweep_fwd<S, W, 1><<<grid, NT, 0, st>>>(X, ld, a, (const T *)Dpack, (const T *)pack);
+        if (atomic) {
+            if (dmode == 0) k_sweep_fwd<S, W, 0, true><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+            else k_sweep_fwd<S, W, 1, true><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+        } else {
+            if (dmode == 0) k_sweep_fwd<S, W, 0, false><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+            else k_sweep_fwd<S, W, 1, false><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+        }
     } else {
-        if (dmode == 0) k_sweep_bwd<S, W, 0><<<grid, NT, 0, st>>>(X, ld, a, (const T *)Dpack, (const T *)pack);
-        else k_sweep_bwd<S, W, 1><<<grid, NT, 0, st>>>(X, ld, a, (const T *)Dpack, (const T *)pack);
+        if (dmode == 0) k_sweep_bwd<S, W, 0><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+        else k_sweep_bwd<S, W, 1><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
     }
 }
 
@@ -694,12 +730,12 @@ static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmod
             grid = (unsigned)(li.cnt * ntile);
         }
         switch (li.cls) {
-        case 0: launch_sweep<S, 1>(fwd, dmode, X, ld, a, grid, fac->Dpack, pack, st); break;
-        case 1: launch_sweep<S, 2>(fwd, dmode, X, ld, a, grid, fac->Dpack, pack, st); break;
-        case 2: launch_sweep<S, 4>(fwd, dmode, X, ld, a, grid, fac->Dpack, pack, st); break;
-        case 3: launch_sweep<S, 8>(fwd, dmode, X, ld, a, grid, fac->Dpack, pack, st); break;
-        case 4: launch_sweep<S, 16>(fwd, dmode, X, ld, a, grid, fac->Dpack, pack, st); break;
-        default: launch_sweep<S, 32>(fwd, dmode, X, ld, a, grid, fac->Dpack, pack, st); break;
+        case 0: launch_sweep<S, 1>(fwd, dmode, !star_rows, X, ld, a, grid, fac->Dpack, pack, st); break;
+        case 1: launch_sweep<S, 2>(fwd, dmode, !star_rows, X, ld, a, grid, fac->Dpack, pack, st); break;
+        case 2: launch_sweep<S, 4>(fwd, dmode, !star_rows, X, ld, a, grid, fac->Dpack, pack, st); break;
+        case 3: launch_sweep<S, 8>(fwd, dmode, !star_rows, X, ld, a, grid, fac->Dpack, pack, st); break;
+        case 4: launch_sweep<S, 16>(fwd, dmode, !star_rows, X, ld, a, grid, fac->Dpack, pack, st); break;
+        default: launch_sweep<S, 32>(fwd, dmode, !star_rows, X, ld, a, grid, fac->Dpack, pack, st); break;
         }
         LAUNCHCHK();
     }

@@ -12,7 +12,9 @@ Python has no ``!`` in names, so ``lmul!``/``rmul!`` are ``lmul_``/``rmul_`` (th
 ``A`` is a square sparse matrix (scipy.sparse, or ``(n, colptr, rowval, nzval)``, or a ``workloads.Graph``) with
 ``A[i, j]`` the weight of the arc i -> j, or a dense numpy array (one dense front, as the reference's DenseSLU).  The
 element type follows the values, as ``ChordalSLU{Sem, T}`` does: float32 / float64, int32 for OrAnd.  Host arrays
-come back as numpy arrays; ``device=True`` keeps results in HBM as torch tensors.
+come back as numpy arrays; ``device=True`` keeps results in HBM as ``DeviceArray`` buffers owned by the library
+(torch is not used on the device path: it ships its own HIP runtime, and one process cannot drive the GPU through
+two runtimes).
 """
 
 from __future__ import annotations
@@ -29,7 +31,7 @@ from ._lib import (PathpackArgumentError, PathpackDeviceError, PathpackError, Pa
 __all__ = [
     "AbstractSemiring", "MinPlus", "MaxPlus", "MaxMin", "MinMax", "PlusProd", "OrAnd",
     "szero", "sone", "mlu", "mstar", "lmul_", "rmul_", "Matrix", "Factorization", "Symbolic", "symbolic",
-    "Context", "context", "PathpackError", "PathpackArgumentError", "PathpackMemoryError",
+    "Context", "context", "DeviceArray", "PathpackError", "PathpackArgumentError", "PathpackMemoryError",
     "PathpackUnsupportedError", "PathpackDeviceError",
 ]
 
@@ -156,6 +158,45 @@ def context(device: int = 0) -> Context:
         if device not in _contexts:
             _contexts[device] = Context(device)
         return _contexts[device]
+
+
+# ===== device buffers =====
+
+class DeviceArray:
+    """A column-major array in HBM allocated through the library (pp_buffer_alloc).  ``DeviceArray.from_numpy``
+    uploads, ``numpy()`` downloads; ``ptr`` is the device address."""
+
+    def __init__(self, shape, dtype, ctx: Context | None = None):
+        self.ctx = ctx or context(0)
+        self.shape = tuple(int(x) for x in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        h = ctypes.c_void_p()
+        self.ctx.check(lib().pp_buffer_alloc(self.ctx.handle, max(1, self.nbytes), ctypes.byref(h)))
+        self.ptr = h.value
+
+    @classmethod
+    def from_numpy(cls, a: np.ndarray, ctx: Context | None = None) -> "DeviceArray":
+        d = cls(a.shape, a.dtype, ctx)
+        d.upload(a)
+        return d
+
+    def upload(self, a: np.ndarray):
+        a = np.asfortranarray(a, dtype=self.dtype)
+        if a.shape != self.shape:
+            raise PathpackArgumentError(_lib.PP_EINVAL, "shape mismatch")
+        self.ctx.check(lib().pp_upload(self.ctx.handle, ctypes.c_void_p(self.ptr), _p(a), self.nbytes))
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype, order="F")
+        self.ctx.check(lib().pp_download(self.ctx.handle, _p(out), ctypes.c_void_p(self.ptr), self.nbytes))
+        return out
+
+    def __del__(self):
+        p = getattr(self, "ptr", None)
+        if p:
+            lib().pp_buffer_free(self.ctx.handle, ctypes.c_void_p(p))
+            self.ptr = None
 
 
 # ===== sparse input =====
@@ -338,18 +379,15 @@ def mlu(s: AbstractSemiring, A, alg=None, amalgamate: bool = True, device: int =
 
 
 def Matrix(F: Factorization, device: bool = False, out=None):
-    """The full star A* of a factorization (Matrix(F), abstract_slu.jl:10-14), n x n in the original labels.
-    ``device=True`` returns a torch tensor in HBM holding A* column-major, i.e. a tensor T with T[j, i] = A*[i, j]
-    (its transpose T.T is the star with Julia's indexing)."""
+    """The full star A* of a factorization (Matrix(F), abstract_slu.jl:10-14), n x n in the original labels,
+    column-major.  ``device=True`` (or a DeviceArray ``out``) leaves it in HBM as a DeviceArray."""
     n = F.n
-    if device or (out is not None and not isinstance(out, np.ndarray)):
-        import torch
-
+    if device or isinstance(out, DeviceArray):
         if out is None:
-            out = torch.empty((n, n), dtype=getattr(torch, str(F.dtype)), device=f"cuda:{F.ctx.device}")
-        if not out.is_contiguous() or tuple(out.shape) != (n, n):
-            raise PathpackArgumentError(_lib.PP_EINVAL, "out must be a contiguous n x n tensor")
-        F.ctx.check(lib().pp_star(F.ctx.handle, F.handle, ctypes.c_void_p(out.data_ptr()), n, 1))
+            out = DeviceArray((n, n), F.dtype, F.ctx)
+        if out.shape != (n, n) or out.dtype != F.dtype:
+            raise PathpackArgumentError(_lib.PP_EINVAL, "out must be an n x n DeviceArray of the factor's type")
+        F.ctx.check(lib().pp_star(F.ctx.handle, F.handle, ctypes.c_void_p(out.ptr), n, 1))
         return out
     C = out if out is not None else np.empty((n, n), dtype=F.dtype, order="F")
     if not C.flags.f_contiguous or C.shape != (n, n) or C.dtype != F.dtype:
@@ -382,18 +420,15 @@ def _solve(F: Factorization, B, left: bool):
         if W is not M:
             M[...] = W
         return B
-    import torch
-
-    if not isinstance(B, torch.Tensor) or not B.is_cuda:
-        raise PathpackArgumentError(_lib.PP_EINVAL, f"{name}: B must be a numpy array or a cuda tensor")
-    # a cuda tensor holds B column-major when B.T is contiguous (the layout Julia uses)
-    if B.dim() != 2 or not B.T.is_contiguous():
-        raise PathpackArgumentError(_lib.PP_EINVAL, f"{name}: a device B must be 2-D with B.T contiguous")
+    if not isinstance(B, DeviceArray) or len(B.shape) != 2:
+        raise PathpackArgumentError(_lib.PP_EINVAL, f"{name}: B must be a numpy array or a 2-D DeviceArray")
+    if B.dtype != F.dtype:
+        raise PathpackArgumentError(_lib.PP_EINVAL, f"{name}: B must have the factor's element type {F.dtype}")
     rows, cols = B.shape
     if left and rows != F.n or (not left and cols != F.n):
         raise PathpackArgumentError(_lib.PP_EINVAL, f"{name}: B has the wrong size")
     nrhs = cols if left else rows
-    F.ctx.check(fn(F.ctx.handle, F.handle, ctypes.c_void_p(B.data_ptr()), max(1, rows), nrhs, 1))
+    F.ctx.check(fn(F.ctx.handle, F.handle, ctypes.c_void_p(B.ptr), max(1, rows), nrhs, 1))
     return B
 
 

@@ -1,0 +1,220 @@
+"""Parity of the HIP path with the oracle, through the C ABI (libpathpack_hip.so), on one MI355X.
+
+Bit-exact for MinPlus / MaxPlus / MaxMin / MinMax / OrAnd (integer-valued weights), relative error <= 1e-12 for
+PlusProd in float64 (1e-5 in float32).  Both sides use the same symbolic structure, so the factors themselves are
+compared, as the reference's GPU suite does (test/gpu/test_factor.jl:31,52).
+"""
+
+import numpy as np
+import pytest
+
+import oracle as O
+import site_fixtures as SF
+from helpers import SEMIRINGS, assert_star_equal, bits, dtype_for, oracle_sym, weighted
+import pathpack_hip as P
+from pathpack_hip import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+ALL = [O.MINPLUS, O.MAXPLUS, O.MAXMIN, O.MINMAX, O.PLUSPROD, O.ORAND]
+
+
+def rtol_for(s, dtype):
+    return 1e-12 if np.dtype(dtype) == np.float64 else 1e-5
+
+
+def graphs():
+    return {
+        "digraph40": W.random_digraph(40, 0.08, 1),
+        "digraph150": W.random_digraph(150, 0.02, 2),
+        "digraph300": W.random_digraph(300, 0.01, 3),
+        "grid17x13": W.grid((17, 13)),
+        "grid6x7x5": W.grid((6, 7, 5)),
+        "rgg700": W.rgg(700, seed=21),
+    }
+
+
+def both(g, s, dtype, amalgamate=True):
+    sym = P.symbolic(g, amalgamate=amalgamate)
+    F = P.mlu(SEMIRINGS[s], g, sym=sym)
+    Fo = O.factor(s, oracle_sym(sym), g.colptr, g.rowval, g.nzval)
+    return sym, F, Fo
+
+
+def compare_factor(s, F, Fo, dtype):
+    e = F.export()
+    if s == O.PLUSPROD:
+        for a, b in ((e["LD"], Fo.LD), (e["LL"], Fo.LL), (e["UL"], Fo.UL)):
+            assert_star_equal(s, a, b, rtol=1e-10 if np.dtype(dtype) == np.float64 else 1e-4)
+        return
+    assert np.array_equal(bits(e["LD"]), bits(Fo.LD))
+    assert np.array_equal(bits(e["LL"]), bits(Fo.LL))
+    assert np.array_equal(bits(e["UL"]), bits(Fo.UL))
+
+
+@pytest.mark.parametrize("name", list(graphs().keys()))
+@pytest.mark.parametrize("s", ALL)
+@pytest.mark.parametrize("fdtype", [np.float32, np.float64])
+def test_factor_and_star_match_oracle(name, s, fdtype):
+    if s == O.ORAND and fdtype == np.float64:
+        pytest.skip("OrAnd is int32 only")
+    dtype = dtype_for(s, fdtype)
+    g = weighted(graphs()[name], s, dtype)
+    print(f"case {name} s={s} dtype={np.dtype(dtype)}", flush=True)
+    sym, F, Fo = both(g, s, dtype)
+    compare_factor(s, F, Fo, dtype)
+    C = P.Matrix(F)
+    Co = O.star(Fo)
+    assert_star_equal(s, C, Co, rtol=rtol_for(s, dtype) * 10)
+
+
+@pytest.mark.parametrize("s", ALL)
+def test_solves_match_oracle(s):
+    dtype = dtype_for(s, np.float64)
+    g = weighted(W.random_digraph(260, 0.012, 8), s, dtype)
+    print(f"case solves s={s}", flush=True)
+    sym, F, Fo = both(g, s, dtype)
+    rng = np.random.default_rng(3)
+    # unit right-hand sides plus a few dense ones
+    k = 37
+    B = np.full((g.n, k), O.zero(s, dtype), dtype=dtype, order="F")
+    B[rng.integers(0, g.n, k), np.arange(k)] = O.one(s, dtype)
+    if s == O.ORAND:
+        B[:, -3:] = rng.integers(0, 128, (g.n, 3)).astype(np.int32)
+    elif s == O.PLUSPROD:
+        B[:, -3:] = rng.random((g.n, 3))
+    else:
+        B[:, -3:] = rng.integers(0, 50, (g.n, 3)).astype(dtype)
+    L = P.lmul_(F, B.copy(order="F"))
+    assert_star_equal(s, L, O.lmul(Fo, B), rtol=1e-12)
+    R = P.rmul_(np.asfortranarray(B.T.copy()), F)
+    assert_star_equal(s, R, O.rmul(Fo, np.asfortranarray(B.T)), rtol=1e-12)
+
+
+@pytest.mark.parametrize("name", ["paris", "bunny"])
+def test_factor_matches_reference_fixture(name):
+    """The HIP factorization with the reference's own ordering and fronts reproduces the reference's factor of the
+    demo graph bit for bit (non-integer Float32 weights)."""
+    n, cp, rv, nz = SF.graph_csc(name)
+    fx = SF.factor_fixture(name)
+    sym = P.symbolic_given((n, cp, rv, nz), fx["perm"], fx["Rptr"])
+    F = P.mlu(P.MinPlus(), (n, cp, rv, nz), sym=sym)
+    e = F.export()
+    nn = np.diff(fx["Rptr"])
+    Dp = np.concatenate([[0], np.cumsum(nn * nn)])
+    D = e["LD"].copy()   # LD holds L (strict lower) and U (upper) of every diagonal block
+    assert np.array_equal(bits(D), bits(fx["D"]))
+    assert np.array_equal(bits(e["UL"]), bits(fx["UL"]))
+    assert np.array_equal(bits(e["LL"]), bits(fx["LL"]))
+    # rows of the star from the fixture factor: GPU rmul! equals the oracle's rmul! bit for bit
+    Fo = O.factor(O.MINPLUS, O.Sym(n, fx["Rptr"], fx["Sptr"], fx["Stgt"], fx["perm"]), cp, rv, nz)
+    srcs = np.array([0, n - 1, 1, n - 2, 777])
+    B = np.full((srcs.size, n), np.inf, np.float32, order="F")
+    B[np.arange(srcs.size), srcs] = 0
+    assert np.array_equal(bits(P.rmul_(B.copy(order="F"), F)), bits(O.rmul(Fo, B)))
+
+
+def test_readme_and_label_convention():
+    inf = np.inf
+    g = W.from_arcs(5, np.array([1, 1, 2, 3, 4, 4]) - 1, np.array([2, 3, 4, 2, 1, 5]) - 1,
+                    np.array([3.0, 8.0, 1.0, 4.0, 2.0, 7.0]))
+    D = P.mstar(P.MinPlus(), g)
+    assert np.array_equal(D, [[0, 3, 8, 4, 11], [3, 0, 11, 1, 8], [7, 4, 0, 5, 12], [2, 5, 10, 0, 7],
+                              [inf, inf, inf, inf, 0]])
+    Wd = P.mstar(P.MaxMin(), g)
+    assert np.array_equal(Wd, [[inf, 4, 8, 1, 1], [1, inf, 1, 1, 1], [1, 4, inf, 1, 1], [2, 2, 2, inf, 7],
+                               [-inf, -inf, -inf, -inf, inf]])
+    F = P.mlu(P.MinPlus(), g)
+    b = np.full(5, inf)
+    b[4] = 0
+    assert np.array_equal(P.lmul_(F, b), [11, 8, 12, 7, 0])
+    Bm = np.full((1, 5), inf)
+    Bm[0, 0] = 0
+    assert np.array_equal(P.rmul_(Bm, F), [[0, 3, 8, 4, 11]])
+    g3 = W.from_arcs(3, np.array([0, 1, 2]), np.array([1, 2, 0]), np.array([1.0, 2.0, 4.0], np.float32))
+    assert np.array_equal(P.mstar(P.MinPlus(), g3), np.array([[0, 1, 3], [6, 0, 2], [4, 5, 0]], np.float32))
+
+
+def test_dense_input_is_one_front():
+    rng = np.random.default_rng(4)
+    A = rng.integers(1, 100, (70, 70)).astype(np.float64)
+    A[rng.random(A.shape) < 0.7] = np.inf
+    D = P.mstar(P.MinPlus(), A)
+    assert np.array_equal(D, O.floyd_warshall(O.MINPLUS, A))
+
+
+def test_grid64_star_vs_dijkstra():
+    """Configuration 1: MinPlus mstar of the directed 64 x 64 grid (Float64) equals Dijkstra exactly."""
+    g = W.config_graph(1)
+    D = P.mstar(P.MinPlus(), g)
+    assert np.array_equal(D, O.dijkstra_rows(g))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (37, 23, 19), (64, 64, 64), (130, 67, 200), (257, 129, 33)])
+@pytest.mark.parametrize("s", [O.MINPLUS, O.MAXMIN, O.PLUSPROD])
+def test_sgemx_matches_oracle(m, n, k, s):
+    dtype = np.float32
+    rng = np.random.default_rng(m * 1000 + n)
+    A = rng.integers(0, 1000, (m, k)).astype(dtype)
+    B = rng.integers(0, 1000, (k, n)).astype(dtype)
+    C = rng.integers(0, 3000, (m, n)).astype(dtype)
+    if s == O.PLUSPROD:
+        A, B, C = A / 1000, B / 1000, C / 1000
+    else:
+        A[rng.random(A.shape) < 0.1] = np.inf
+        B[rng.random(B.shape) < 0.1] = np.inf
+    ref = O.sgemx(s, A, B, C)
+    ctx = P.context(0)
+    dA, dB, dC = P.DeviceArray.from_numpy(A), P.DeviceArray.from_numpy(B), P.DeviceArray.from_numpy(C)
+    ctx.check(P.lib().pp_sgemx(ctx.handle, s, 0, m, n, k, dA.ptr, m, dB.ptr, k, dC.ptr, m))
+    ctx.synchronize()
+    got = dC.numpy()
+    if s == O.PLUSPROD:
+        assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)) < 1e-5
+    else:
+        assert np.array_equal(bits(got), bits(ref))
+
+
+@pytest.mark.parametrize("s", [O.MINPLUS, O.MAXMIN, O.ORAND, O.PLUSPROD])
+@pytest.mark.parametrize("nb", [1, 7, 33, 64])
+def test_getrf_star_batched_matches_oracle(s, nb):
+    dtype = dtype_for(s, np.float32 if s != O.PLUSPROD else np.float64)
+    rng = np.random.default_rng(nb)
+    batch = 50
+    if s == O.ORAND:
+        A = rng.integers(0, 2 ** 20, (batch, nb, nb)).astype(np.int32)
+    elif s == O.PLUSPROD:
+        A = (rng.random((batch, nb, nb)) * (0.5 / nb)).astype(dtype)
+    else:
+        A = rng.integers(0, 1000, (batch, nb, nb)).astype(dtype)
+        A[rng.random(A.shape) < 0.1] = np.inf if s == O.MINPLUS else -np.inf
+        A[:, np.arange(nb), np.arange(nb)] = 0 if s == O.MINPLUS else A[:, np.arange(nb), np.arange(nb)]
+    LU, TL, TU = O.getrf_star_batched(s, A)
+    ctx = P.context(0)
+    flat = A.reshape(batch * nb, nb)            # fronts back to back, each stored as the C-order block A[b]
+    dA = P.DeviceArray.from_numpy(np.asfortranarray(flat.ravel().reshape(-1, 1)))
+    dTL = P.DeviceArray(dA.shape, dA.dtype)
+    dTU = P.DeviceArray(dA.shape, dA.dtype)
+    dt = {np.dtype(np.float32): 0, np.dtype(np.float64): 1, np.dtype(np.int32): 2}[np.dtype(dtype)]
+    ctx.check(P.lib().pp_getrf_star_batched(ctx.handle, s, dt, nb, batch, dA.ptr, dTL.ptr, dTU.ptr))
+    ctx.synchronize()
+    for got, ref in ((dA, LU), (dTL, TL), (dTU, TU)):
+        assert_star_equal(s, got.numpy().reshape(batch, nb, nb), ref, rtol=1e-12)
+
+
+def test_device_resident_star_and_solves():
+    """Matrix(F, device=True) and solves on DeviceArrays give the same bits as the host paths."""
+    g = weighted(W.random_digraph(90, 0.05, 12), O.MINPLUS, np.float32)
+    F = P.mlu(P.MinPlus(), g)
+    C = P.Matrix(F)
+    D = P.Matrix(F, device=True)
+    assert np.array_equal(bits(D.numpy()), bits(C))
+    B = np.full((g.n, 5), np.inf, np.float32, order="F")
+    B[[0, 10, 20, 30, 89], np.arange(5)] = 0
+    dB = P.DeviceArray.from_numpy(B)
+    P.lmul_(F, dB)
+    assert np.array_equal(bits(dB.numpy()), bits(C[:, [0, 10, 20, 30, 89]]))
+    R = np.asfortranarray(B.T)
+    dR = P.DeviceArray.from_numpy(R)
+    P.rmul_(dR, F)
+    assert np.array_equal(bits(dR.numpy()), bits(C[[0, 10, 20, 30, 89], :]))

