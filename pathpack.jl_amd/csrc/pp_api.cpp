@@ -246,7 +246,8 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *sym, int semiring, int
     const size_t need = es * ((size_t)P.arena + nD + 2 * nL + (size_t)W.ndpack + 2 * (size_t)W.npack + (size_t)S.nnz) +
                         sizeof(i64) * (3 * (size_t)S.nnz + 6 * (size_t)S.nf + 2 * (size_t)S.n) +
                         sizeof(int32_t) * (W.Eidx.size() + W.plist.size() + W.tiles.size() + 16 * (size_t)W.np +
-                                           P.ftask.size() + P.stask.size() + P.flist.size() + P.relpos.size());
+                                           P.ftask.size() + P.stask.size() + P.flist.size() + P.atask.size() +
+                                           P.relpos.size());
     size_t freeb = 0, totalb = 0;
     CHECK_HIP(ctx, hipMemGetInfo(&freeb, &totalb));
     if (need > freeb)
@@ -279,6 +280,7 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *sym, int semiring, int
     UP(P.Sptr32, d.Sptr);
     UP(P.entry_pos, d.entry_pos);
     UP(P.flist, d.flist);
+    UP(P.atask, d.atask);
     UP(P.ftask, d.ftask);
     UP(P.stask, d.stask);
     UP(S.Dptr, d.Dptr);
@@ -289,6 +291,7 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *sym, int semiring, int
     UP(W.w, d.p_w);
     UP(W.e, d.p_e);
     UP(W.lo_ext, d.p_lo);
+    UP(W.chunks, d.p_chunks);
     UP(W.eoff, d.p_eoff);
     UP(W.poff, d.p_poff);
     UP(W.doff, d.p_doff);
@@ -301,6 +304,8 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *sym, int semiring, int
     UP(W.tiles, d.tiles);
     UP(S.perm, d.perm);
     UP(S.invp, d.invp);
+    std::vector<int32_t> invp32(S.invp.begin(), S.invp.end());
+    UP(invp32, d.invp32);
 #undef UP
     auto alloc = [&](void **p, size_t elems) -> bool {
         return hipMalloc(p, std::max<size_t>(1, elems) * es) == hipSuccess;

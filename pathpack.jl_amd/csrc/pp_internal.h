@@ -12,8 +12,9 @@
 // Sweep plan.  Each front's residual is cut into panels of at most PANEL_W columns.  A panel p of front f covers
 // the permuted columns [c0, c0 + w); its "extension" E_p is the rest of the residual after the panel followed by
 // sep(f), i.e. the frontal-matrix local indices lo_ext .. nj-1 with lo_ext = c0 - Rptr[f] + w.  Packs:
-//   Dpack[p]: the panel's w x w diagonal block of F (L strict lower, U upper with diagonal), at i + j*w
-//   Upack[p]: U[c_j, E_t] at t*w + j          Lpack[p]: L[E_t, c_j] at t*w + j
+//   Dpack[p]: the panel's w x w diagonal block of F (L strict lower, U upper with diagonal), at i + j*Wc
+//   Upack[p]: U[c_j, E_t] at t*Wc + j         Lpack[p]: L[E_t, c_j] at t*Wc + j
+// with Wc the panel's width class (the power of two >= w); the padding holds the semiring zero.
 // A forward sweep visits panels leaves to root (each panel after its front's previous panel and after all
 // panels of its children), a backward sweep root to leaves.
 #pragma once
@@ -28,10 +29,13 @@
 namespace pp {
 
 constexpr int SMALL_NJ = 64;   // fronts up to this size are factorized in one workgroup's LDS
+constexpr int ASM_BLOCK = 16;  // parent columns per extend-add workgroup
 constexpr int NB = 32;         // pivot block of the blocked front factorization
 constexpr int PANEL_W = 32;    // widest sweep panel
-constexpr int SWEEP_ROWS = 256;  // rows of X per sweep workgroup (one per thread)
 constexpr int NCLASS = 6;      // sweep width classes 1, 2, 4, 8, 16, 32
+constexpr int TRSM_ROWS = 256;   // rows per forward-solve workgroup (one per thread)
+constexpr int TILE_ROWS = 64;    // rows per scatter / backward workgroup (one per lane, 4 waves)
+constexpr int SCATTER_T = 128;   // extension columns per scatter workgroup
 
 inline int width_class(int w) {
     int c = 0;
@@ -54,12 +58,13 @@ struct FactorPlan {
         i64 schur_off, schur_cnt;    // (front, ti, tj) triples in stask
     };
     struct Level {
-        i64 asm_off, asm_cnt;        // fronts with children, in flist
+        i64 asm_off, asm_cnt;        // extend-add tasks (front, first parent column) in atask
         i64 small_off, small_cnt;    // fronts with nj <= SMALL_NJ, in flist
         std::vector<Step> steps;     // blocked steps for the large fronts
     };
     std::vector<Level> levels;
     std::vector<int32_t> flist;      // front lists of all levels
+    std::vector<int32_t> atask;      // (front, first column) per extend-add task: 2 ints
     std::vector<int32_t> ftask;      // (front, step offset, chunk) per panel task: 3 ints
     std::vector<int32_t> stask;      // (front, step offset, ti, tj) per Schur task: 4 ints
     i64 max_nj = 0;
@@ -68,7 +73,7 @@ struct FactorPlan {
 struct SweepPlan {
     i64 np = 0;
     // per panel
-    std::vector<int32_t> front, c0, w, e, lo_ext;
+    std::vector<int32_t> front, c0, w, e, lo_ext, chunks;   // chunks: ceil(e / SCATTER_T), at least 1
     std::vector<i64> eoff, poff, doff;
     std::vector<int32_t> rowA_lo, rowA_hi, rowB_lo, rowB_hi;   // rows of the star sweeps
     std::vector<int32_t> Eidx;       // extension column indices (permuted labels)
@@ -76,11 +81,13 @@ struct SweepPlan {
     struct List {
         int cls;                     // width class
         i64 off, cnt;                // panel ids in plist
-        i64 tA_off, tB_off;          // tile prefix sums (cnt + 1 each) for the star's row ranges
+        // offsets into `tiles` of per-panel prefix sums (cnt + 1 entries each): forward-solve tiles and scatter
+        // units (tiles x chunks) over the star's forward rows, backward tiles over its backward rows, chunks
+        i64 pA256, pAu, pB64, pC;
     };
     std::vector<List> fwd, bwd;      // in execution order
     std::vector<int32_t> plist;
-    std::vector<int32_t> tiles;      // prefix sums of row tiles, per list: star forward / star backward
+    std::vector<int32_t> tiles;      // the prefix sums of all lists
     i64 max_e = 0;
 };
 
@@ -92,15 +99,16 @@ struct DevPlan {
     // factor
     int32_t *nn = nullptr, *na = nullptr, *nj = nullptr, *relpos = nullptr, *chptr = nullptr, *chidx = nullptr;
     i64 *Foff = nullptr, *Sptr = nullptr, *entry_pos = nullptr;
-    int32_t *flist = nullptr, *ftask = nullptr, *stask = nullptr;
+    int32_t *flist = nullptr, *ftask = nullptr, *stask = nullptr, *atask = nullptr;
     i64 *Dptr = nullptr, *Lptr = nullptr, *Rptr = nullptr;
     // sweeps
-    int32_t *p_front = nullptr, *p_c0 = nullptr, *p_w = nullptr, *p_e = nullptr, *p_lo = nullptr;
+    int32_t *p_front = nullptr, *p_c0 = nullptr, *p_w = nullptr, *p_e = nullptr, *p_lo = nullptr, *p_chunks = nullptr;
     i64 *p_eoff = nullptr, *p_poff = nullptr, *p_doff = nullptr;
     int32_t *p_rowA_lo = nullptr, *p_rowA_hi = nullptr, *p_rowB_lo = nullptr, *p_rowB_hi = nullptr;
     int32_t *Eidx = nullptr, *plist = nullptr, *tiles = nullptr;
     // permutation
     i64 *perm = nullptr, *invp = nullptr;
+    int32_t *invp32 = nullptr;
     std::vector<void *> owned;
 };
 

@@ -61,25 +61,38 @@ template <class S> __global__ void k_identity(typename S::value_type *__restrict
 }
 
 // ===== extend-add: F_f <- F_f (+) inj M_c inj^T for every child c (sgetrf_send!, chordal/sgetrf.jl:257-290) =====
-
+//
+// One workgroup per (parent front, block of ASM_BLOCK parent columns).  A child's map into its parent's bag (relpos)
+// is increasing, so the child columns landing in the block are a contiguous range found by binary search; blocks of
+// one parent never write the same entry, and the children of a parent are added one after another.
 template <class S>
 __global__ __launch_bounds__(NT) void k_assemble(typename S::value_type *__restrict__ F, const i64 *__restrict__ Foff,
                                                  const int32_t *__restrict__ nn, const int32_t *__restrict__ na,
                                                  const int32_t *__restrict__ nj, const i64 *__restrict__ Sptr,
                                                  const int32_t *__restrict__ relpos, const int32_t *__restrict__ chptr,
-                                                 const int32_t *__restrict__ chidx, const int32_t *__restrict__ list) {
+                                                 const int32_t *__restrict__ chidx, const int32_t *__restrict__ tasks) {
     typedef typename S::value_type T;
-    const int f = list[blockIdx.x];
-    T *Ff = F + Foff[f];
+    const int f = tasks[2 * blockIdx.x], a = tasks[2 * blockIdx.x + 1];
     const int ldf = nj[f];
+    const int b = min(ldf, a + ASM_BLOCK);
+    T *Ff = F + Foff[f];
     for (int q = chptr[f]; q < chptr[f + 1]; q++) {
         const int c = chidx[q];
         const int nc = na[c], ldc = nj[c], off = nn[c];
         const T *M = F + Foff[c] + off + (i64)off * ldc;
         const int32_t *rp = relpos + Sptr[c];
-        const int cnt = nc * nc;
+        // child columns w with a <= rp[w] < b
+        int lo = 0, hi = nc;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (rp[mid] < a) lo = mid + 1;
+            else hi = mid;
+        }
+        int w1 = lo;
+        while (w1 < nc && rp[w1] < b) w1++;
+        const int w0 = lo, cnt = (w1 - w0) * nc;
         for (int e = threadIdx.x; e < cnt; e += NT) {
-            const int v = e % nc, w = e / nc;
+            const int v = e % nc, w = w0 + e / nc;
             T *dst = Ff + rp[v] + (i64)rp[w] * ldf;
             *dst = S::plus(*dst, M[v + (i64)w * ldc]);
         }
@@ -289,40 +302,70 @@ __global__ __launch_bounds__(NT) void k_extract_ref(const T *__restrict__ F, con
     }
 }
 
-// Dpack / Upack / Lpack of every panel, one workgroup per panel
-template <class T>
-__global__ __launch_bounds__(NT) void k_build_packs(const T *__restrict__ F, const i64 *__restrict__ Foff,
+// Dpack (Wc x Wc) / Upack / Lpack (e x Wc) of every panel, Wc = the panel's width class; padding holds the semiring
+// zero.  One workgroup per panel.
+template <class S>
+__global__ __launch_bounds__(NT) void k_build_packs(const typename S::value_type *__restrict__ F, const i64 *__restrict__ Foff,
                                                    const int32_t *__restrict__ nj, const i64 *__restrict__ Rptr,
                                                    const int32_t *__restrict__ p_front, const int32_t *__restrict__ p_c0,
                                                    const int32_t *__restrict__ p_w, const int32_t *__restrict__ p_e,
                                                    const int32_t *__restrict__ p_lo, const i64 *__restrict__ p_poff,
-                                                   const i64 *__restrict__ p_doff, T *__restrict__ Dpack,
-                                                   T *__restrict__ Upack, T *__restrict__ Lpack) {
+                                                   const i64 *__restrict__ p_doff, typename S::value_type *__restrict__ Dpack,
+                                                   typename S::value_type *__restrict__ Upack,
+                                                   typename S::value_type *__restrict__ Lpack) {
+    typedef typename S::value_type T;
     const int p = blockIdx.x;
     const int f = p_front[p], w = p_w[p], e = p_e[p], lo = p_lo[p];
+    int Wc = 1;
+    while (Wc < w) Wc <<= 1;
     const int n = nj[f];
     const int lj0 = p_c0[p] - (int)Rptr[f];
     const T *G = F + Foff[f];
-    for (int q = threadIdx.x; q < w * w; q += NT) {
-        const int i = q % w, j = q / w;
-        Dpack[p_doff[p] + q] = G[(lj0 + i) + (i64)(lj0 + j) * n];
+    for (int q = threadIdx.x; q < Wc * Wc; q += NT) {
+        const int i = q % Wc, j = q / Wc;
+        Dpack[p_doff[p] + q] = (i < w && j < w) ? G[(lj0 + i) + (i64)(lj0 + j) * n] : S::zero();
     }
-    for (int q = threadIdx.x; q < w * e; q += NT) {
-        const int j = q % w, t = q / w;   // element (j, t) at t*w + j
-        Upack[p_poff[p] + q] = G[(lj0 + j) + (i64)(lo + t) * n];
-        Lpack[p_poff[p] + q] = G[(lo + t) + (i64)(lj0 + j) * n];
+    for (int q = threadIdx.x; q < Wc * e; q += NT) {
+        const int j = q % Wc, t = q / Wc;   // element (j, t) at t*Wc + j
+        Upack[p_poff[p] + q] = j < w ? G[(lj0 + j) + (i64)(lo + t) * n] : S::zero();
+        Lpack[p_poff[p] + q] = j < w ? G[(lo + t) + (i64)(lj0 + j) * n] : S::zero();
     }
 }
 
 // ===== sweeps over the rows of X (X column-major, ld rows) =====
 //
 // Forward (leaves to root), one panel with columns c_0..c_{w-1}:
-//   x_j <- (x_j (+) sum_{i<j} x_i (x) D(i,j)) (x) star(D(j,j))?,   then   X[:, E_t] <- X[:, E_t] (+) sum_j x_j (x) P(j,t)
+//   x_j <- (x_j (+) sum_{i<j} x_i (x) D(i,j)) (x) star(D(j,j))?          (k_fwd_trsm)
+//   X[:, E_t] <- X[:, E_t] (+) sum_j x_j (x) P(j,t)                        (k_fwd_scatter)
 // Backward (root to leaves):
 //   x_j <- x_j (+) sum_t X[:, E_t] (x) Q(t,j),   then   x_j <- (x_j (+) sum_{i>j} x_i (x) D(i,j)) (x) star(D(j,j))?
-// DMODE 0 reads the panel block as stored (U upper for forward with star, L strict lower for backward, unit);
-// DMODE 1 reads it transposed (L^T for forward, unit; U^T for backward with star), which is how lmul! runs on the
-// transposed right-hand sides.  One thread per row; the column indices and pack values are wave-uniform.
+// DMODE 0 reads the panel block as stored (U upper with star for forward, L strict lower unit for backward);
+// DMODE 1 reads it transposed (L^T unit for forward, U^T with star for backward): lmul! runs on B^T.
+// A panel of width w runs in the kernel of its width class W (power of two >= w); its packs are padded to W columns
+// with the semiring zero, so every inner loop runs over W without branches (a zero term changes nothing).
+// The column indices and pack values are wave-uniform (scalar loads); X is read and written one row per lane, so
+// each gathered column is a coalesced 256-byte wave access.
+
+struct SweepArgs {
+    const int32_t *plist;            // the list's panel ids
+    const int32_t *pre;              // per-panel prefix of work units over each panel's own rows (null: rows [0, nrows))
+    const int32_t *cpre;             // per-panel prefix of target chunks (k_fwd_scatter, rows [0, nrows))
+    int32_t np, nrows;
+    const int32_t *p_c0, *p_w, *p_e, *p_chunks, *row_lo, *row_hi;
+    const i64 *p_eoff, *p_poff, *p_doff;
+    const int32_t *Eidx;
+};
+
+// largest i in [0, np) with pre[i] <= u
+__device__ inline int search(const int32_t *pre, int np, int u) {
+    int lo = 0, hi = np;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (pre[mid] <= u) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
 
 // X[addr] <- X[addr] (+) v by compare-and-swap on the bit pattern; returns at once when (+) leaves the value
 // unchanged (the common case for min / max / or).  Exact and order-independent for the idempotent semirings.
@@ -341,101 +384,81 @@ template <class S> __device__ inline void atomic_plus(typename S::value_type *ad
     }
 }
 
-struct SweepArgs {
-    const int32_t *plist, *tiles;   // tiles: prefix sums of row tiles (null: uniform [0, nrows))
-    int32_t np, nrows;
-    const int32_t *p_c0, *p_w, *p_e, *row_lo, *row_hi;
-    const i64 *p_eoff, *p_poff, *p_doff;
-    const int32_t *Eidx;
-};
-
-__device__ inline void locate(const SweepArgs &a, int &pi, int &tile) {
-    const int bid = blockIdx.x;
-    if (a.tiles) {
-        int lo = 0, hi = a.np;   // largest lo with tiles[lo] <= bid
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (a.tiles[mid] <= bid) lo = mid;
-            else hi = mid;
-        }
-        pi = lo;
-        tile = bid - a.tiles[lo];
-    } else {
-        pi = bid % a.np;
-        tile = bid / a.np;
-    }
-}
-
-template <class S, int W, int DMODE, bool ATOMIC>
-__global__ __launch_bounds__(NT) void k_sweep_fwd(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
-                                                  const typename S::value_type *__restrict__ Dpack,
-                                                  const typename S::value_type *__restrict__ P) {
+template <class S, int W, int DMODE>
+__global__ __launch_bounds__(NT) void k_fwd_trsm(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
+                                                 const typename S::value_type *__restrict__ Dpack) {
     typedef typename S::value_type T;
     int pi, tile;
-    locate(a, pi, tile);
+    if (a.pre) {
+        pi = search(a.pre, a.np, blockIdx.x);
+        tile = blockIdx.x - a.pre[pi];
+    } else {
+        pi = blockIdx.x % a.np;
+        tile = blockIdx.x / a.np;
+    }
     const int p = a.plist[pi];
-    const int lo = a.tiles ? a.row_lo[p] : 0, hi = a.tiles ? a.row_hi[p] : a.nrows;
-    const int r = lo + tile * NT + threadIdx.x;
+    const int lo = a.pre ? a.row_lo[p] : 0, hi = a.pre ? a.row_hi[p] : a.nrows;
+    const int r = lo + tile * TRSM_ROWS + threadIdx.x;
     if (r >= hi) return;
-    const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
+    const int w = a.p_w[p], c0 = a.p_c0[p];
     const T *D = Dpack + a.p_doff[p];
-    const T *Pp = P + a.p_poff[p];
-    const int32_t *E = a.Eidx + a.p_eoff[p];
     T x[W];
 #pragma unroll
-    for (int j = 0; j < W; j++)
-        if (j < w) x[j] = X[(i64)(c0 + j) * ld + r];
+    for (int j = 0; j < W; j++) x[j] = j < w ? X[(i64)(c0 + j) * ld + r] : S::zero();
 #pragma unroll
     for (int j = 0; j < W; j++) {
-        if (j < w) {
-            T acc = x[j];
+        T acc = x[j];
 #pragma unroll
-            for (int i = 0; i < j; i++) acc = S::muladd(x[i], DMODE == 0 ? D[i + j * w] : D[j + i * w], acc);
-            if (DMODE == 0 && !S::integral) acc = S::prod(acc, S::star(D[j + j * w]));
-            x[j] = acc;
-        }
+        for (int i = 0; i < j; i++) acc = S::muladd(x[i], DMODE == 0 ? D[i + j * W] : D[j + i * W], acc);
+        if (DMODE == 0 && !S::integral) acc = S::prod(acc, S::star(D[j + j * W]));
+        x[j] = acc;
     }
 #pragma unroll
     for (int j = 0; j < W; j++)
         if (j < w) X[(i64)(c0 + j) * ld + r] = x[j];
-    if (ATOMIC) {
-        // several panels of one level may target the same columns of the same rows (solves): (+) atomically
-        for (int t = 0; t < e; t++) {
-            const T *q = Pp + (i64)t * w;
-            T v = S::zero();
+}
+
+template <class S, int W, bool ATOMIC>
+__global__ __launch_bounds__(NT) void k_fwd_scatter(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
+                                                    const typename S::value_type *__restrict__ P) {
+    typedef typename S::value_type T;
+    int pi, tile, chunk;
+    if (a.pre) {
+        pi = search(a.pre, a.np, blockIdx.x);
+        const int u = blockIdx.x - a.pre[pi];
+        const int nc = a.p_chunks[a.plist[pi]];
+        tile = u / nc;
+        chunk = u - tile * nc;
+    } else {
+        const int total = a.cpre[a.np];
+        tile = blockIdx.x / total;
+        const int u = blockIdx.x - tile * total;
+        pi = search(a.cpre, a.np, u);
+        chunk = u - a.cpre[pi];
+    }
+    const int p = a.plist[pi];
+    const int lo = a.pre ? a.row_lo[p] : 0, hi = a.pre ? a.row_hi[p] : a.nrows;
+    const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+    const int r = lo + tile * TILE_ROWS + lane;
+    if (r >= hi) return;
+    const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
+    const T *Pp = P + a.p_poff[p];
+    const int32_t *E = a.Eidx + a.p_eoff[p];
+    T x[W];
 #pragma unroll
-            for (int j = 0; j < W; j++)
-                if (j < w) v = S::muladd(x[j], q[j], v);
-            atomic_plus<S>(X + (i64)E[t] * ld + r, v);
+    for (int j = 0; j < W; j++) x[j] = j < w ? X[(i64)(c0 + j) * ld + r] : S::zero();
+    const int t1 = min(e, (chunk + 1) * SCATTER_T);
+    for (int t = chunk * SCATTER_T + q; t < t1; t += 4) {
+        const T *pc = Pp + (i64)t * W;
+        T v = ATOMIC ? S::zero() : X[(i64)E[t] * ld + r];
+        if (W == 1) {
+            v = S::muladd(x[0], pc[0], v);
+        } else {
+#pragma unroll
+            for (int j = 0; j < W; j += 2) v = S::muladd2(x[j], pc[j], x[j + 1], pc[j + 1], v);
         }
-        return;
-    }
-    int t = 0;
-    for (; t + 4 <= e; t += 4) {
-        T *y0 = X + (i64)E[t] * ld, *y1 = X + (i64)E[t + 1] * ld, *y2 = X + (i64)E[t + 2] * ld, *y3 = X + (i64)E[t + 3] * ld;
-        T v0 = y0[r], v1 = y1[r], v2 = y2[r], v3 = y3[r];
-        const T *q = Pp + (i64)t * w;
-#pragma unroll
-        for (int j = 0; j < W; j++)
-            if (j < w) {
-                v0 = S::muladd(x[j], q[j], v0);
-                v1 = S::muladd(x[j], q[w + j], v1);
-                v2 = S::muladd(x[j], q[2 * w + j], v2);
-                v3 = S::muladd(x[j], q[3 * w + j], v3);
-            }
-        y0[r] = v0;
-        y1[r] = v1;
-        y2[r] = v2;
-        y3[r] = v3;
-    }
-    for (; t < e; t++) {
-        T *y = X + (i64)E[t] * ld;
-        T v = y[r];
-        const T *q = Pp + (i64)t * w;
-#pragma unroll
-        for (int j = 0; j < W; j++)
-            if (j < w) v = S::muladd(x[j], q[j], v);
-        y[r] = v;
+        if (ATOMIC) atomic_plus<S>(X + (i64)E[t] * ld + r, v);
+        else X[(i64)E[t] * ld + r] = v;
     }
 }
 
@@ -444,53 +467,61 @@ __global__ __launch_bounds__(NT) void k_sweep_bwd(typename S::value_type *__rest
                                                   const typename S::value_type *__restrict__ Dpack,
                                                   const typename S::value_type *__restrict__ Q) {
     typedef typename S::value_type T;
+    __shared__ T red[3][W][TILE_ROWS];
     int pi, tile;
-    locate(a, pi, tile);
+    if (a.pre) {
+        pi = search(a.pre, a.np, blockIdx.x);
+        tile = blockIdx.x - a.pre[pi];
+    } else {
+        pi = blockIdx.x % a.np;
+        tile = blockIdx.x / a.np;
+    }
     const int p = a.plist[pi];
-    const int lo = a.tiles ? a.row_lo[p] : 0, hi = a.tiles ? a.row_hi[p] : a.nrows;
-    const int r = lo + tile * NT + threadIdx.x;
-    if (r >= hi) return;
+    const int lo = a.pre ? a.row_lo[p] : 0, hi = a.pre ? a.row_hi[p] : a.nrows;
+    const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+    const int r = lo + tile * TILE_ROWS + lane;
+    const bool valid = r < hi;
     const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
-    const T *D = Dpack + a.p_doff[p];
     const T *Qp = Q + a.p_poff[p];
     const int32_t *E = a.Eidx + a.p_eoff[p];
     T acc[W];
 #pragma unroll
-    for (int j = 0; j < W; j++)
-        if (j < w) acc[j] = X[(i64)(c0 + j) * ld + r];
-    int t = 0;
-    for (; t + 4 <= e; t += 4) {
-        const T v0 = X[(i64)E[t] * ld + r], v1 = X[(i64)E[t + 1] * ld + r], v2 = X[(i64)E[t + 2] * ld + r],
-                v3 = X[(i64)E[t + 3] * ld + r];
-        const T *q = Qp + (i64)t * w;
+    for (int j = 0; j < W; j++) acc[j] = (q == 0 && j < w && valid) ? X[(i64)(c0 + j) * ld + r] : S::zero();
+    // this wave's quarter of the gather list
+    const int k0 = (e * q) >> 2, k1 = (e * (q + 1)) >> 2;
+    if (valid) {
+        int k = k0;
+        for (; k + 2 <= k1; k += 2) {
+            const T v0 = X[(i64)E[k] * ld + r], v1 = X[(i64)E[k + 1] * ld + r];
+            const T *q0 = Qp + (i64)k * W, *q1 = q0 + W;
 #pragma unroll
-        for (int j = 0; j < W; j++)
-            if (j < w) {
-                T s = acc[j];
-                s = S::muladd(v0, q[j], s);
-                s = S::muladd(v1, q[w + j], s);
-                s = S::muladd(v2, q[2 * w + j], s);
-                s = S::muladd(v3, q[3 * w + j], s);
-                acc[j] = s;
-            }
-    }
-    for (; t < e; t++) {
-        const T v = X[(i64)E[t] * ld + r];
-        const T *q = Qp + (i64)t * w;
+            for (int j = 0; j < W; j++) acc[j] = S::muladd2(v0, q0[j], v1, q1[j], acc[j]);
+        }
+        if (k < k1) {
+            const T v0 = X[(i64)E[k] * ld + r];
+            const T *q0 = Qp + (i64)k * W;
 #pragma unroll
-        for (int j = 0; j < W; j++)
-            if (j < w) acc[j] = S::muladd(v, q[j], acc[j]);
+            for (int j = 0; j < W; j++) acc[j] = S::muladd(v0, q0[j], acc[j]);
+        }
     }
+    if (q > 0) {
+#pragma unroll
+        for (int j = 0; j < W; j++) red[q - 1][j][lane] = acc[j];
+    }
+    __syncthreads();
+    if (q != 0 || !valid) return;
+#pragma unroll
+    for (int qq = 0; qq < 3; qq++)
+#pragma unroll
+        for (int j = 0; j < W; j++) acc[j] = S::plus(acc[j], red[qq][j][lane]);
+    const T *D = Dpack + a.p_doff[p];
 #pragma unroll
     for (int j = W - 1; j >= 0; j--) {
-        if (j < w) {
-            T s = acc[j];
+        T s = acc[j];
 #pragma unroll
-            for (int i = j + 1; i < W; i++)
-                if (i < w) s = S::muladd(acc[i], DMODE == 0 ? D[i + j * w] : D[j + i * w], s);
-            if (DMODE == 1 && !S::integral) s = S::prod(s, S::star(D[j + j * w]));
-            acc[j] = s;
-        }
+        for (int i = j + 1; i < W; i++) s = S::muladd(acc[i], DMODE == 0 ? D[i + j * W] : D[j + i * W], s);
+        if (DMODE == 1 && !S::integral) s = S::prod(s, S::star(D[j + j * W]));
+        acc[j] = s;
     }
 #pragma unroll
     for (int j = 0; j < W; j++)
@@ -507,6 +538,25 @@ __global__ __launch_bounds__(NT) void k_relabel(const T *__restrict__ X, i64 n, 
     const T *src = X + invp[j] * n;
     T *dst = C + j * ldc;
     for (i64 i = threadIdx.x; i < n; i += NT) dst[i] = src[invp[i]];
+}
+
+// The same with the source column staged in LDS (coalesced read, gather from LDS, coalesced write), for columns of
+// at most RELABEL_LDS bytes; persistent workgroups, one per CU.
+constexpr int RELABEL_LDS = 131072;
+constexpr int RELABEL_NT = 1024;
+
+template <class T>
+__global__ __launch_bounds__(RELABEL_NT) void k_relabel_lds(const T *__restrict__ X, i64 n, T *__restrict__ C, i64 ldc,
+                                                           const int32_t *__restrict__ invp) {
+    __shared__ T col[RELABEL_LDS / sizeof(T)];
+    for (i64 j = blockIdx.x; j < n; j += gridDim.x) {
+        const T *src = X + (i64)invp[j] * n;
+        for (i64 i = threadIdx.x; i < n; i += RELABEL_NT) col[i] = src[i];
+        __syncthreads();
+        T *dst = C + j * ldc;
+        for (i64 i = threadIdx.x; i < n; i += RELABEL_NT) dst[i] = col[invp[i]];
+        __syncthreads();
+    }
 }
 
 // rmul!: Y[:, invp[c]] = B[:, c] (dir 0) or B[:, c] = Y[:, invp[c]] (dir 1); B nrhs x n (ldb), Y nrhs x n (nrhs)
@@ -647,7 +697,7 @@ template <class S> struct FactorRun {
         for (const auto &L : P.levels) {
             if (L.asm_cnt)
                 k_assemble<S><<<(unsigned)L.asm_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.na, d.nj, d.Sptr, d.relpos, d.chptr,
-                                                                 d.chidx, d.flist + L.asm_off);
+                                                                 d.chidx, d.atask + 2 * L.asm_off);
             if (L.small_cnt)
                 k_front_small<S><<<(unsigned)L.small_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.flist + L.small_off);
             for (const auto &s : L.steps) {
@@ -663,7 +713,7 @@ template <class S> struct FactorRun {
             k_extract_ref<T><<<(unsigned)nf, NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.Dptr, d.Lptr, (T *)fac->LD,
                                                           (T *)fac->LL, (T *)fac->UL);
         if (W.np > 0)
-            k_build_packs<T><<<(unsigned)W.np, NT, 0, st>>>(F, d.Foff, d.nj, d.Rptr, d.p_front, d.p_c0, d.p_w, d.p_e,
+            k_build_packs<S><<<(unsigned)W.np, NT, 0, st>>>(F, d.Foff, d.nj, d.Rptr, d.p_front, d.p_c0, d.p_w, d.p_e,
                                                             d.p_lo, d.p_poff, d.p_doff, (T *)fac->Dpack,
                                                             (T *)fac->Upack, (T *)fac->Lpack);
         LAUNCHCHK();
@@ -674,68 +724,91 @@ template <class S> struct FactorRun {
 };
 
 template <class S, int W>
-static void launch_sweep(bool fwd, int dmode, bool atomic, typename S::value_type *X, i64 ld, const SweepArgs &a,
-                         unsigned grid, const void *Dpack, const void *pack, hipStream_t st) {
+static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type *X, i64 ld, const SweepArgs &base,
+                        const SweepPlan &Wp, const SweepPlan::List &li, bool star_rows, i64 nrows, const void *Dpack,
+                        const void *pack, hipStream_t st) {
     typedef typename S::value_type T;
     const T *D = (const T *)Dpack, *Pk = (const T *)pack;
+    const int32_t *tiles = base.pre;   // device copy of Wp.tiles
+    SweepArgs a = base;
     if (fwd) {
-        if (atomic) {
-            if (dmode == 0) k_sweep_fwd<S, W, 0, true><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
-            else k_sweep_fwd<S, W, 1, true><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+        // triangular solves of the panels' own columns
+        unsigned grid;
+        if (star_rows) {
+            a.pre = tiles + li.pA256;
+            grid = (unsigned)Wp.tiles[li.pA256 + li.cnt];
         } else {
-            if (dmode == 0) k_sweep_fwd<S, W, 0, false><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
-            else k_sweep_fwd<S, W, 1, false><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+            a.pre = nullptr;
+            grid = (unsigned)(li.cnt * ((nrows + TRSM_ROWS - 1) / TRSM_ROWS));
+        }
+        if (grid) {
+            if (dmode == 0) k_fwd_trsm<S, W, 0><<<grid, NT, 0, st>>>(X, ld, a, D);
+            else k_fwd_trsm<S, W, 1><<<grid, NT, 0, st>>>(X, ld, a, D);
+        }
+        // scatter into the extension columns
+        a.cpre = tiles + li.pC;
+        if (star_rows) {
+            a.pre = tiles + li.pAu;
+            grid = (unsigned)Wp.tiles[li.pAu + li.cnt];
+        } else {
+            a.pre = nullptr;
+            grid = (unsigned)(((nrows + TILE_ROWS - 1) / TILE_ROWS) * Wp.tiles[li.pC + li.cnt]);
+        }
+        if (grid) {
+            if (atomic) k_fwd_scatter<S, W, true><<<grid, NT, 0, st>>>(X, ld, a, Pk);
+            else k_fwd_scatter<S, W, false><<<grid, NT, 0, st>>>(X, ld, a, Pk);
         }
     } else {
-        if (dmode == 0) k_sweep_bwd<S, W, 0><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
-        else k_sweep_bwd<S, W, 1><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+        unsigned grid;
+        if (star_rows) {
+            a.pre = tiles + li.pB64;
+            grid = (unsigned)Wp.tiles[li.pB64 + li.cnt];
+        } else {
+            a.pre = nullptr;
+            grid = (unsigned)(li.cnt * ((nrows + TILE_ROWS - 1) / TILE_ROWS));
+        }
+        if (grid) {
+            if (dmode == 0) k_sweep_bwd<S, W, 0><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+            else k_sweep_bwd<S, W, 1><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+        }
     }
 }
 
-// Run the forward or backward lists of the sweep plan over X.  star_rows: use each panel's own row range of the
-// star (tiles from the plan); otherwise rows [0, nrows) for every panel.
+// Run the forward or backward lists of the sweep plan over X.  star_rows: each panel's own row range of the star;
+// otherwise rows [0, nrows) for every panel (solves), where forward scatters of one level may meet: atomic.
 template <class S>
 static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmode, typename S::value_type *X, i64 ld,
                               bool star_rows, i64 nrows, const void *pack) {
-    const SweepPlan &W = *fac->sym->splan;
+    const SweepPlan &Wp = *fac->sym->splan;
     const DevPlan &d = fac->plan;
     hipStream_t st = ctx->stream;
-    const auto &lists = fwd ? W.fwd : W.bwd;
-    const i64 ntile = (nrows + NT - 1) / NT;
+    const auto &lists = fwd ? Wp.fwd : Wp.bwd;
+    if (nrows == 0) return "";
     for (const auto &li : lists) {
         SweepArgs a;
         a.plist = d.plist + li.off;
+        a.pre = d.tiles;   // base of the prefix arrays; launch_list offsets it
+        a.cpre = nullptr;
         a.np = (int32_t)li.cnt;
         a.nrows = (int32_t)nrows;
         a.p_c0 = d.p_c0;
         a.p_w = d.p_w;
         a.p_e = d.p_e;
+        a.p_chunks = d.p_chunks;
+        a.row_lo = fwd ? d.p_rowA_lo : d.p_rowB_lo;
+        a.row_hi = fwd ? d.p_rowA_hi : d.p_rowB_hi;
         a.p_eoff = d.p_eoff;
         a.p_poff = d.p_poff;
         a.p_doff = d.p_doff;
         a.Eidx = d.Eidx;
-        unsigned grid;
-        if (star_rows) {
-            const i64 toff = fwd ? li.tA_off : li.tB_off;
-            a.tiles = d.tiles + toff;
-            a.row_lo = fwd ? d.p_rowA_lo : d.p_rowB_lo;
-            a.row_hi = fwd ? d.p_rowA_hi : d.p_rowB_hi;
-            const i64 total = W.tiles[toff + li.cnt];
-            if (total == 0) continue;
-            grid = (unsigned)total;
-        } else {
-            a.tiles = nullptr;
-            a.row_lo = a.row_hi = nullptr;
-            if (ntile == 0) continue;
-            grid = (unsigned)(li.cnt * ntile);
-        }
+        const bool atomic = !star_rows;
         switch (li.cls) {
-        case 0: launch_sweep<S, 1>(fwd, dmode, !star_rows, X, ld, a, grid, fac->Dpack, pack, st); break;
-        case 1: launch_sweep<S, 2>(fwd, dmode, !star_rows, X, ld, a, grid, fac->Dpack, pack, st); break;
-        case 2: launch_sweep<S, 4>(fwd, dmode, !star_rows, X, ld, a, grid, fac->Dpack, pack, st); break;
-        case 3: launch_sweep<S, 8>(fwd, dmode, !star_rows, X, ld, a, grid, fac->Dpack, pack, st); break;
-        case 4: launch_sweep<S, 16>(fwd, dmode, !star_rows, X, ld, a, grid, fac->Dpack, pack, st); break;
-        default: launch_sweep<S, 32>(fwd, dmode, !star_rows, X, ld, a, grid, fac->Dpack, pack, st); break;
+        case 0: launch_list<S, 1>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
+        case 1: launch_list<S, 2>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
+        case 2: launch_list<S, 4>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
+        case 3: launch_list<S, 8>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
+        case 4: launch_list<S, 16>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
+        default: launch_list<S, 32>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
         }
         LAUNCHCHK();
     }
@@ -766,7 +839,13 @@ template <class S> struct StarRun {
         if (!e.empty()) return e;
         t2.stop();
         Timer t3(ctx, 3);
-        if (n > 0) k_relabel<T><<<(unsigned)n, NT, 0, st>>>(X, n, (T *)out, ldc, fac->plan.invp);
+        if (n > 0) {
+            if (n * (i64)sizeof(T) <= RELABEL_LDS)
+                k_relabel_lds<T><<<(unsigned)std::min<i64>(n, 512), RELABEL_NT, 0, st>>>(X, n, (T *)out, ldc,
+                                                                                         fac->plan.invp32);
+            else
+                k_relabel<T><<<(unsigned)n, NT, 0, st>>>(X, n, (T *)out, ldc, fac->plan.invp);
+        }
         LAUNCHCHK();
         t3.stop();
         HIPCHK(hipFreeAsync(X, st));

@@ -70,14 +70,19 @@ std::string build_factor_plan(const Symbolic &S, FactorPlan &P) {
     for (i64 f = 0; f < nf; f++) byh[h[f]].push_back((int32_t)f);
     P.levels.clear();
     P.flist.clear();
+    P.atask.clear();
     P.ftask.clear();
     P.stask.clear();
     for (i64 l = 0; l < H; l++) {
         FactorPlan::Level L;
-        L.asm_off = (i64)P.flist.size();
+        L.asm_off = (i64)P.atask.size() / 2;
         for (int32_t f : byh[l])
-            if (P.chptr[f + 1] > P.chptr[f]) P.flist.push_back(f);
-        L.asm_cnt = (i64)P.flist.size() - L.asm_off;
+            if (P.chptr[f + 1] > P.chptr[f])
+                for (int32_t a = 0; a < P.nj[f]; a += ASM_BLOCK) {
+                    P.atask.push_back(f);
+                    P.atask.push_back(a);
+                }
+        L.asm_cnt = (i64)P.atask.size() / 2 - L.asm_off;
         L.small_off = (i64)P.flist.size();
         for (int32_t f : byh[l])
             if (P.nj[f] <= SMALL_NJ) P.flist.push_back(f);
@@ -126,6 +131,7 @@ std::string build_sweep_plan(const Symbolic &S, const FactorPlan &F, SweepPlan &
     P.w.clear();
     P.e.clear();
     P.lo_ext.clear();
+    P.chunks.clear();
     P.eoff.clear();
     P.poff.clear();
     P.doff.clear();
@@ -146,13 +152,15 @@ std::string build_sweep_plan(const Symbolic &S, const FactorPlan &F, SweepPlan &
             P.w.push_back((int32_t)w);
             P.e.push_back((int32_t)e);
             P.lo_ext.push_back((int32_t)lo);
+            P.chunks.push_back((int32_t)std::max<i64>(1, (e + SCATTER_T - 1) / SCATTER_T));
+            const i64 Wc = (i64)1 << width_class((int)w);
             P.eoff.push_back((i64)P.Eidx.size());
             for (i64 v = c0 + w; v < Rp + nn; v++) P.Eidx.push_back((int32_t)v);
             for (i64 q = S.Sptr[f]; q < S.Sptr[f + 1]; q++) P.Eidx.push_back((int32_t)S.Stgt[q]);
             P.poff.push_back(P.npack);
-            P.npack += w * e;
+            P.npack += Wc * e;
             P.doff.push_back(P.ndpack);
-            P.ndpack += w * w;
+            P.ndpack += Wc * Wc;
             P.rowA_lo.push_back((int32_t)S.Rptr[S.fdsc[f]]);
             P.rowA_hi.push_back((int32_t)(c0 + w));
             P.rowB_lo.push_back((int32_t)S.Rptr[S.fdsc[root[f]]]);
@@ -189,20 +197,21 @@ std::string build_sweep_plan(const Symbolic &S, const FactorPlan &F, SweepPlan &
             li.off = (i64)P.plist.size();
             li.cnt = (i64)buckets[b].size();
             P.plist.insert(P.plist.end(), buckets[b].begin(), buckets[b].end());
-            li.tA_off = (i64)P.tiles.size();
-            int32_t acc = 0;
-            P.tiles.push_back(0);
-            for (int32_t p : buckets[b]) {
-                acc += (P.rowA_hi[p] - P.rowA_lo[p] + SWEEP_ROWS - 1) / SWEEP_ROWS;
-                P.tiles.push_back(acc);
-            }
-            li.tB_off = (i64)P.tiles.size();
-            acc = 0;
-            P.tiles.push_back(0);
-            for (int32_t p : buckets[b]) {
-                acc += (P.rowB_hi[p] - P.rowB_lo[p] + SWEEP_ROWS - 1) / SWEEP_ROWS;
-                P.tiles.push_back(acc);
-            }
+            auto prefix = [&](auto units) {
+                const i64 off = (i64)P.tiles.size();
+                int64_t acc = 0;
+                P.tiles.push_back(0);
+                for (int32_t p : buckets[b]) {
+                    acc += units(p);
+                    P.tiles.push_back((int32_t)acc);
+                }
+                return off;
+            };
+            auto tiles_of = [&](i64 lo, i64 hi, i64 rows) { return (hi - lo + rows - 1) / rows; };
+            li.pA256 = prefix([&](int32_t p) { return tiles_of(P.rowA_lo[p], P.rowA_hi[p], TRSM_ROWS); });
+            li.pAu = prefix([&](int32_t p) { return tiles_of(P.rowA_lo[p], P.rowA_hi[p], TILE_ROWS) * P.chunks[p]; });
+            li.pB64 = prefix([&](int32_t p) { return tiles_of(P.rowB_lo[p], P.rowB_hi[p], TILE_ROWS); });
+            li.pC = prefix([&](int32_t p) { return (i64)P.chunks[p]; });
             out.push_back(li);
         }
     };

@@ -7,6 +7,8 @@
 //   star      = tropical: one if a <= one in the semiring order else the top; PlusProd 1/(1-a); lattices one
 //               (tropical.jl:210-218, real.jl:50-58, bottleneck.jl:63-65, boolean.jl:65-67)
 //   integral  = lattices (MaxMin, MinMax, OrAnd): no star scaling in the LU and the solves (semiring.jl:478-492)
+//   muladd2   = plus(plus(a0 (x) b0, a1 (x) b1), c): two multiply-adds into one accumulator, which min/max
+//               semirings issue as v_add, v_add, v_min3 (1.5 VALU instructions per multiply-add)
 // min and max use the hardware v_min/v_max (IEEE minNum/maxNum, as the reference's GPU backend does with
 // llvm.minnum/maxnum, PATHPACKCUDAExt.jl:37-49): identical to ifelse(x < y, x, y) whenever the accumulator is not
 // NaN, which the factorization never produces, and apart from the sign of a zero when both operands are zeros of
@@ -41,6 +43,7 @@ template <class T> struct MinPlus {
     __host__ __device__ static T one() { return T(0); }
     __host__ __device__ static T plus(T a, T b) { return pmin(a, b); }
     __host__ __device__ static T muladd(T a, T b, T c) { return pmin(a + b, c); }
+    __host__ __device__ static T muladd2(T a0, T b0, T a1, T b1, T c) { return pmin(pmin(a0 + b0, a1 + b1), c); }
     __host__ __device__ static T prod(T a, T b) { T c = a + b; return c != c ? zero() : c; }
     __host__ __device__ static T star(T a) { return a >= T(0) ? one() : -Lim<T>::inf(); }
 };
@@ -53,6 +56,7 @@ template <class T> struct MaxPlus {
     __host__ __device__ static T one() { return T(0); }
     __host__ __device__ static T plus(T a, T b) { return pmax(a, b); }
     __host__ __device__ static T muladd(T a, T b, T c) { return pmax(a + b, c); }
+    __host__ __device__ static T muladd2(T a0, T b0, T a1, T b1, T c) { return pmax(pmax(a0 + b0, a1 + b1), c); }
     __host__ __device__ static T prod(T a, T b) { T c = a + b; return c != c ? zero() : c; }
     __host__ __device__ static T star(T a) { return a <= T(0) ? one() : Lim<T>::inf(); }
 };
@@ -65,6 +69,7 @@ template <class T> struct MaxMin {
     __host__ __device__ static T one() { return Lim<T>::inf(); }
     __host__ __device__ static T plus(T a, T b) { return pmax(a, b); }
     __host__ __device__ static T muladd(T a, T b, T c) { return pmax(pmin(a, b), c); }
+    __host__ __device__ static T muladd2(T a0, T b0, T a1, T b1, T c) { return pmax(pmax(pmin(a0, b0), pmin(a1, b1)), c); }
     __host__ __device__ static T prod(T a, T b) { return pmin(a, b); }
     __host__ __device__ static T star(T) { return one(); }
 };
@@ -77,6 +82,7 @@ template <class T> struct MinMax {
     __host__ __device__ static T one() { return -Lim<T>::inf(); }
     __host__ __device__ static T plus(T a, T b) { return pmin(a, b); }
     __host__ __device__ static T muladd(T a, T b, T c) { return pmin(pmax(a, b), c); }
+    __host__ __device__ static T muladd2(T a0, T b0, T a1, T b1, T c) { return pmin(pmin(pmax(a0, b0), pmax(a1, b1)), c); }
     __host__ __device__ static T prod(T a, T b) { return pmax(a, b); }
     __host__ __device__ static T star(T) { return one(); }
 };
@@ -89,6 +95,7 @@ template <class T> struct PlusProd {
     __host__ __device__ static T one() { return T(1); }
     __host__ __device__ static T plus(T a, T b) { return a + b; }
     __host__ __device__ static T muladd(T a, T b, T c) { return __builtin_fma(a, b, c); }
+    __host__ __device__ static T muladd2(T a0, T b0, T a1, T b1, T c) { return muladd(a1, b1, muladd(a0, b0, c)); }
     __host__ __device__ static T prod(T a, T b) { return a * b; }
     __host__ __device__ static T star(T a) { return a < T(1) ? T(1) / (T(1) - a) : Lim<T>::inf(); }
 };
@@ -104,6 +111,9 @@ struct OrAnd {
     __host__ __device__ static int32_t one() { return 0x7fffffff; }
     __host__ __device__ static int32_t plus(int32_t a, int32_t b) { return a | b; }
     __host__ __device__ static int32_t muladd(int32_t a, int32_t b, int32_t c) { return (a & b) | c; }
+    __host__ __device__ static int32_t muladd2(int32_t a0, int32_t b0, int32_t a1, int32_t b1, int32_t c) {
+        return (a0 & b0) | (a1 & b1) | c;
+    }
     __host__ __device__ static int32_t prod(int32_t a, int32_t b) { return a & b; }
     __host__ __device__ static int32_t star(int32_t) { return one(); }
 };

@@ -6,6 +6,8 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <numeric>
 
@@ -207,8 +209,9 @@ struct ND {
                 }
                 continue;
             }
-            // pseudo-peripheral root
-            for (int iter = 0; iter < 8; iter++) {
+            // pseudo-peripheral root: restart from a vertex of minimum degree in the last level while the level
+            // structure gets deeper; a structure as deep as the current one is kept as it is
+            for (int iter = 0; iter < 4; iter++) {
                 i32 best = -1;
                 i64 bd = 1LL << 60;
                 for (i64 k = lptr[nlev - 1]; k < lptr[nlev]; k++) {
@@ -220,10 +223,13 @@ struct ND {
                 std::vector<i64> lptr2;
                 i64 cnt2;
                 int nlev2 = bfs(id, best, cnt2, lptr2);
-                if (nlev2 > nlev) {
+                if (nlev2 >= nlev) {
+                    const bool deeper = nlev2 > nlev;
                     nlev = nlev2;
                     lptr = lptr2;
+                    cnt = cnt2;
                     root = best;
+                    if (!deeper) break;
                 } else {
                     clear_levels(cnt2);
                     nlev = bfs(id, root, cnt, lptr);
@@ -338,6 +344,76 @@ void etree_postorder(const Adj &G, const std::vector<i64> &perm, std::vector<i64
     }
 }
 
+// ===== column counts of L (Gilbert, Ng & Peyton, "An efficient algorithm to compute row and column counts for
+// sparse Cholesky factorization", SIMAX 1994) =====
+//
+// The labels are a postorder of the elimination tree.  L[i, j] != 0 iff j lies in the row subtree T_i, whose leaves
+// are among the j < i with A[i, j] != 0.  Every node counts +1; for each row subtree, each leaf j (a neighbour of i
+// that is not a descendant of the previous leaf) adds +1 at j and -1 at the least common ancestor of j and the
+// previous leaf (found with a disjoint-set forest over the nodes already visited); each leaf of the tree counts 1
+// and each non-root node subtracts 1 from its parent.  The column count of j (with the diagonal) is then the sum of
+// these weights over the subtree of j.  O(nnz(A) a(n)).
+void column_counts(const Adj &G, const std::vector<i64> &perm, std::vector<i64> &parent, std::vector<i64> &cc) {
+    const i64 n = G.n;
+    std::vector<i64> invp(n);
+    for (i64 k = 0; k < n; k++) invp[perm[k]] = k;
+    // elimination tree in the new labels
+    parent.assign(n, -1);
+    std::vector<i64> anc(n, -1);
+    for (i64 j = 0; j < n; j++) {
+        const i64 v = perm[j];
+        for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) {
+            i64 r = invp[G.adj[p]];
+            if (r >= j) continue;
+            while (anc[r] != -1 && anc[r] != j) {
+                const i64 t = anc[r];
+                anc[r] = j;
+                r = t;
+            }
+            if (anc[r] == -1) {
+                anc[r] = j;
+                parent[r] = j;
+            }
+        }
+    }
+    // first descendant of every node (labels are a postorder, so a subtree is the range [first[j], j])
+    std::vector<i64> first(n, -1);
+    for (i64 k = 0; k < n; k++)
+        for (i64 j = k; j != -1 && first[j] == -1; j = parent[j]) first[j] = k;
+    std::vector<i64> delta(n), maxfirst(n, -1), prevleaf(n, -1), set(n);
+    for (i64 j = 0; j < n; j++) {
+        set[j] = j;
+        delta[j] = first[j] == j ? 1 : 0;   // leaves of the elimination tree
+    }
+    for (i64 j = 0; j < n; j++) {
+        if (parent[j] != -1) delta[parent[j]]--;
+        const i64 v = perm[j];
+        for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) {
+            const i64 i = invp[G.adj[p]];
+            if (i <= j || first[j] <= maxfirst[i]) continue;   // j is no new leaf of the row subtree of i
+            maxfirst[i] = first[j];
+            const i64 jprev = prevleaf[i];
+            prevleaf[i] = j;
+            delta[j]++;
+            if (jprev != -1) {
+                // least common ancestor of jprev and j: the representative of jprev's set
+                i64 q = jprev;
+                while (set[q] != q) q = set[q];
+                for (i64 s = jprev; s != q;) {
+                    const i64 t = set[s];
+                    set[s] = q;
+                    s = t;
+                }
+                delta[q]--;
+            }
+        }
+        if (parent[j] != -1) set[j] = parent[j];
+    }
+    cc = delta;
+    for (i64 j = 0; j < n; j++)
+        if (parent[j] != -1) cc[parent[j]] += cc[j];
+}
+
 // ===== supernodal symbolic factorization for (perm, Rptr) =====
 //
 // sep(f) = (adj(res(f)) and the separators of f's children) restricted to vertices after res(f); parent(f) is the
@@ -394,6 +470,14 @@ double now() {
     return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
 }
 
+// PP_SYMTIME=1 prints the time of each stage of the analysis to stderr
+void stage(const char *name, double &t) {
+    static const bool on = std::getenv("PP_SYMTIME") != nullptr;
+    const double t1 = now();
+    if (on) std::fprintf(stderr, "pp_symbolic: %-28s %8.2f ms\n", name, (t1 - t) * 1e3);
+    t = t1;
+}
+
 // Work counts of a structure (the formulas of the reference's per-front costs): factor sum nn^3/3 + nn^2 na +
 // nn na^2; star n * sum nn (na + (nn-1)/2) for X <- X L* plus sum |subtree(f)| nn (na + (nn-1)/2) for X <- U*;
 // one right-hand side 2 sum nn (na + (nn-1)/2).
@@ -420,8 +504,10 @@ std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, st
                    std::vector<i64> Rptr, Symbolic &out) {
     std::vector<i64> Sptr, parent;
     std::vector<i32> Stgt;
+    double ts = now();
     std::string err = supernodal(G, perm, Rptr, Sptr, Stgt, parent);
     if (!err.empty()) return err;
+    stage("  separators", ts);
     const i64 nf = (i64)Rptr.size() - 1;
     out.n = n;
     out.perm = std::move(perm);
@@ -447,6 +533,7 @@ std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, st
     std::vector<i64> idx(n);
     for (i64 f = 0; f < nf; f++)
         for (i64 v = out.Rptr[f]; v < out.Rptr[f + 1]; v++) idx[v] = f;
+    stage("  copies", ts);
     out.nnz = colptr[n];
     out.entry_front.resize(out.nnz);
     out.entry_row.resize(out.nnz);
@@ -469,6 +556,7 @@ std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, st
             out.entry_row[p] = (i32)li;
             out.entry_col[p] = (i32)lj;
         }
+    stage("  entries", ts);
     work_counts(n, out.Rptr, out.Sptr, out.parent, out.madds_factor, out.madds_star, out.madds_rhs, out.nnzL);
     return "";
 }
@@ -524,34 +612,39 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
         }
     }
     out.seconds_order = now() - t0;
+    double ts = t0;
+    stage("symmetrize + order", ts);
     // 2. postordered elimination tree
     std::vector<i64> perm1;
     etree_postorder(G, perm0, perm1);
-    // 3. column structures, then fundamental supernodes
-    std::vector<i64> Rcol(n + 1);
-    std::iota(Rcol.begin(), Rcol.end(), 0);
-    std::vector<i64> Scol, pcol;
-    std::vector<i32> Tcol;
-    err = supernodal(G, perm1, Rcol, Scol, Tcol, pcol);
-    if (!err.empty()) return err;
-    std::vector<i32> Tfree;
-    Tcol.swap(Tfree);   // column structures are no longer needed: only counts and the tree
+    stage("etree + postorder", ts);
+    // 3. column counts, then fundamental supernodes: j + 1 continues j's supernode when it is j's parent, has no
+    //    other child, and its column holds exactly one entry fewer
+    std::vector<i64> pcol, ccol;
+    column_counts(G, perm1, pcol, ccol);
     std::vector<i64> nchild(n, 0);
     for (i64 j = 0; j < n; j++)
         if (pcol[j] >= 0) nchild[pcol[j]]++;
     std::vector<i64> R1;
     R1.push_back(0);
     for (i64 j = 1; j < n; j++) {
-        i64 ccp = Scol[j] - Scol[j - 1], ccj = Scol[j + 1] - Scol[j];
-        bool cont = pcol[j - 1] == j && nchild[j] == 1 && ccj == ccp - 1;
+        const bool cont = pcol[j - 1] == j && nchild[j] == 1 && ccol[j] == ccol[j - 1] - 1;
         if (!cont) R1.push_back(j);
     }
     R1.push_back(n);
-    std::vector<i64> S1, par1;
-    std::vector<i32> T1;
-    err = supernodal(G, perm1, R1, S1, T1, par1);
-    if (!err.empty()) return err;
+    stage("column counts + supernodes", ts);
+    // the fundamental supernodes' separator sizes and tree, from the counts: na = count(first column) - nn, and
+    // the parent holds the elimination-tree parent of the last column
     const i64 ns = (i64)R1.size() - 1;
+    std::vector<i64> S1(ns + 1, 0), par1(ns, -1), sidx(n);
+    for (i64 s = 0; s < ns; s++) {
+        for (i64 v = R1[s]; v < R1[s + 1]; v++) sidx[v] = s;
+        S1[s + 1] = S1[s] + (ccol[R1[s]] - (R1[s + 1] - R1[s]));
+    }
+    for (i64 s = 0; s < ns; s++) {
+        const i64 pj = pcol[R1[s + 1] - 1];
+        par1[s] = pj >= 0 ? sidx[pj] : -1;
+    }
     {
         double f, s, r, l;
         work_counts(n, R1, S1, par1, f, s, r, l);
@@ -646,7 +739,9 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
         }
     }
     if ((i64)perm2.size() != n) return "internal error: amalgamation lost vertices";
+    stage("amalgamation", ts);
     err = finish(G, n, colptr, rowval, perm2, R2, out);
+    stage("final structure + entries", ts);
     out.seconds_total = now() - t0;
     return err;
 }
