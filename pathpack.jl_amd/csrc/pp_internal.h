@@ -84,6 +84,8 @@ struct SweepPlan {
         // offsets into `tiles` of per-panel prefix sums (cnt + 1 entries each): forward-solve tiles and scatter
         // units (tiles x chunks) over the star's forward rows, backward tiles over its backward rows, chunks
         i64 pA256, pAu, pB64, pC;
+        bool uniB;                   // every panel of the list has the same backward rows [rowB_lo, rowB_hi)
+        int32_t rowB_lo, rowB_hi;
     };
     std::vector<List> fwd, bwd;      // in execution order
     std::vector<int32_t> plist;

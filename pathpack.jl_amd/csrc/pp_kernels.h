@@ -350,7 +350,7 @@ struct SweepArgs {
     const int32_t *plist;            // the list's panel ids
     const int32_t *pre;              // per-panel prefix of work units over each panel's own rows (null: rows [0, nrows))
     const int32_t *cpre;             // per-panel prefix of target chunks (k_fwd_scatter, rows [0, nrows))
-    int32_t np, nrows;
+    int32_t np, nrows, row_base;     // without a prefix: rows [row_base, row_base + nrows)
     const int32_t *p_c0, *p_w, *p_e, *p_chunks, *row_lo, *row_hi;
     const i64 *p_eoff, *p_poff, *p_doff;
     const int32_t *Eidx;
@@ -438,7 +438,8 @@ __global__ __launch_bounds__(NT) void k_fwd_scatter(typename S::value_type *__re
     }
     const int p = a.plist[pi];
     const int lo = a.pre ? a.row_lo[p] : 0, hi = a.pre ? a.row_hi[p] : a.nrows;
-    const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // the wave: uniform, so pack loads are scalar
     const int r = lo + tile * TILE_ROWS + lane;
     if (r >= hi) return;
     const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
@@ -462,23 +463,34 @@ __global__ __launch_bounds__(NT) void k_fwd_scatter(typename S::value_type *__re
     }
 }
 
-template <class S, int W, int DMODE>
-__global__ __launch_bounds__(NT) void k_sweep_bwd(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
-                                                  const typename S::value_type *__restrict__ Dpack,
-                                                  const typename S::value_type *__restrict__ Q) {
-    typedef typename S::value_type T;
-    __shared__ T red[3][W][TILE_ROWS];
-    int pi, tile;
+// Locate (panel, row tile) of a backward / solve workgroup.  With a prefix (star rows): panel-major over each
+// panel's own rows.  Without (one row range [row_base, row_base + nrows) for the whole list): XCD-aware tile-major
+// order -- workgroups are dealt to the 8 XCDs round-robin, so XCD x gets the tiles t = x mod 8, each with all panels
+// of the list, and the gathered columns of a row tile are reused from that XCD's L2.
+__device__ inline void locate_tile(const SweepArgs &a, int np, int &pi, int &tile) {
+    const int bid = blockIdx.x;
     if (a.pre) {
-        pi = search(a.pre, a.np, blockIdx.x);
-        tile = blockIdx.x - a.pre[pi];
+        pi = search(a.pre, np, bid);
+        tile = bid - a.pre[pi];
     } else {
-        pi = blockIdx.x % a.np;
-        tile = blockIdx.x / a.np;
+        const int xcd = bid & 7, local = bid >> 3;
+        tile = (local / np) * 8 + xcd;
+        pi = local - (local / np) * np;
     }
+}
+
+template <class S, int W, int DMODE, int KSPLIT>
+__global__ __launch_bounds__(64 * KSPLIT) void k_sweep_bwd(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
+                                                           const typename S::value_type *__restrict__ Dpack,
+                                                           const typename S::value_type *__restrict__ Q) {
+    typedef typename S::value_type T;
+    __shared__ T red[KSPLIT - 1][W][TILE_ROWS];
+    int pi, tile;
+    locate_tile(a, a.np, pi, tile);
     const int p = a.plist[pi];
-    const int lo = a.pre ? a.row_lo[p] : 0, hi = a.pre ? a.row_hi[p] : a.nrows;
-    const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+    const int lo = a.pre ? a.row_lo[p] : a.row_base, hi = a.pre ? a.row_hi[p] : a.row_base + a.nrows;
+    const int lane = threadIdx.x & 63;
+    const int q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // the wave: uniform, so pack loads are scalar
     const int r = lo + tile * TILE_ROWS + lane;
     const bool valid = r < hi;
     const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
@@ -487,17 +499,37 @@ __global__ __launch_bounds__(NT) void k_sweep_bwd(typename S::value_type *__rest
     T acc[W];
 #pragma unroll
     for (int j = 0; j < W; j++) acc[j] = (q == 0 && j < w && valid) ? X[(i64)(c0 + j) * ld + r] : S::zero();
-    // this wave's quarter of the gather list
-    const int k0 = (e * q) >> 2, k1 = (e * (q + 1)) >> 2;
+    // this wave's share of the gather list, four columns per step with the next four already in flight
+    const int k0 = (int)(((i64)e * q) / KSPLIT), k1 = (int)(((i64)e * (q + 1)) / KSPLIT);
     if (valid) {
         int k = k0;
-        for (; k + 2 <= k1; k += 2) {
-            const T v0 = X[(i64)E[k] * ld + r], v1 = X[(i64)E[k + 1] * ld + r];
-            const T *q0 = Qp + (i64)k * W, *q1 = q0 + W;
+        if (k + 4 <= k1) {
+            T v0 = X[(i64)E[k] * ld + r], v1 = X[(i64)E[k + 1] * ld + r], v2 = X[(i64)E[k + 2] * ld + r],
+              v3 = X[(i64)E[k + 3] * ld + r];
+            while (true) {
+                const bool more = k + 8 <= k1;
+                T n0 = v0, n1 = v1, n2 = v2, n3 = v3;
+                if (more) {
+                    n0 = X[(i64)E[k + 4] * ld + r];
+                    n1 = X[(i64)E[k + 5] * ld + r];
+                    n2 = X[(i64)E[k + 6] * ld + r];
+                    n3 = X[(i64)E[k + 7] * ld + r];
+                }
+                const T *q0 = Qp + (i64)k * W;
 #pragma unroll
-            for (int j = 0; j < W; j++) acc[j] = S::muladd2(v0, q0[j], v1, q1[j], acc[j]);
+                for (int j = 0; j < W; j++) {
+                    acc[j] = S::muladd2(v0, q0[j], v1, q0[W + j], acc[j]);
+                    acc[j] = S::muladd2(v2, q0[2 * W + j], v3, q0[3 * W + j], acc[j]);
+                }
+                k += 4;
+                if (!more) break;
+                v0 = n0;
+                v1 = n1;
+                v2 = n2;
+                v3 = n3;
+            }
         }
-        if (k < k1) {
+        for (; k < k1; k++) {
             const T v0 = X[(i64)E[k] * ld + r];
             const T *q0 = Qp + (i64)k * W;
 #pragma unroll
@@ -511,7 +543,7 @@ __global__ __launch_bounds__(NT) void k_sweep_bwd(typename S::value_type *__rest
     __syncthreads();
     if (q != 0 || !valid) return;
 #pragma unroll
-    for (int qq = 0; qq < 3; qq++)
+    for (int qq = 0; qq < KSPLIT - 1; qq++)
 #pragma unroll
         for (int j = 0; j < W; j++) acc[j] = S::plus(acc[j], red[qq][j][lane]);
     const T *D = Dpack + a.p_doff[p];
@@ -760,16 +792,30 @@ static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type
         }
     } else {
         unsigned grid;
-        if (star_rows) {
+        i64 ntile = 0;
+        if (star_rows && !li.uniB) {
             a.pre = tiles + li.pB64;
             grid = (unsigned)Wp.tiles[li.pB64 + li.cnt];
+            ntile = grid / std::max<i64>(1, li.cnt);
         } else {
             a.pre = nullptr;
-            grid = (unsigned)(li.cnt * ((nrows + TILE_ROWS - 1) / TILE_ROWS));
+            if (star_rows) {
+                a.row_base = li.rowB_lo;
+                a.nrows = li.rowB_hi - li.rowB_lo;
+            }
+            ntile = (a.nrows + TILE_ROWS - 1) / TILE_ROWS;
+            grid = (unsigned)(li.cnt * ((ntile + 7) / 8) * 8);
         }
+        // few workgroups for the whole chip: split each row tile's gather list over eight waves instead of four
+        const bool wide = li.cnt * ntile < 1024;
         if (grid) {
-            if (dmode == 0) k_sweep_bwd<S, W, 0><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
-            else k_sweep_bwd<S, W, 1><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+            if (wide) {
+                if (dmode == 0) k_sweep_bwd<S, W, 0, 8><<<grid, 512, 0, st>>>(X, ld, a, D, Pk);
+                else k_sweep_bwd<S, W, 1, 8><<<grid, 512, 0, st>>>(X, ld, a, D, Pk);
+            } else {
+                if (dmode == 0) k_sweep_bwd<S, W, 0, 4><<<grid, 256, 0, st>>>(X, ld, a, D, Pk);
+                else k_sweep_bwd<S, W, 1, 4><<<grid, 256, 0, st>>>(X, ld, a, D, Pk);
+            }
         }
     }
 }
@@ -791,6 +837,7 @@ static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmod
         a.cpre = nullptr;
         a.np = (int32_t)li.cnt;
         a.nrows = (int32_t)nrows;
+        a.row_base = 0;
         a.p_c0 = d.p_c0;
         a.p_w = d.p_w;
         a.p_e = d.p_e;

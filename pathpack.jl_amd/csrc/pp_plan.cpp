@@ -132,6 +132,10 @@ std::string build_sweep_plan(const Symbolic &S, const FactorPlan &F, SweepPlan &
     P.e.clear();
     P.lo_ext.clear();
     P.chunks.clear();
+    P.rowA_lo.clear();
+    P.rowA_hi.clear();
+    P.rowB_lo.clear();
+    P.rowB_hi.clear();
     P.eoff.clear();
     P.poff.clear();
     P.doff.clear();
@@ -212,6 +216,11 @@ std::string build_sweep_plan(const Symbolic &S, const FactorPlan &F, SweepPlan &
             li.pAu = prefix([&](int32_t p) { return tiles_of(P.rowA_lo[p], P.rowA_hi[p], TILE_ROWS) * P.chunks[p]; });
             li.pB64 = prefix([&](int32_t p) { return tiles_of(P.rowB_lo[p], P.rowB_hi[p], TILE_ROWS); });
             li.pC = prefix([&](int32_t p) { return (i64)P.chunks[p]; });
+            li.uniB = true;
+            li.rowB_lo = P.rowB_lo[buckets[b][0]];
+            li.rowB_hi = P.rowB_hi[buckets[b][0]];
+            for (int32_t p : buckets[b])
+                if (P.rowB_lo[p] != li.rowB_lo || P.rowB_hi[p] != li.rowB_hi) li.uniB = false;
             out.push_back(li);
         }
     };
