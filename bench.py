@@ -180,7 +180,21 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-timing", dest="timing", action="store_false")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MiB",
+                    help="only run the plain copy kernel (pp_copy) over this many MiB: the calibration of the memory "
+                         "counters FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        import ctypes
+
+        ctx = P.context(0)
+        nb = args.calibrate_copy << 20
+        src = P.DeviceArray((nb // 4,), np.float32)
+        dst = P.DeviceArray((nb // 4,), np.float32)
+        for _ in range(2):
+            ctx.check(P.lib().pp_copy(ctx.handle, ctypes.c_void_p(dst.ptr), ctypes.c_void_p(src.ptr), nb))
+        print(json.dumps({"calibrate_copy_bytes": nb, "launches": 2}))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU: the star's row blocks would shard across GPUs "
                                    "with a replicated factor, which this build does not implement"}))

@@ -124,7 +124,7 @@ pp_status pp_fac_destroy(pp_fac *fac);
 /* ===== star and solves (device) ===== */
 
 /* Matrix(F): the full star A* (n x n, column-major, ldc >= n, original labels) into `out`: a device pointer when
- * out_on_device != 0, else a host pointer (copied back through pinned staging).  Replaces sgetri!(F, C)
+ * out_on_device != 0, else a host pointer (the star is assembled in HBM, then copied back).  Replaces sgetri!(F, C)
  * (src/CPU/chordal_slu.jl:501-513 -> chordal/sgetri.jl:13-31, utils.jl:261-505). */
 pp_status pp_star(pp_ctx *ctx, const pp_fac *fac, void *out, int64_t ldc, int out_on_device);
 /* lmul!(F, B): B (n x nrhs, column-major, ldb >= n) <- A* B, the least solution of X = A X (+) B.
@@ -152,6 +152,9 @@ pp_status pp_buffer_alloc(pp_ctx *ctx, size_t bytes, void **dptr);
 pp_status pp_buffer_free(pp_ctx *ctx, void *dptr);
 pp_status pp_upload(pp_ctx *ctx, void *dst_device, const void *src_host, size_t bytes);
 pp_status pp_download(pp_ctx *ctx, void *dst_host, const void *src_device, size_t bytes);
+/* Device-to-device copy by a plain copy kernel on the context's stream (also the calibration kernel for memory
+ * counters).  Replaces nothing in the reference. */
+pp_status pp_copy(pp_ctx *ctx, void *dst_device, const void *src_device, size_t bytes);
 
 /* ===== measurement ===== */
 

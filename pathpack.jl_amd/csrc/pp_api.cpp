@@ -501,6 +501,15 @@ pp_status pp_download(pp_ctx *ctx, void *dst, const void *src, size_t bytes) {
     return PP_OK;
 }
 
+pp_status pp_copy(pp_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return fail(ctx, PP_EINVAL, "pp_copy: null argument");
+    CHECK_HIP(ctx, hipSetDevice(ctx->device));
+    std::string e = pp::device_copy(ctx, dst, src, bytes);
+    if (!e.empty()) return fail(ctx, PP_EHIP, "pp_copy: " + e);
+    CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return PP_OK;
+}
+
 pp_status pp_set_timing(pp_ctx *ctx, int on) {
     if (!ctx) return fail(nullptr, PP_EINVAL, "pp_set_timing: null context");
     ctx->timing = on;

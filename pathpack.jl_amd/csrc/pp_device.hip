@@ -2,6 +2,7 @@
 //
 // The kernels and drivers are templates (pp_kernels.h); each pair is instantiated in its own translation unit
 // (pp_inst_*.hip) so that they compile in parallel.
+#include <cstdint>
 #include <string>
 
 #include "pp_internal.h"
@@ -15,6 +16,25 @@ template <class S> std::string solve_impl(pp_ctx *ctx, const pp_fac *fac, void *
 template <class S>
 std::string gemm_impl(pp_ctx *ctx, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B, i64 ldb, void *C, i64 ldc);
 template <class S> std::string getrf_impl(pp_ctx *ctx, i64 nb, i64 batch, void *A, void *TL, void *TU);
+
+// plain copy, 16 bytes per thread per step (the memory-counter calibration kernel)
+__global__ __launch_bounds__(256) void k_copy16(uint4 *__restrict__ dst, const uint4 *__restrict__ src, i64 n16) {
+    for (i64 i = blockIdx.x * (i64)256 + threadIdx.x; i < n16; i += (i64)gridDim.x * 256) dst[i] = src[i];
+}
+
+__global__ __launch_bounds__(256) void k_copy1(unsigned char *__restrict__ dst, const unsigned char *__restrict__ src,
+                                               i64 n) {
+    for (i64 i = blockIdx.x * (i64)256 + threadIdx.x; i < n; i += (i64)gridDim.x * 256) dst[i] = src[i];
+}
+
+std::string device_copy(pp_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return "";
+    const bool aligned = ((uintptr_t)dst % 16 == 0) && ((uintptr_t)src % 16 == 0) && bytes % 16 == 0;
+    if (aligned) k_copy16<<<2048, 256, 0, ctx->stream>>>((uint4 *)dst, (const uint4 *)src, (i64)(bytes / 16));
+    else k_copy1<<<2048, 256, 0, ctx->stream>>>((unsigned char *)dst, (const unsigned char *)src, (i64)bytes);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? "" : std::string("kernel launch: ") + hipGetErrorString(e);
+}
 
 #define PP_DISPATCH(sr, dt, EXPR)                                        \
     do {                                                                 \

@@ -5,7 +5,11 @@
 #include "pp_symbolic.h"
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
+#include <condition_variable>
+#include <mutex>
+#include <thread>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -80,16 +84,17 @@ std::string symmetrize(i64 n, const i64 *colptr, const i64 *rowval, Adj &G) {
 struct ND {
     const Adj &G;
     int leaf;
-    std::vector<i32> part;
-    std::vector<i32> level, queue;
+    std::vector<i32> part;    // item id of every vertex (items own disjoint vertex sets)
+    std::vector<i32> level;   // BFS level, -1 outside a BFS (per vertex, so items can run concurrently)
     std::vector<i64> order;   // order[k] = vertex eliminated k-th
-    i32 next_id = 1;
+    std::atomic<i32> next_id{1};
+    struct Item { std::vector<i32> V; i64 hi; };
 
     ND(const Adj &g, int leaf_) : G(g), leaf(std::max(2, std::min(leaf_, 64))), part(g.n, 0), level(g.n, -1),
-                                   queue(g.n), order(g.n, -1) {}
+                                   order(g.n, -1) {}
 
     // BFS inside item id from root; returns the number of levels; fills queue[0..cnt) and level[]
-    int bfs(i32 id, i32 root, i64 &cnt, std::vector<i64> &lptr) {
+    int bfs(std::vector<i32> &queue, i32 id, i32 root, i64 &cnt, std::vector<i64> &lptr) {
         lptr.clear();
         cnt = 0;
         queue[cnt++] = root;
@@ -114,7 +119,7 @@ struct ND {
         return nlev;
     }
 
-    void clear_levels(i64 cnt) {
+    void clear_levels(const std::vector<i32> &queue, i64 cnt) {
         for (i64 k = 0; k < cnt; k++) level[queue[k]] = -1;
     }
 
@@ -153,8 +158,135 @@ struct ND {
         }
     }
 
-    void run() {
-        struct Item { std::vector<i32> V; i64 hi; };
+    // One item: split it (components, or sides + separator) or order it (leaf); new items go to `out`.
+    void process(Item &it, std::vector<i32> &queue, std::vector<i64> &lptr, std::vector<Item> &out) {
+        const i64 sz = (i64)it.V.size();
+        if (sz == 0) return;
+        const i32 id = next_id.fetch_add(1);
+        for (i32 v : it.V) part[v] = id;
+        const i64 lo = it.hi - sz;
+        if (sz <= leaf) {
+            md_leaf(it.V, lo);
+            return;
+        }
+        // connected components of the item
+        i64 cnt;
+        i32 root = it.V[0];
+        {
+            i64 bd = 1LL << 60;
+            for (i32 v : it.V) {
+                i64 d = degree_in(v, id);
+                if (d < bd) { bd = d; root = v; }
+            }
+        }
+        int nlev = bfs(queue, id, root, cnt, lptr);
+        if (cnt < sz) {
+            // disconnected: every component becomes an item of its own
+            clear_levels(queue, cnt);
+            std::vector<std::vector<i32>> comps;
+            std::vector<i64> lp2;
+            for (i32 v : it.V) {
+                if (part[v] != id) continue;
+                i64 c2;
+                bfs(queue, id, v, c2, lp2);
+                comps.emplace_back(queue.begin(), queue.begin() + c2);
+                clear_levels(queue, c2);
+                for (i32 u : comps.back()) part[u] = -id;
+            }
+            i64 hi = it.hi;
+            for (auto &c : comps) {
+                for (i32 u : c) part[u] = id;
+                i64 csz = (i64)c.size();
+                out.push_back({std::move(c), hi});
+                hi -= csz;
+            }
+            return;
+        }
+        // pseudo-peripheral root: restart from a vertex of minimum degree in the last level while the level
+        // structure gets deeper; a structure as deep as the current one is kept as it is
+        for (int iter = 0; iter < 4; iter++) {
+            i32 best = -1;
+            i64 bd = 1LL << 60;
+            for (i64 k = lptr[nlev - 1]; k < lptr[nlev]; k++) {
+                i32 v = queue[k];
+                i64 d = degree_in(v, id);
+                if (d < bd) { bd = d; best = v; }
+            }
+            clear_levels(queue, cnt);
+            std::vector<i64> lptr2;
+            i64 cnt2;
+            int nlev2 = bfs(queue, id, best, cnt2, lptr2);
+            if (nlev2 >= nlev) {
+                const bool deeper = nlev2 > nlev;
+                nlev = nlev2;
+                lptr = lptr2;
+                cnt = cnt2;
+                root = best;
+                if (!deeper) break;
+            } else {
+                clear_levels(queue, cnt2);
+                nlev = bfs(queue, id, root, cnt, lptr);
+                break;
+            }
+        }
+        if (nlev < 3) {
+            // too shallow to dissect: minimum degree would be too slow on a large item; natural order
+            for (i64 k = 0; k < cnt; k++) order[lo + k] = queue[k];
+            clear_levels(queue, cnt);
+            return;
+        }
+        // the separator level
+        int sl = -1;
+        i64 ssz = 1LL << 60, sbal = 1LL << 60;
+        const i64 minside = (i64)(0.3 * (double)sz);
+        for (int k = 1; k + 1 < nlev; k++) {
+            i64 a = lptr[k], s = lptr[k + 1] - lptr[k], b = sz - a - s;
+            if (a < minside || b < minside) continue;
+            i64 bal = a > b ? a - b : b - a;
+            if (s < ssz || (s == ssz && bal < sbal)) { ssz = s; sbal = bal; sl = k; }
+        }
+        if (sl < 0) {
+            for (int k = 1; k + 1 < nlev; k++)
+                if (lptr[k + 1] * 2 >= sz) { sl = k; break; }
+            if (sl < 0) sl = nlev / 2;
+        }
+        // sides: A = levels < sl, B = levels > sl, S = level sl; then drop separator vertices that touch only
+        // one side (a minimal separator)
+        const i32 idA = next_id.fetch_add(3), idB = idA + 1, idS = idA + 2;
+        for (i64 k = 0; k < cnt; k++) {
+            i32 v = queue[k];
+            part[v] = level[v] < sl ? idA : (level[v] > sl ? idB : idS);
+        }
+        clear_levels(queue, cnt);
+        std::vector<i32> S;
+        for (i64 k = lptr[sl]; k < lptr[sl + 1]; k++) S.push_back(queue[k]);
+        std::vector<i32> keep;
+        for (i32 v : S) {
+            bool ta = false, tb = false;
+            for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) {
+                i32 u = G.adj[p];
+                ta |= part[u] == idA;
+                tb |= part[u] == idB;
+            }
+            if (!tb) part[v] = idA;
+            else if (!ta) part[v] = idB;
+            else keep.push_back(v);
+        }
+        std::vector<i32> A, B;
+        for (i32 v : it.V) {
+            if (part[v] == idA) A.push_back(v);
+            else if (part[v] == idB) B.push_back(v);
+        }
+        const i64 ns = (i64)keep.size();
+        for (i64 k = 0; k < ns; k++) order[it.hi - ns + k] = keep[k];
+        const i64 na = (i64)A.size();
+        out.push_back({std::move(B), it.hi - ns});
+        out.push_back({std::move(A), lo + na});
+    }
+
+    // Items run on a pool of threads; a worker keeps splitting small items itself (depth first) and shares the
+    // large ones.
+    void run(int nthreads) {
         std::vector<Item> stack;
         {
             Item all;
@@ -163,133 +295,49 @@ struct ND {
             all.hi = G.n;
             stack.push_back(std::move(all));
         }
-        std::vector<i64> lptr;
-        while (!stack.empty()) {
-            Item it = std::move(stack.back());
-            stack.pop_back();
-            const i64 sz = (i64)it.V.size();
-            if (sz == 0) continue;
-            const i32 id = next_id++;
-            for (i32 v : it.V) part[v] = id;
-            const i64 lo = it.hi - sz;
-            if (sz <= leaf) {
-                md_leaf(it.V, lo);
-                continue;
-            }
-            // connected components of the item
-            i64 cnt;
-            i32 root = it.V[0];
-            {
-                i64 bd = 1LL << 60;
-                for (i32 v : it.V) {
-                    i64 d = degree_in(v, id);
-                    if (d < bd) { bd = d; root = v; }
+        std::mutex mu;
+        std::condition_variable cv;
+        int active = 0;
+        const i64 share = 2048;   // items at least this large go back to the shared stack
+        auto work = [&]() {
+            std::vector<i32> queue(G.n);
+            std::vector<i64> lptr;
+            std::vector<Item> out, local;
+            while (true) {
+                Item it;
+                {
+                    std::unique_lock<std::mutex> lk(mu);
+                    cv.wait(lk, [&] { return !stack.empty() || active == 0; });
+                    if (stack.empty()) return;
+                    it = std::move(stack.back());
+                    stack.pop_back();
+                    active++;
                 }
-            }
-            int nlev = bfs(id, root, cnt, lptr);
-            if (cnt < sz) {
-                // disconnected: every component becomes an item of its own
-                clear_levels(cnt);
-                std::vector<std::vector<i32>> comps;
-                std::vector<i64> lp2;
-                for (i32 v : it.V) {
-                    if (part[v] != id) continue;
-                    i64 c2;
-                    bfs(id, v, c2, lp2);
-                    comps.emplace_back(queue.begin(), queue.begin() + c2);
-                    clear_levels(c2);
-                    for (i32 u : comps.back()) part[u] = -id;
+                local.clear();
+                local.push_back(std::move(it));
+                std::vector<Item> shared;
+                while (!local.empty()) {
+                    Item cur = std::move(local.back());
+                    local.pop_back();
+                    out.clear();
+                    process(cur, queue, lptr, out);
+                    for (auto &o : out) {
+                        if ((i64)o.V.size() >= share && nthreads > 1) shared.push_back(std::move(o));
+                        else local.push_back(std::move(o));
+                    }
                 }
-                i64 hi = it.hi;
-                for (auto &c : comps) {
-                    for (i32 u : c) part[u] = id;
-                    i64 csz = (i64)c.size();
-                    stack.push_back({std::move(c), hi});
-                    hi -= csz;
+                {
+                    std::lock_guard<std::mutex> lk(mu);
+                    for (auto &o : shared) stack.push_back(std::move(o));
+                    active--;
                 }
-                continue;
+                cv.notify_all();
             }
-            // pseudo-peripheral root: restart from a vertex of minimum degree in the last level while the level
-            // structure gets deeper; a structure as deep as the current one is kept as it is
-            for (int iter = 0; iter < 4; iter++) {
-                i32 best = -1;
-                i64 bd = 1LL << 60;
-                for (i64 k = lptr[nlev - 1]; k < lptr[nlev]; k++) {
-                    i32 v = queue[k];
-                    i64 d = degree_in(v, id);
-                    if (d < bd) { bd = d; best = v; }
-                }
-                clear_levels(cnt);
-                std::vector<i64> lptr2;
-                i64 cnt2;
-                int nlev2 = bfs(id, best, cnt2, lptr2);
-                if (nlev2 >= nlev) {
-                    const bool deeper = nlev2 > nlev;
-                    nlev = nlev2;
-                    lptr = lptr2;
-                    cnt = cnt2;
-                    root = best;
-                    if (!deeper) break;
-                } else {
-                    clear_levels(cnt2);
-                    nlev = bfs(id, root, cnt, lptr);
-                    break;
-                }
-            }
-            if (nlev < 3) {
-                // too shallow to dissect: minimum degree would be too slow on a large item; natural order
-                for (i64 k = 0; k < cnt; k++) order[lo + k] = queue[k];
-                clear_levels(cnt);
-                continue;
-            }
-            // the separator level
-            int sl = -1;
-            i64 ssz = 1LL << 60, sbal = 1LL << 60;
-            const i64 minside = (i64)(0.3 * (double)sz);
-            for (int k = 1; k + 1 < nlev; k++) {
-                i64 a = lptr[k], s = lptr[k + 1] - lptr[k], b = sz - a - s;
-                if (a < minside || b < minside) continue;
-                i64 bal = a > b ? a - b : b - a;
-                if (s < ssz || (s == ssz && bal < sbal)) { ssz = s; sbal = bal; sl = k; }
-            }
-            if (sl < 0) {
-                for (int k = 1; k + 1 < nlev; k++)
-                    if (lptr[k + 1] * 2 >= sz) { sl = k; break; }
-                if (sl < 0) sl = nlev / 2;
-            }
-            // sides: A = levels < sl, B = levels > sl, S = level sl; then drop separator vertices that touch only
-            // one side (a minimal separator)
-            const i32 idA = next_id++, idB = next_id++, idS = next_id++;
-            for (i64 k = 0; k < cnt; k++) {
-                i32 v = queue[k];
-                part[v] = level[v] < sl ? idA : (level[v] > sl ? idB : idS);
-            }
-            clear_levels(cnt);
-            std::vector<i32> S;
-            for (i64 k = lptr[sl]; k < lptr[sl + 1]; k++) S.push_back(queue[k]);
-            std::vector<i32> keep;
-            for (i32 v : S) {
-                bool ta = false, tb = false;
-                for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) {
-                    i32 u = G.adj[p];
-                    ta |= part[u] == idA;
-                    tb |= part[u] == idB;
-                }
-                if (!tb) part[v] = idA;
-                else if (!ta) part[v] = idB;
-                else keep.push_back(v);
-            }
-            std::vector<i32> A, B;
-            for (i32 v : it.V) {
-                if (part[v] == idA) A.push_back(v);
-                else if (part[v] == idB) B.push_back(v);
-            }
-            const i64 ns = (i64)keep.size();
-            for (i64 k = 0; k < ns; k++) order[it.hi - ns + k] = keep[k];
-            const i64 na = (i64)A.size();
-            stack.push_back({std::move(B), it.hi - ns});
-            stack.push_back({std::move(A), lo + na});
-        }
+        };
+        std::vector<std::thread> pool;
+        for (int t = 1; t < nthreads; t++) pool.emplace_back(work);
+        work();
+        for (auto &th : pool) th.join();
     }
 };
 
@@ -529,33 +577,56 @@ std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, st
         out.Dptr[f + 1] = out.Dptr[f] + nn * nn;
         out.Lptr[f + 1] = out.Lptr[f] + nn * na;
     }
-    // where each stored entry lands: front of min(i, j), local positions in its bag
-    std::vector<i64> idx(n);
-    for (i64 f = 0; f < nf; f++)
-        for (i64 v = out.Rptr[f]; v < out.Rptr[f + 1]; v++) idx[v] = f;
-    stage("  copies", ts);
+    // where each stored entry lands: the front of min(i, j) (new labels), local positions in its bag.  Front by
+    // front with a position map of its bag: the entries of its residual's columns (row in the bag), then -- through
+    // the transpose -- those of its residual's rows whose column lies in its separator.
     out.nnz = colptr[n];
     out.entry_front.resize(out.nnz);
     out.entry_row.resize(out.nnz);
     out.entry_col.resize(out.nnz);
-    auto local = [&](i64 f, i64 v) -> i64 {
-        const i64 r0 = out.Rptr[f], r1 = out.Rptr[f + 1];
-        if (v >= r0 && v < r1) return v - r0;
-        const i64 *b = out.Stgt.data() + out.Sptr[f], *e = out.Stgt.data() + out.Sptr[f + 1];
-        const i64 *q = std::lower_bound(b, e, v);
-        if (q == e || *q != v) return -1;
-        return (r1 - r0) + (q - b);
-    };
+    std::vector<i64> rowptr(n + 1, 0);
+    for (i64 p = 0; p < out.nnz; p++) rowptr[rowval[p] + 1]++;
+    for (i64 i = 0; i < n; i++) rowptr[i + 1] += rowptr[i];
+    std::vector<i64> rowent(out.nnz), fill(rowptr.begin(), rowptr.end() - 1);
     for (i64 c = 0; c < n; c++)
-        for (i64 p = colptr[c]; p < colptr[c + 1]; p++) {
-            i64 i = out.invp[rowval[p]], j = out.invp[c];
-            i64 f = idx[std::min(i, j)];
-            i64 li = local(f, i), lj = local(f, j);
-            if (li < 0 || lj < 0) return "an entry of A falls outside the structure";
-            out.entry_front[p] = f;
-            out.entry_row[p] = (i32)li;
-            out.entry_col[p] = (i32)lj;
+        for (i64 p = colptr[c]; p < colptr[c + 1]; p++) rowent[fill[rowval[p]]++] = p;   // CSC position, by row
+    std::vector<i64> colof(out.nnz);
+    for (i64 c = 0; c < n; c++)
+        for (i64 p = colptr[c]; p < colptr[c + 1]; p++) colof[p] = c;
+    std::vector<int32_t> pos(n, -1);
+    i64 placed = 0;
+    for (i64 f = 0; f < nf; f++) {
+        const i64 r0 = out.Rptr[f], r1 = out.Rptr[f + 1], nn = r1 - r0;
+        const i64 s0 = out.Sptr[f], s1 = out.Sptr[f + 1];
+        for (i64 v = r0; v < r1; v++) pos[v] = (int32_t)(v - r0);
+        for (i64 q = s0; q < s1; q++) pos[out.Stgt[q]] = (int32_t)(nn + q - s0);
+        for (i64 j = r0; j < r1; j++) {
+            const i64 c = out.perm[j];
+            for (i64 p = colptr[c]; p < colptr[c + 1]; p++) {   // entry (i, j): front f when i >= r0
+                const i64 i = out.invp[rowval[p]];
+                if (i < r0) continue;
+                if (pos[i] < 0) return "an entry of A falls outside the structure";
+                out.entry_front[p] = f;
+                out.entry_row[p] = pos[i];
+                out.entry_col[p] = (i32)(j - r0);
+                placed++;
+            }
+            const i64 orow = out.perm[j];   // entries (j, i) with i after the residual: front f
+            for (i64 q = rowptr[orow]; q < rowptr[orow + 1]; q++) {
+                const i64 p = rowent[q];
+                const i64 i = out.invp[colof[p]];
+                if (i < r1) continue;
+                if (pos[i] < 0) return "an entry of A falls outside the structure";
+                out.entry_front[p] = f;
+                out.entry_row[p] = (i32)(j - r0);
+                out.entry_col[p] = pos[i];
+                placed++;
+            }
         }
+        for (i64 v = r0; v < r1; v++) pos[v] = -1;
+        for (i64 q = s0; q < s1; q++) pos[out.Stgt[q]] = -1;
+    }
+    if (placed != out.nnz) return "internal error: entries not placed";
     stage("  entries", ts);
     work_counts(n, out.Rptr, out.Sptr, out.parent, out.madds_factor, out.madds_star, out.madds_rhs, out.nnzL);
     return "";
@@ -598,7 +669,10 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
     std::vector<i64> perm0(n);
     if (opts.ordering == 0) {
         ND nd(G, opts.nd_leaf);
-        nd.run();
+        int threads = (int)std::min<unsigned>(16, std::max(1u, std::thread::hardware_concurrency()));
+        if (const char *e = std::getenv("PP_SYMBOLIC_THREADS")) threads = std::max(1, std::atoi(e));
+        if (n < 20000) threads = 1;
+        nd.run(threads);
         perm0 = nd.order;
     } else if (opts.ordering == 1) {
         std::iota(perm0.begin(), perm0.end(), 0);
