@@ -35,9 +35,7 @@ pp_sym::~pp_sym() {
 }
 
 pp_fac::~pp_fac() {
-    for (void *p : plan.owned) hipFree(p);
-    for (void *p : {LD, LL, UL, Dpack, Upack, Lpack})
-        if (p) hipFree(p);
+    for (void *p : plan.owned) hipFree(p);   // one block: the plans and the factor arrays
 }
 
 static bool supported(int semiring, int dtype) {
@@ -191,19 +189,6 @@ pp_status pp_sym_destroy(pp_sym *sym) {
 
 // ===== factor =====
 
-template <class V> static std::string upload(pp_fac *fac, hipStream_t st, const std::vector<V> &v, V **dst) {
-    *dst = nullptr;
-    if (v.empty()) return "";
-    void *p = nullptr;
-    hipError_t e = hipMalloc(&p, v.size() * sizeof(V));
-    if (e != hipSuccess) return std::string("hipMalloc: ") + hipGetErrorString(e);
-    fac->plan.owned.push_back(p);
-    e = hipMemcpyAsync(p, v.data(), v.size() * sizeof(V), hipMemcpyHostToDevice, st);
-    if (e != hipSuccess) return std::string("hipMemcpyAsync: ") + hipGetErrorString(e);
-    *dst = (V *)p;
-    return "";
-}
-
 static std::string ensure_plans(const pp_sym *csym) {
     pp_sym *sym = const_cast<pp_sym *>(csym);   // plans are a cache of the immutable structure
     if (!sym->fplan) {
@@ -261,59 +246,87 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *sym, int semiring, int
     fac->dtype = dtype;
     hipStream_t st = ctx->stream;
     pp::DevPlan &d = fac->plan;
-    std::vector<int32_t> tmp;
-#define UP(vec, ptr)                                   \
-    do {                                               \
-        e = upload(fac, st, vec, &ptr);                \
-        if (!e.empty()) {                              \
-            delete fac;                                \
-            return fail(ctx, PP_EHIP, "pp_factor: " + e); \
-        }                                              \
-    } while (0)
-    UP(P.nn, d.nn);
-    UP(P.na, d.na);
-    UP(P.nj, d.nj);
-    UP(P.relpos, d.relpos);
-    UP(P.chptr, d.chptr);
-    UP(P.chidx, d.chidx);
-    UP(P.Foff, d.Foff);
-    UP(P.Sptr32, d.Sptr);
-    UP(P.entry_pos, d.entry_pos);
-    UP(P.flist, d.flist);
-    UP(P.atask, d.atask);
-    UP(P.ftask, d.ftask);
-    UP(P.stask, d.stask);
-    UP(S.Dptr, d.Dptr);
-    UP(S.Lptr, d.Lptr);
-    UP(S.Rptr, d.Rptr);
-    UP(W.front, d.p_front);
-    UP(W.c0, d.p_c0);
-    UP(W.w, d.p_w);
-    UP(W.e, d.p_e);
-    UP(W.lo_ext, d.p_lo);
-    UP(W.chunks, d.p_chunks);
-    UP(W.eoff, d.p_eoff);
-    UP(W.poff, d.p_poff);
-    UP(W.doff, d.p_doff);
-    UP(W.rowA_lo, d.p_rowA_lo);
-    UP(W.rowA_hi, d.p_rowA_hi);
-    UP(W.rowB_lo, d.p_rowB_lo);
-    UP(W.rowB_hi, d.p_rowB_hi);
-    UP(W.Eidx, d.Eidx);
-    UP(W.plist, d.plist);
-    UP(W.tiles, d.tiles);
-    UP(S.perm, d.perm);
-    UP(S.invp, d.invp);
+    // One device block holds the plans (uploaded by one copy from pinned staging) and the factor arrays.
     std::vector<int32_t> invp32(S.invp.begin(), S.invp.end());
-    UP(invp32, d.invp32);
-#undef UP
-    auto alloc = [&](void **p, size_t elems) -> bool {
-        return hipMalloc(p, std::max<size_t>(1, elems) * es) == hipSuccess;
+    struct Part { const void *src; size_t bytes; size_t off; void **dst; };
+    std::vector<Part> parts;
+    size_t total = 0;
+    auto place = [&](size_t bytes) {
+        const size_t off = total;
+        total += (std::max<size_t>(bytes, 1) + 255) & ~size_t(255);
+        return off;
     };
-    if (!alloc(&fac->LD, nD) || !alloc(&fac->LL, nL) || !alloc(&fac->UL, nL) || !alloc(&fac->Dpack, W.ndpack) ||
-        !alloc(&fac->Upack, W.npack) || !alloc(&fac->Lpack, W.npack)) {
+    auto plan_part = [&](const auto &vec, auto **ptr) {
+        const size_t bytes = vec.size() * sizeof(vec[0]);
+        parts.push_back({vec.data(), bytes, place(bytes), (void **)ptr});
+    };
+    plan_part(P.nn, &d.nn);
+    plan_part(P.na, &d.na);
+    plan_part(P.nj, &d.nj);
+    plan_part(P.relpos, &d.relpos);
+    plan_part(P.chptr, &d.chptr);
+    plan_part(P.chidx, &d.chidx);
+    plan_part(P.Foff, &d.Foff);
+    plan_part(P.Sptr32, &d.Sptr);
+    plan_part(P.entry_pos, &d.entry_pos);
+    plan_part(P.flist, &d.flist);
+    plan_part(P.atask, &d.atask);
+    plan_part(P.etask, &d.etask);
+    plan_part(P.ftask, &d.ftask);
+    plan_part(P.stask, &d.stask);
+    plan_part(S.Dptr, &d.Dptr);
+    plan_part(S.Lptr, &d.Lptr);
+    plan_part(S.Rptr, &d.Rptr);
+    plan_part(W.front, &d.p_front);
+    plan_part(W.c0, &d.p_c0);
+    plan_part(W.w, &d.p_w);
+    plan_part(W.e, &d.p_e);
+    plan_part(W.lo_ext, &d.p_lo);
+    plan_part(W.chunks, &d.p_chunks);
+    plan_part(W.eoff, &d.p_eoff);
+    plan_part(W.poff, &d.p_poff);
+    plan_part(W.doff, &d.p_doff);
+    plan_part(W.rowA_lo, &d.p_rowA_lo);
+    plan_part(W.rowA_hi, &d.p_rowA_hi);
+    plan_part(W.rowB_lo, &d.p_rowB_lo);
+    plan_part(W.rowB_hi, &d.p_rowB_hi);
+    plan_part(W.Eidx, &d.Eidx);
+    plan_part(W.plist, &d.plist);
+    plan_part(W.tiles, &d.tiles);
+    plan_part(S.perm, &d.perm);
+    plan_part(S.invp, &d.invp);
+    plan_part(invp32, &d.invp32);
+    const size_t plan_bytes = total;
+    const size_t oLD = place(nD * es), oLL = place(nL * es), oUL = place(nL * es), oD = place(W.ndpack * es),
+                 oU = place(W.npack * es), oL = place(W.npack * es);
+    if (ctx->staging_bytes < plan_bytes) {
+        if (ctx->staging) hipHostFree(ctx->staging);
+        ctx->staging = nullptr;
+        ctx->staging_bytes = 0;
+        if (hipHostMalloc(&ctx->staging, plan_bytes, hipHostMallocDefault) != hipSuccess) {
+            delete fac;
+            return fail(ctx, PP_ENOMEM, "pp_factor: pinned staging allocation failed");
+        }
+        ctx->staging_bytes = plan_bytes;
+    }
+    for (const Part &q : parts)
+        if (q.bytes) std::memcpy((char *)ctx->staging + q.off, q.src, q.bytes);
+    void *block = nullptr;
+    if (hipMalloc(&block, total) != hipSuccess) {
         delete fac;
         return fail(ctx, PP_ENOMEM, "pp_factor: hipMalloc of the factor failed");
+    }
+    d.owned.push_back(block);
+    for (const Part &q : parts) *q.dst = q.bytes ? (void *)((char *)block + q.off) : nullptr;
+    fac->LD = (char *)block + oLD;
+    fac->LL = (char *)block + oLL;
+    fac->UL = (char *)block + oUL;
+    fac->Dpack = (char *)block + oD;
+    fac->Upack = (char *)block + oU;
+    fac->Lpack = (char *)block + oL;
+    if (hipMemcpyAsync(block, ctx->staging, plan_bytes, hipMemcpyHostToDevice, st) != hipSuccess) {
+        delete fac;
+        return fail(ctx, PP_EHIP, "pp_factor: upload of the plans failed");
     }
     const void *dnz = nzval;
     void *tmpnz = nullptr;

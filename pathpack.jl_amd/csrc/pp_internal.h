@@ -2,9 +2,9 @@
 //
 // Factorization plan.  Every frontal matrix F_f (nj x nj, nj = nn + na, column-major, local order res(f) then
 // sep(f)) has a fixed place in one arena.  Fronts are grouped by height in the front tree (leaves 0); a height level
-// runs: extend-add of the children's update blocks F_c[nn_c:, nn_c:] into the parents (one workgroup per parent,
-// children one after another), then the partial LU of the fronts' first nn pivots.  Fronts with nj <= SMALL_NJ are
-// factorized by one workgroup in LDS; larger fronts take blocked steps of NB pivots: a panel kernel (LU of the
+// runs: extend-add of the children's update blocks F_c[nn_c:, nn_c:] into the parents (one workgroup per parent
+// column block, children one after another), then the partial LU of the fronts' first nn pivots.  Fronts with
+// nj <= MID_NJ are factorized by one workgroup in LDS; larger fronts take blocked steps of NB pivots: a panel kernel (LU of the
 // NB x NB diagonal block in LDS + triangular solves of the row and column panels) and a batched semiring GEMM on
 // the trailing block.  Afterwards the factor values are copied into the reference's storage layout and into
 // per-panel packs for the sweeps.
@@ -28,8 +28,10 @@
 
 namespace pp {
 
-constexpr int SMALL_NJ = 64;   // fronts up to this size are factorized in one workgroup's LDS
+constexpr int SMALL_NJ = 64;   // fronts up to this size are factorized in one workgroup's LDS ...
+constexpr int MID_NJ = 128;    // ... and up to this size too, in a workgroup with a larger LDS block
 constexpr int ASM_BLOCK = 16;  // parent columns per extend-add workgroup
+constexpr int EXTRACT_COLS = 32;  // frontal columns per factor-extraction workgroup
 constexpr int NB = 32;         // pivot block of the blocked front factorization
 constexpr int PANEL_W = 32;    // widest sweep panel
 constexpr int NCLASS = 6;      // sweep width classes 1, 2, 4, 8, 16, 32
@@ -60,11 +62,13 @@ struct FactorPlan {
     struct Level {
         i64 asm_off, asm_cnt;        // extend-add tasks (front, first parent column) in atask
         i64 small_off, small_cnt;    // fronts with nj <= SMALL_NJ, in flist
+        i64 mid_off, mid_cnt;        // fronts with SMALL_NJ < nj <= MID_NJ, in flist
         std::vector<Step> steps;     // blocked steps for the large fronts
     };
     std::vector<Level> levels;
     std::vector<int32_t> flist;      // front lists of all levels
     std::vector<int32_t> atask;      // (front, first column) per extend-add task: 2 ints
+    std::vector<int32_t> etask;      // (front, first column) per extraction task: 2 ints
     std::vector<int32_t> ftask;      // (front, step offset, chunk) per panel task: 3 ints
     std::vector<int32_t> stask;      // (front, step offset, ti, tj) per Schur task: 4 ints
     i64 max_nj = 0;
@@ -101,7 +105,7 @@ struct DevPlan {
     // factor
     int32_t *nn = nullptr, *na = nullptr, *nj = nullptr, *relpos = nullptr, *chptr = nullptr, *chidx = nullptr;
     i64 *Foff = nullptr, *Sptr = nullptr, *entry_pos = nullptr;
-    int32_t *flist = nullptr, *ftask = nullptr, *stask = nullptr, *atask = nullptr;
+    int32_t *flist = nullptr, *ftask = nullptr, *stask = nullptr, *atask = nullptr, *etask = nullptr;
     i64 *Dptr = nullptr, *Lptr = nullptr, *Rptr = nullptr;
     // sweeps
     int32_t *p_front = nullptr, *p_c0 = nullptr, *p_w = nullptr, *p_e = nullptr, *p_lo = nullptr, *p_chunks = nullptr;

@@ -90,11 +90,11 @@ __global__ __launch_bounds__(NT) void k_assemble(typename S::value_type *__restr
         }
         int w1 = lo;
         while (w1 < nc && rp[w1] < b) w1++;
-        const int w0 = lo, cnt = (w1 - w0) * nc;
-        for (int e = threadIdx.x; e < cnt; e += NT) {
-            const int v = e % nc, w = w0 + e / nc;
-            T *dst = Ff + rp[v] + (i64)rp[w] * ldf;
-            *dst = S::plus(*dst, M[v + (i64)w * ldc]);
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        for (int w = lo + wave; w < w1; w += NT / 64) {
+            T *dcol = Ff + (i64)rp[w] * ldf;
+            const T *scol = M + (i64)w * ldc;
+            for (int v = lane; v < nc; v += 64) dcol[rp[v]] = S::plus(dcol[rp[v]], scol[v]);
         }
         __syncthreads();
     }
@@ -104,28 +104,29 @@ __global__ __launch_bounds__(NT) void k_assemble(typename S::value_type *__restr
 
 template <class S>
 __device__ inline void lds_lu(typename S::value_type *A, int n, int lda, int p) {
+    // waves take columns, lanes take rows: no integer division in the update
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     for (int i = 0; i < p; i++) {
         if (!S::integral) {
             const typename S::value_type s = S::star(A[i + i * lda]);
-            for (int k = i + 1 + threadIdx.x; k < n; k += NT) A[k + i * lda] = S::prod(A[k + i * lda], s);
+            for (int k = i + 1 + (int)threadIdx.x; k < n; k += (int)blockDim.x) A[k + i * lda] = S::prod(A[k + i * lda], s);
             __syncthreads();
         }
-        const int m = n - i - 1;
-        for (int e = threadIdx.x; e < m * m; e += NT) {
-            const int k = i + 1 + e % m, j = i + 1 + e / m;
-            A[k + j * lda] = S::muladd(A[k + i * lda], A[i + j * lda], A[k + j * lda]);
+        for (int j = i + 1 + wave; j < n; j += nw) {
+            const typename S::value_type aij = A[i + j * lda];
+            for (int k = i + 1 + lane; k < n; k += 64) A[k + j * lda] = S::muladd(A[k + i * lda], aij, A[k + j * lda]);
         }
         __syncthreads();
     }
 }
 
-// fronts with nj <= SMALL_NJ: the whole partial LU (nn pivots of the nj x nj front) in one workgroup
-template <class S>
+// fronts with nj <= MAXN: the whole partial LU (nn pivots of the nj x nj front) in one workgroup
+template <class S, int MAXN>
 __global__ __launch_bounds__(NT) void k_front_small(typename S::value_type *__restrict__ F, const i64 *__restrict__ Foff,
                                                     const int32_t *__restrict__ nn, const int32_t *__restrict__ nj,
                                                     const int32_t *__restrict__ list) {
     typedef typename S::value_type T;
-    __shared__ T A[SMALL_NJ * SMALL_NJ];
+    __shared__ T A[MAXN * MAXN];
     const int f = list[blockIdx.x];
     const int n = nj[f], p = nn[f];
     T *G = F + Foff[f];
@@ -151,50 +152,57 @@ __global__ __launch_bounds__(NT) void k_front_panel(typename S::value_type *__re
     const int b = min(NB, nn[f] - off);
     const int m0 = off + b;
     T *A = F + Foff[f];
-    for (int e = threadIdx.x; e < b * b; e += NT) {
-        const int i = e % b, j = e / b;
-        D[i + j * LD] = A[(off + i) + (i64)(off + j) * n];
+    {
+        const int i = threadIdx.x & 31;
+        for (int j = threadIdx.x >> 5; j < b; j += NT / 32)
+            if (i < b) D[i + j * LD] = A[(off + i) + (i64)(off + j) * n];
     }
     __syncthreads();
     lds_lu<S>(D, b, LD, b);
-    if (chunk == 0)
-        for (int e = threadIdx.x; e < b * b; e += NT) {
-            const int i = e % b, j = e / b;
-            A[(off + i) + (i64)(off + j) * n] = D[i + j * LD];
-        }
+    if (chunk == 0) {
+        const int i = threadIdx.x & 31;
+        for (int j = threadIdx.x >> 5; j < b; j += NT / 32)
+            if (i < b) A[(off + i) + (i64)(off + j) * n] = D[i + j * LD];
+    }
+    // pad the factored block to NB x NB with the semiring zero: the solves below then run over all NB columns
+    // without guards.  A real unknown j < b reads only unknowns i < j and D[i, j] with i, j < b; the padded unknowns
+    // (whatever they hold) feed padded unknowns only and are never stored.
+    for (int q = threadIdx.x; q < NB * NB; q += NT) {
+        const int i = q & (NB - 1), j = q / NB;
+        if (i >= b || j >= b) D[i + j * LD] = S::zero();
+    }
+    __syncthreads();
     const int r = m0 + chunk * NT + threadIdx.x;
     if (r < n) {
-        // row r of the column panel
+        // row r of the column panel: x <- x U_kk*
         T x[NB];
 #pragma unroll
-        for (int j = 0; j < NB; j++)
-            if (j < b) x[j] = A[r + (i64)(off + j) * n];
+        for (int j = 0; j < NB; j++) x[j] = A[r + (i64)(off + min(j, b - 1)) * n];   // padded unknowns: any value
 #pragma unroll
         for (int j = 0; j < NB; j++) {
-            if (j < b) {
-                T acc = x[j];
+            T acc = x[j];
 #pragma unroll
-                for (int i = 0; i < j; i++) acc = S::muladd(x[i], D[i + j * LD], acc);
-                if (!S::integral) acc = S::prod(acc, S::star(D[j + j * LD]));
-                x[j] = acc;
-            }
+            for (int i = 0; i < j; i++) acc = S::muladd(x[i], D[i + j * LD], acc);
+            if (!S::integral) acc = S::prod(acc, S::star(D[j + j * LD]));
+            x[j] = acc;
+            // compiler barrier: column j is computed before the LDS reads of column j + 1 are issued, which bounds
+            // the live registers (otherwise all D reads are hoisted and the arithmetic sunk, and the kernel spills)
+            asm volatile("" : "+v"(x[j])::"memory");
         }
 #pragma unroll
         for (int j = 0; j < NB; j++)
             if (j < b) A[r + (i64)(off + j) * n] = x[j];
-        // column r of the row panel
+        // column r of the row panel: y <- L_kk* y
         T y[NB];
 #pragma unroll
-        for (int i = 0; i < NB; i++)
-            if (i < b) y[i] = A[(off + i) + (i64)r * n];
+        for (int i = 0; i < NB; i++) y[i] = A[(off + min(i, b - 1)) + (i64)r * n];
 #pragma unroll
         for (int i = 0; i < NB; i++) {
-            if (i < b) {
-                T acc = y[i];
+            T acc = y[i];
 #pragma unroll
-                for (int k = 0; k < i; k++) acc = S::muladd(D[i + k * LD], y[k], acc);
-                y[i] = acc;
-            }
+            for (int k = 0; k < i; k++) acc = S::muladd(D[i + k * LD], y[k], acc);
+            y[i] = acc;
+            asm volatile("" : "+v"(y[i])::"memory");
         }
 #pragma unroll
         for (int i = 0; i < NB; i++)
@@ -282,23 +290,25 @@ __global__ __launch_bounds__(NT) void k_gemm(typename S::value_type *__restrict_
 
 // ===== factor extraction: the reference layout and the sweep packs =====
 
-// LD (nn x nn at Dptr), LL (na x nn at Lptr), UL (nn x na at Lptr), one workgroup per front
+// LD (nn x nn at Dptr), LL (na x nn at Lptr), UL (nn x na at Lptr); one workgroup per (front, EXTRACT_COLS columns)
 template <class T>
 __global__ __launch_bounds__(NT) void k_extract_ref(const T *__restrict__ F, const i64 *__restrict__ Foff,
                                                    const int32_t *__restrict__ nn, const int32_t *__restrict__ nj,
                                                    const i64 *__restrict__ Dptr, const i64 *__restrict__ Lptr,
-                                                   T *__restrict__ LD, T *__restrict__ LL, T *__restrict__ UL) {
-    const int f = blockIdx.x;
+                                                   const int32_t *__restrict__ tasks, T *__restrict__ LD,
+                                                   T *__restrict__ LL, T *__restrict__ UL) {
+    const int f = tasks[2 * blockIdx.x], c0 = tasks[2 * blockIdx.x + 1];
     const int a = nn[f], n = nj[f], c = n - a;
     const T *G = F + Foff[f];
-    for (int e = threadIdx.x; e < a * a; e += NT) LD[Dptr[f] + e] = G[(e % a) + (i64)(e / a) * n];
-    for (int e = threadIdx.x; e < a * c; e += NT) {
-        const int r = e % c, col = e / c;   // LL[r, col] = F[a + r, col]
-        LL[Lptr[f] + e] = G[(a + r) + (i64)col * n];
-    }
-    for (int e = threadIdx.x; e < a * c; e += NT) {
-        const int r = e % a, col = e / a;   // UL[r, col] = F[r, a + col]
-        UL[Lptr[f] + e] = G[r + (i64)(a + col) * n];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c1 = min(n, c0 + EXTRACT_COLS);
+    for (int col = c0 + wave; col < c1; col += NT / 64) {
+        if (col < a) {
+            for (int r = lane; r < a; r += 64) LD[Dptr[f] + r + (i64)col * a] = G[r + (i64)col * n];
+            for (int r = lane; r < c; r += 64) LL[Lptr[f] + r + (i64)col * c] = G[(a + r) + (i64)col * n];   // F[a+r, col]
+        } else {
+            for (int r = lane; r < a; r += 64) UL[Lptr[f] + r + (i64)(col - a) * a] = G[r + (i64)col * n];   // F[r, col]
+        }
     }
 }
 
@@ -321,12 +331,13 @@ __global__ __launch_bounds__(NT) void k_build_packs(const typename S::value_type
     const int n = nj[f];
     const int lj0 = p_c0[p] - (int)Rptr[f];
     const T *G = F + Foff[f];
+    const int sh = __builtin_ctz(Wc);
     for (int q = threadIdx.x; q < Wc * Wc; q += NT) {
-        const int i = q % Wc, j = q / Wc;
+        const int i = q & (Wc - 1), j = q >> sh;
         Dpack[p_doff[p] + q] = (i < w && j < w) ? G[(lj0 + i) + (i64)(lj0 + j) * n] : S::zero();
     }
     for (int q = threadIdx.x; q < Wc * e; q += NT) {
-        const int j = q % Wc, t = q / Wc;   // element (j, t) at t*Wc + j
+        const int j = q & (Wc - 1), t = q >> sh;   // element (j, t) at t*Wc + j
         Upack[p_poff[p] + q] = j < w ? G[(lj0 + j) + (i64)(lo + t) * n] : S::zero();
         Lpack[p_poff[p] + q] = j < w ? G[(lo + t) + (i64)(lj0 + j) * n] : S::zero();
     }
@@ -731,7 +742,10 @@ template <class S> struct FactorRun {
                 k_assemble<S><<<(unsigned)L.asm_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.na, d.nj, d.Sptr, d.relpos, d.chptr,
                                                                  d.chidx, d.atask + 2 * L.asm_off);
             if (L.small_cnt)
-                k_front_small<S><<<(unsigned)L.small_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.flist + L.small_off);
+                k_front_small<S, SMALL_NJ><<<(unsigned)L.small_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.nj,
+                                                                                  d.flist + L.small_off);
+            if (L.mid_cnt)
+                k_front_small<S, MID_NJ><<<(unsigned)L.mid_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.flist + L.mid_off);
             for (const auto &s : L.steps) {
                 if (s.panel_cnt)
                     k_front_panel<S><<<(unsigned)s.panel_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.ftask + 3 * s.panel_off);
@@ -741,9 +755,9 @@ template <class S> struct FactorRun {
             LAUNCHCHK();
         }
         const i64 nf = P.nf;
-        if (nf > 0)
-            k_extract_ref<T><<<(unsigned)nf, NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.Dptr, d.Lptr, (T *)fac->LD,
-                                                          (T *)fac->LL, (T *)fac->UL);
+        if (P.etask.size())
+            k_extract_ref<T><<<(unsigned)(P.etask.size() / 2), NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.Dptr, d.Lptr, d.etask,
+                                                                            (T *)fac->LD, (T *)fac->LL, (T *)fac->UL);
         if (W.np > 0)
             k_build_packs<S><<<(unsigned)W.np, NT, 0, st>>>(F, d.Foff, d.nj, d.Rptr, d.p_front, d.p_c0, d.p_w, d.p_e,
                                                             d.p_lo, d.p_poff, d.p_doff, (T *)fac->Dpack,

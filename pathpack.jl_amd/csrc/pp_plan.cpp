@@ -68,6 +68,12 @@ std::string build_factor_plan(const Symbolic &S, FactorPlan &P) {
     }
     std::vector<std::vector<int32_t>> byh(H);
     for (i64 f = 0; f < nf; f++) byh[h[f]].push_back((int32_t)f);
+    P.etask.clear();
+    for (i64 f = 0; f < nf; f++)
+        for (int32_t c = 0; c < P.nj[f]; c += EXTRACT_COLS) {
+            P.etask.push_back((int32_t)f);
+            P.etask.push_back(c);
+        }
     P.levels.clear();
     P.flist.clear();
     P.atask.clear();
@@ -87,15 +93,19 @@ std::string build_factor_plan(const Symbolic &S, FactorPlan &P) {
         for (int32_t f : byh[l])
             if (P.nj[f] <= SMALL_NJ) P.flist.push_back(f);
         L.small_cnt = (i64)P.flist.size() - L.small_off;
+        L.mid_off = (i64)P.flist.size();
+        for (int32_t f : byh[l])
+            if (P.nj[f] > SMALL_NJ && P.nj[f] <= MID_NJ) P.flist.push_back(f);
+        L.mid_cnt = (i64)P.flist.size() - L.mid_off;
         i64 maxsteps = 0;
         for (int32_t f : byh[l])
-            if (P.nj[f] > SMALL_NJ) maxsteps = std::max<i64>(maxsteps, (P.nn[f] + NB - 1) / NB);
+            if (P.nj[f] > MID_NJ) maxsteps = std::max<i64>(maxsteps, (P.nn[f] + NB - 1) / NB);
         for (i64 s = 0; s < maxsteps; s++) {
             FactorPlan::Step st;
             st.panel_off = (i64)P.ftask.size() / 3;
             st.schur_off = (i64)P.stask.size() / 4;
             for (int32_t f : byh[l]) {
-                if (P.nj[f] <= SMALL_NJ || s * NB >= P.nn[f]) continue;
+                if (P.nj[f] <= MID_NJ || s * NB >= P.nn[f]) continue;
                 i64 off = s * NB, b = std::min<i64>(NB, P.nn[f] - off), m = P.nj[f] - off - b;
                 i64 chunks = std::max<i64>(1, (m + 255) / 256);
                 for (i64 c = 0; c < chunks; c++) {
