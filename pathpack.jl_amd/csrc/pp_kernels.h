@@ -491,72 +491,95 @@ __device__ inline void locate_tile(const SweepArgs &a, int np, int &pi, int &til
 }
 
 template <class S, int W, int DMODE, int KSPLIT>
-__global__ __launch_bounds__(64 * KSPLIT) void k_sweep_bwd(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
+__global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(sizeof(typename S::value_type) == 4 ? 4 : 2))) void k_sweep_bwd(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
                                                            const typename S::value_type *__restrict__ Dpack,
                                                            const typename S::value_type *__restrict__ Q) {
     typedef typename S::value_type T;
-    __shared__ T red[KSPLIT - 1][W][TILE_ROWS];
+    __shared__ T red[KSPLIT > 1 ? KSPLIT - 1 : 1][W][TILE_ROWS];
     int pi, tile;
     locate_tile(a, a.np, pi, tile);
     const int p = a.plist[pi];
     const int lo = a.pre ? a.row_lo[p] : a.row_base, hi = a.pre ? a.row_hi[p] : a.row_base + a.nrows;
     const int lane = threadIdx.x & 63;
     const int q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // the wave: uniform, so pack loads are scalar
+    if (lo + tile * TILE_ROWS >= hi) return;   // a padding tile of the XCD-aware mapping (whole workgroup)
     const int r = lo + tile * TILE_ROWS + lane;
     const bool valid = r < hi;
+    const T *xr = X + (valid ? r : hi - 1);   // lanes past the last row compute on a valid row and store nothing
     const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
     const T *Qp = Q + a.p_poff[p];
     const int32_t *E = a.Eidx + a.p_eoff[p];
     T acc[W];
+    if (q == 0) {
 #pragma unroll
-    for (int j = 0; j < W; j++) acc[j] = (q == 0 && j < w && valid) ? X[(i64)(c0 + j) * ld + r] : S::zero();
-    // this wave's share of the gather list, four columns per step with the next four already in flight
-    const int k0 = (int)(((i64)e * q) / KSPLIT), k1 = (int)(((i64)e * (q + 1)) / KSPLIT);
-    if (valid) {
-        int k = k0;
-        if (k + 4 <= k1) {
-            T v0 = X[(i64)E[k] * ld + r], v1 = X[(i64)E[k + 1] * ld + r], v2 = X[(i64)E[k + 2] * ld + r],
-              v3 = X[(i64)E[k + 3] * ld + r];
-            while (true) {
-                const bool more = k + 8 <= k1;
-                T n0 = v0, n1 = v1, n2 = v2, n3 = v3;
-                if (more) {
-                    n0 = X[(i64)E[k + 4] * ld + r];
-                    n1 = X[(i64)E[k + 5] * ld + r];
-                    n2 = X[(i64)E[k + 6] * ld + r];
-                    n3 = X[(i64)E[k + 7] * ld + r];
-                }
-                const T *q0 = Qp + (i64)k * W;
-#pragma unroll
-                for (int j = 0; j < W; j++) {
-                    acc[j] = S::muladd2(v0, q0[j], v1, q0[W + j], acc[j]);
-                    acc[j] = S::muladd2(v2, q0[2 * W + j], v3, q0[3 * W + j], acc[j]);
-                }
-                k += 4;
-                if (!more) break;
-                v0 = n0;
-                v1 = n1;
-                v2 = n2;
-                v3 = n3;
-            }
+        for (int j = 0; j < W; j++) {
+            const T v = xr[(i64)(c0 + min(j, w - 1)) * ld];
+            acc[j] = j < w ? v : S::zero();
         }
-        for (; k < k1; k++) {
-            const T v0 = X[(i64)E[k] * ld + r];
-            const T *q0 = Qp + (i64)k * W;
+    } else {
 #pragma unroll
-            for (int j = 0; j < W; j++) acc[j] = S::muladd(v0, q0[j], acc[j]);
+        for (int j = 0; j < W; j++) acc[j] = S::zero();
+    }
+    // this wave's share of the gather list, in groups of four columns, with the next two groups' loads in flight
+    // (three register sets used in rotation, so no copy waits on a load); the lookahead reads up to eight entries
+    // past the share, into the following lists or the zero padding after the last one
+    const int ng = e >> 2;
+    const int g0 = (int)(((i64)ng * q) / KSPLIT), g1 = (int)(((i64)ng * (q + 1)) / KSPLIT);
+    const int kt = 4 * g1, kend = q == KSPLIT - 1 ? e : kt;
+    const int32_t *ep = E + 4 * g0;
+    const T *qp = Qp + (i64)(4 * g0) * W;
+    auto ld4 = [&](const int32_t *ei, T(&v)[4]) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = xr[(i64)ei[u] * ld];
+        __builtin_amdgcn_sched_barrier(0);   // issue the loads here, ahead of the arithmetic that follows
+    };
+    auto mad4 = [&](const T(&v)[4], const T *qq) {
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            acc[j] = S::muladd2(v[0], qq[j], v[1], qq[W + j], acc[j]);
+            acc[j] = S::muladd2(v[2], qq[2 * W + j], v[3], qq[3 * W + j], acc[j]);
+        }
+    };
+    const int ngw = g1 - g0;
+    if (ngw > 0) {
+        T A[4], B[4], C[4];
+        ld4(ep, A);
+        ld4(ep + 4, B);
+        int g = 0;
+        for (; g + 3 <= ngw; g += 3) {
+            ld4(ep + 8, C);
+            mad4(A, qp);
+            ld4(ep + 12, A);
+            mad4(B, qp + 4 * W);
+            ld4(ep + 16, B);
+            mad4(C, qp + 8 * W);
+            ep += 12;
+            qp += 12 * W;
+        }
+        if (g < ngw) {
+            mad4(A, qp);
+            qp += 4 * W;
+            if (g + 1 < ngw) mad4(B, qp);
         }
     }
-    if (q > 0) {
+    for (int k = kt; k < kend; k++) {
+        const T v0 = xr[(i64)E[k] * ld];
+        const T *q0 = Qp + (i64)k * W;
 #pragma unroll
-        for (int j = 0; j < W; j++) red[q - 1][j][lane] = acc[j];
+        for (int j = 0; j < W; j++) acc[j] = S::muladd(v0, q0[j], acc[j]);
     }
-    __syncthreads();
-    if (q != 0 || !valid) return;
+    if (KSPLIT > 1) {
+        if (q > 0) {
 #pragma unroll
-    for (int qq = 0; qq < KSPLIT - 1; qq++)
+            for (int j = 0; j < W; j++) red[q - 1][j][lane] = acc[j];
+        }
+        __syncthreads();
+        if (q != 0) return;
 #pragma unroll
-        for (int j = 0; j < W; j++) acc[j] = S::plus(acc[j], red[qq][j][lane]);
+        for (int qq = 0; qq < KSPLIT - 1; qq++)
+#pragma unroll
+            for (int j = 0; j < W; j++) acc[j] = S::plus(acc[j], red[qq][j][lane]);
+    }
     const T *D = Dpack + a.p_doff[p];
 #pragma unroll
     for (int j = W - 1; j >= 0; j--) {
@@ -566,9 +589,11 @@ __global__ __launch_bounds__(64 * KSPLIT) void k_sweep_bwd(typename S::value_typ
         if (DMODE == 1 && !S::integral) s = S::prod(s, S::star(D[j + j * W]));
         acc[j] = s;
     }
+    if (valid) {
 #pragma unroll
-    for (int j = 0; j < W; j++)
-        if (j < w) X[(i64)(c0 + j) * ld + r] = acc[j];
+        for (int j = 0; j < W; j++)
+            if (j < w) X[(i64)(c0 + j) * ld + r] = acc[j];
+    }
 }
 
 // ===== relabel and permutations =====
@@ -820,16 +845,24 @@ static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type
             ntile = (a.nrows + TILE_ROWS - 1) / TILE_ROWS;
             grid = (unsigned)(li.cnt * ((ntile + 7) / 8) * 8);
         }
-        // few workgroups for the whole chip: split each row tile's gather list over eight waves instead of four
-        const bool wide = li.cnt * ntile < 1024;
+        // split each row tile's gather list over KS waves when the list has too few tiles to fill the chip (about
+        // 4096 waves), keeping at least 32 gather columns per wave
+        const i64 tiles_total = li.cnt * ntile, emean = li.esum / std::max<i64>(1, li.cnt);
+        int ks = 1;
+        while (ks < 8 && tiles_total * ks < 4096 && emean >= 64 * ks) ks *= 2;
         if (grid) {
-            if (wide) {
-                if (dmode == 0) k_sweep_bwd<S, W, 0, 8><<<grid, 512, 0, st>>>(X, ld, a, D, Pk);
-                else k_sweep_bwd<S, W, 1, 8><<<grid, 512, 0, st>>>(X, ld, a, D, Pk);
-            } else {
-                if (dmode == 0) k_sweep_bwd<S, W, 0, 4><<<grid, 256, 0, st>>>(X, ld, a, D, Pk);
-                else k_sweep_bwd<S, W, 1, 4><<<grid, 256, 0, st>>>(X, ld, a, D, Pk);
+#define PP_BWD(KS)                                                                                             \
+    do {                                                                                                         \
+        if (dmode == 0) k_sweep_bwd<S, W, 0, KS><<<grid, 64 * KS, 0, st>>>(X, ld, a, D, Pk);                     \
+        else k_sweep_bwd<S, W, 1, KS><<<grid, 64 * KS, 0, st>>>(X, ld, a, D, Pk);                                \
+    } while (0)
+            switch (ks) {
+            case 1: PP_BWD(1); break;
+            case 2: PP_BWD(2); break;
+            case 4: PP_BWD(4); break;
+            default: PP_BWD(8); break;
             }
+#undef PP_BWD
         }
     }
 }

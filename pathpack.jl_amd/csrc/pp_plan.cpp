@@ -184,6 +184,7 @@ std::string build_sweep_plan(const Symbolic &S, const FactorPlan &F, SweepPlan &
         }
         last[f] = P.np - 1;
     }
+    P.Eidx.insert(P.Eidx.end(), EIDX_PAD, 0);
     // forward levels (leaves to root) and backward levels (root to leaves)
     std::vector<i64> lvA(P.np, 0), lvB(P.np, 0);
     std::vector<i64> endA(nf, -1);
@@ -226,6 +227,8 @@ std::string build_sweep_plan(const Symbolic &S, const FactorPlan &F, SweepPlan &
             li.pAu = prefix([&](int32_t p) { return tiles_of(P.rowA_lo[p], P.rowA_hi[p], TILE_ROWS) * P.chunks[p]; });
             li.pB64 = prefix([&](int32_t p) { return tiles_of(P.rowB_lo[p], P.rowB_hi[p], TILE_ROWS); });
             li.pC = prefix([&](int32_t p) { return (i64)P.chunks[p]; });
+            li.esum = 0;
+            for (int32_t p : buckets[b]) li.esum += P.e[p];
             li.uniB = true;
             li.rowB_lo = P.rowB_lo[buckets[b][0]];
             li.rowB_hi = P.rowB_hi[buckets[b][0]];
