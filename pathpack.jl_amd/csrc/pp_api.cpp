@@ -56,6 +56,11 @@ pp_status pp_init(pp_ctx **out, int device) {
     pp_ctx *ctx = new (std::nothrow) pp_ctx;
     if (!ctx) return fail(nullptr, PP_ENOMEM, "pp_init: out of host memory");
     ctx->device = device;
+    {
+        int cu = 0;
+        if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cu > 0)
+            ctx->num_cu = cu;
+    }
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
         delete ctx;
         return fail(nullptr, PP_EHIP, "pp_init: hipStreamCreate failed");

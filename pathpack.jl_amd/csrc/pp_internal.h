@@ -132,6 +132,7 @@ struct pp_sym {
 
 struct pp_ctx {
     int device = 0;
+    int num_cu = 256;                // compute units of the device
     hipStream_t stream = nullptr;
     std::string err;
     int timing = 0;

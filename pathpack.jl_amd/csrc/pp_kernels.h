@@ -136,9 +136,26 @@ __global__ __launch_bounds__(NT) void k_front_small(typename S::value_type *__re
     for (int e = threadIdx.x; e < n * n; e += NT) G[e] = A[e];
 }
 
+// value of v in lane `src` of the wave (src uniform)
+template <class T> __device__ inline T bcast_lane(T v, int src) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int32_t, v), src));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int32_t)(uint32_t)u, src);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int32_t)(uint32_t)(u >> 32), src);
+        return __builtin_bit_cast(T, (uint64_t)lo | ((uint64_t)hi << 32));
+    }
+}
+
 // large fronts, step at pivot `off`: LU of the b x b diagonal block (redundantly in every chunk), then the chunk's
 // rows of the column panel (L <- L U_kk*, right upper non-unit) and columns of the row panel (U <- L_kk* U, left
 // lower unit).
+//
+// The block is padded to NB x NB by repeating its last row and column.  A real entry (i, j < b) only ever meets
+// real entries: the LU updates it with pivots k < min(i, j), and a real unknown j of the solves reads unknowns
+// i < j and block entries D[i, j] with i, j < b.  The padded entries and unknowns hold whatever the same arithmetic
+// gives and are never stored.
 template <class S>
 __global__ __launch_bounds__(NT) void k_front_panel(typename S::value_type *__restrict__ F, const i64 *__restrict__ Foff,
                                                     const int32_t *__restrict__ nn, const int32_t *__restrict__ nj,
@@ -152,32 +169,50 @@ __global__ __launch_bounds__(NT) void k_front_panel(typename S::value_type *__re
     const int b = min(NB, nn[f] - off);
     const int m0 = off + b;
     T *A = F + Foff[f];
-    {
-        const int i = threadIdx.x & 31;
-        for (int j = threadIdx.x >> 5; j < b; j += NT / 32)
-            if (i < b) D[i + j * LD] = A[(off + i) + (i64)(off + j) * n];
-    }
-    __syncthreads();
-    lds_lu<S>(D, b, LD, b);
-    if (chunk == 0) {
-        const int i = threadIdx.x & 31;
-        for (int j = threadIdx.x >> 5; j < b; j += NT / 32)
-            if (i < b) A[(off + i) + (i64)(off + j) * n] = D[i + j * LD];
-    }
-    // pad the factored block to NB x NB with the semiring zero: the solves below then run over all NB columns
-    // without guards.  A real unknown j < b reads only unknowns i < j and D[i, j] with i, j < b; the padded unknowns
-    // (whatever they hold) feed padded unknowns only and are never stored.
-    for (int q = threadIdx.x; q < NB * NB; q += NT) {
-        const int i = q & (NB - 1), j = q / NB;
-        if (i >= b || j >= b) D[i + j * LD] = S::zero();
-    }
-    __syncthreads();
     const int r = m0 + chunk * NT + threadIdx.x;
-    if (r < n) {
-        // row r of the column panel: x <- x U_kk*
-        T x[NB];
+    const bool act = r < n;
+    const int rr = act ? r : n - 1;
+    // all loads are issued before the diagonal LU: the thread's row of the column panel and its column of the row
+    // panel, and wave 0's rows of the block
+    T x[NB], y[NB];
 #pragma unroll
-        for (int j = 0; j < NB; j++) x[j] = A[r + (i64)(off + min(j, b - 1)) * n];   // padded unknowns: any value
+    for (int j = 0; j < NB; j++) x[j] = A[rr + (i64)(off + min(j, b - 1)) * n];
+#pragma unroll
+    for (int i = 0; i < NB; i++) y[i] = A[(off + min(i, b - 1)) + (i64)rr * n];
+    if (threadIdx.x < 64) {
+        // LU of the block in registers (dense/sgetrf.jl:151-175, the operations of lds_lu in the same order): lane i
+        // holds row i (lanes NB.. repeat lanes 0..NB-1), and pivot row k is read from lane k
+        const int i = threadIdx.x & (NB - 1);
+        const int ic = min(i, b - 1);
+        T d[NB];
+#pragma unroll
+        for (int j = 0; j < NB; j++) d[j] = A[(off + ic) + (i64)(off + min(j, b - 1)) * n];
+#pragma unroll
+        for (int k = 0; k < NB; k++) {
+            const bool below = i > k;
+            if (!S::integral) {
+                const T l = S::prod(d[k], S::star(bcast_lane(d[k], k)));
+                d[k] = below ? l : d[k];
+            }
+#pragma unroll
+            for (int j = k + 1; j < NB; j++) {
+                const T v = S::muladd(d[k], bcast_lane(d[j], k), d[j]);
+                d[j] = below ? v : d[j];
+            }
+        }
+        if (threadIdx.x < NB) {
+#pragma unroll
+            for (int j = 0; j < NB; j++) D[i + j * LD] = d[j];
+            if (chunk == 0 && i < b) {
+#pragma unroll
+                for (int j = 0; j < NB; j++)
+                    if (j < b) A[(off + i) + (i64)(off + j) * n] = d[j];
+            }
+        }
+    }
+    __syncthreads();
+    if (act) {
+        // row r of the column panel: x <- x U_kk*
 #pragma unroll
         for (int j = 0; j < NB; j++) {
             T acc = x[j];
@@ -193,9 +228,6 @@ __global__ __launch_bounds__(NT) void k_front_panel(typename S::value_type *__re
         for (int j = 0; j < NB; j++)
             if (j < b) A[r + (i64)(off + j) * n] = x[j];
         // column r of the row panel: y <- L_kk* y
-        T y[NB];
-#pragma unroll
-        for (int i = 0; i < NB; i++) y[i] = A[(off + min(i, b - 1)) + (i64)r * n];
 #pragma unroll
         for (int i = 0; i < NB; i++) {
             T acc = y[i];
@@ -609,20 +641,59 @@ __global__ __launch_bounds__(NT) void k_relabel(const T *__restrict__ X, i64 n, 
 }
 
 // The same with the source column staged in LDS (coalesced read, gather from LDS, coalesced write), for columns of
-// at most RELABEL_LDS bytes; persistent workgroups, one per CU.
+// at most RELABEL_LDS bytes; persistent workgroups, one per CU.  Rows move in 16-byte vectors (n and ldc multiples
+// of the vector width, 16-byte aligned output), and the next column's loads are in flight while the current one is
+// gathered and written.
 constexpr int RELABEL_LDS = 131072;
 constexpr int RELABEL_NT = 1024;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+template <class T> struct Vec16;
+template <> struct Vec16<float> { typedef f32x4 type; typedef i32x4 idx; };
+template <> struct Vec16<double> { typedef f64x2 type; typedef i32x2 idx; };
+template <> struct Vec16<int32_t> { typedef i32x4 type; typedef i32x4 idx; };
 
 template <class T>
 __global__ __launch_bounds__(RELABEL_NT) void k_relabel_lds(const T *__restrict__ X, i64 n, T *__restrict__ C, i64 ldc,
                                                            const int32_t *__restrict__ invp) {
-    __shared__ T col[RELABEL_LDS / sizeof(T)];
-    for (i64 j = blockIdx.x; j < n; j += gridDim.x) {
-        const T *src = X + (i64)invp[j] * n;
-        for (i64 i = threadIdx.x; i < n; i += RELABEL_NT) col[i] = src[i];
+    typedef typename Vec16<T>::type V;
+    typedef typename Vec16<T>::idx I;
+    constexpr int VW = 16 / sizeof(T);
+    constexpr int RV = RELABEL_LDS / 16 / RELABEL_NT;   // vectors per thread and column
+    __shared__ V col[RELABEL_LDS / 16];
+    const T *cs = reinterpret_cast<const T *>(col);
+    const int nv = (int)(n / VW);
+    V buf[RV];
+    auto load = [&](i64 j) {
+        const V *src = reinterpret_cast<const V *>(X + (i64)invp[j] * n);
+#pragma unroll
+        for (int u = 0; u < RV; u++) {
+            const int v = threadIdx.x + u * RELABEL_NT;
+            if (v < nv) buf[u] = __builtin_nontemporal_load(src + v);
+        }
+    };
+    i64 j = blockIdx.x;
+    if (j < n) load(j);
+    for (; j < n; j += gridDim.x) {
+#pragma unroll
+        for (int u = 0; u < RV; u++) {
+            const int v = threadIdx.x + u * RELABEL_NT;
+            if (v < nv) col[v] = buf[u];
+        }
         __syncthreads();
-        T *dst = C + j * ldc;
-        for (i64 i = threadIdx.x; i < n; i += RELABEL_NT) dst[i] = col[invp[i]];
+        if (j + gridDim.x < n) load(j + gridDim.x);
+        V *dst = reinterpret_cast<V *>(C + j * ldc);
+        const I *ip = reinterpret_cast<const I *>(invp);
+        for (int v = threadIdx.x; v < nv; v += RELABEL_NT) {
+            const I p = ip[v];
+            V o;
+            if constexpr (VW == 4) o = V{cs[p.x], cs[p.y], cs[p.z], cs[p.w]};
+            else o = V{cs[p.x], cs[p.y]};
+            __builtin_nontemporal_store(o, dst + v);
+        }
         __syncthreads();
     }
 }
@@ -934,9 +1005,10 @@ template <class S> struct StarRun {
         t2.stop();
         Timer t3(ctx, 3);
         if (n > 0) {
-            if (n * (i64)sizeof(T) <= RELABEL_LDS)
-                k_relabel_lds<T><<<(unsigned)std::min<i64>(n, 512), RELABEL_NT, 0, st>>>(X, n, (T *)out, ldc,
-                                                                                         fac->plan.invp32);
+            constexpr i64 VW = 16 / sizeof(T);
+            if (n * (i64)sizeof(T) <= RELABEL_LDS && n % VW == 0 && ldc % VW == 0 && ((uintptr_t)out & 15) == 0)
+                k_relabel_lds<T><<<(unsigned)std::min<i64>(n, ctx->num_cu), RELABEL_NT, 0, st>>>(X, n, (T *)out, ldc,
+                                                                                                fac->plan.invp32);
             else
                 k_relabel<T><<<(unsigned)n, NT, 0, st>>>(X, n, (T *)out, ldc, fac->plan.invp);
         }
