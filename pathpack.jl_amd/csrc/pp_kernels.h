@@ -51,13 +51,24 @@ __global__ void k_scatter_entries(T *__restrict__ F, const i64 *__restrict__ pos
     for (i64 i = blockIdx.x * (i64)NT + threadIdx.x; i < nnz; i += (i64)gridDim.x * NT) F[pos[i]] = val[i];
 }
 
-// X <- I in the semiring (the start of X <- U*)
-template <class S> __global__ void k_identity(typename S::value_type *__restrict__ X, i64 n) {
+// X <- I in the semiring (the start of X <- U*), on the entries the sweeps read before writing them: column c of
+// panel p over the rows [alo[p], ahi[p]) of its subtree (every forward write into column c comes from a panel of
+// that subtree; the backward sweep takes the other rows of its component as zero), and over the rows outside the
+// component [blo[p], bhi[p]), which no sweep visits.
+template <class S>
+__global__ __launch_bounds__(NT) void k_identity_panels(typename S::value_type *__restrict__ X, i64 n,
+                                                        const int32_t *__restrict__ c0, const int32_t *__restrict__ w,
+                                                        const int32_t *__restrict__ alo, const int32_t *__restrict__ ahi,
+                                                        const int32_t *__restrict__ blo,
+                                                        const int32_t *__restrict__ bhi) {
     typedef typename S::value_type T;
-    for (i64 col = blockIdx.x; col < n; col += gridDim.x) {
-        T *x = X + col * n;
-        for (i64 i = threadIdx.x; i < n; i += NT) x[i] = i == col ? S::one() : S::zero();
-    }
+    const int p = blockIdx.x, j = blockIdx.y;
+    if (j >= w[p]) return;
+    const i64 col = c0[p] + j;
+    T *x = X + col * n;
+    for (i64 i = alo[p] + threadIdx.x; i < ahi[p]; i += NT) x[i] = i == col ? S::one() : S::zero();
+    for (i64 i = threadIdx.x; i < blo[p]; i += NT) x[i] = S::zero();
+    for (i64 i = bhi[p] + threadIdx.x; i < n; i += NT) x[i] = S::zero();
 }
 
 // ===== extend-add: F_f <- F_f (+) inj M_c inj^T for every child c (sgetrf_send!, chordal/sgetrf.jl:257-290) =====
@@ -397,6 +408,9 @@ struct SweepArgs {
     const int32_t *p_c0, *p_w, *p_e, *p_chunks, *row_lo, *row_hi;
     const i64 *p_eoff, *p_poff, *p_doff;
     const int32_t *Eidx;
+    // backward star sweep: the rows [init_lo[p], init_hi[p]) where the forward sweep left panel p's columns; the
+    // other rows of those columns are zero (null: X holds every row, as in the solves)
+    const int32_t *init_lo, *init_hi;
 };
 
 // largest i in [0, np) with pre[i] <= u
@@ -492,17 +506,64 @@ __global__ __launch_bounds__(NT) void k_fwd_scatter(typename S::value_type *__re
 #pragma unroll
     for (int j = 0; j < W; j++) x[j] = j < w ? X[(i64)(c0 + j) * ld + r] : S::zero();
     const int t1 = min(e, (chunk + 1) * SCATTER_T);
-    for (int t = chunk * SCATTER_T + q; t < t1; t += 4) {
-        const T *pc = Pp + (i64)t * W;
-        T v = ATOMIC ? S::zero() : X[(i64)E[t] * ld + r];
-        if (W == 1) {
-            v = S::muladd(x[0], pc[0], v);
-        } else {
+    if (ATOMIC) {
+        for (int t = chunk * SCATTER_T + q; t < t1; t += 4) {
+            const T *pc = Pp + (i64)t * W;
+            T v = S::zero();
+            if (W == 1) {
+                v = S::muladd(x[0], pc[0], v);
+            } else {
 #pragma unroll
-            for (int j = 0; j < W; j += 2) v = S::muladd2(x[j], pc[j], x[j + 1], pc[j + 1], v);
+                for (int j = 0; j < W; j += 2) v = S::muladd2(x[j], pc[j], x[j + 1], pc[j + 1], v);
+            }
+            atomic_plus<S>(X + (i64)E[t] * ld + r, v);
         }
-        if (ATOMIC) atomic_plus<S>(X + (i64)E[t] * ld + r, v);
-        else X[(i64)E[t] * ld + r] = v;
+        return;
+    }
+    // the wave's targets t = tb + 4 i, in groups of four with the next two groups' loads in flight (three register
+    // sets in rotation); the targets of a panel are distinct columns, so a load never meets a pending store.  Loads
+    // past the last target repeat it and are dropped.
+    const int tb = chunk * SCATTER_T + q;
+    if (tb >= t1) return;
+    const int ng = ((t1 - tb + 3) / 4 + 3) / 4;
+    T *xr = X + r;
+    auto ldg = [&](int g, T(&v)[4]) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = xr[(i64)E[min(tb + 4 * (4 * g + u), t1 - 1)] * ld];
+        __builtin_amdgcn_sched_barrier(0);   // issue the loads here, ahead of the arithmetic that follows
+    };
+    auto upd = [&](int g, const T(&v)[4]) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int t = tb + 4 * (4 * g + u);
+            if (t < t1) {
+                const T *pc = Pp + (i64)t * W;
+                T acc = v[u];
+                if (W == 1) {
+                    acc = S::muladd(x[0], pc[0], acc);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < W; j += 2) acc = S::muladd2(x[j], pc[j], x[j + 1], pc[j + 1], acc);
+                }
+                xr[(i64)E[t] * ld] = acc;
+            }
+        }
+    };
+    T A[4], B[4], C[4];
+    ldg(0, A);
+    ldg(1, B);
+    int g = 0;
+    for (; g + 3 <= ng; g += 3) {
+        ldg(g + 2, C);
+        upd(g, A);
+        ldg(g + 3, A);
+        upd(g + 1, B);
+        ldg(g + 4, B);
+        upd(g + 2, C);
+    }
+    if (g < ng) {
+        upd(g, A);
+        if (g + 1 < ng) upd(g + 1, B);
     }
 }
 
@@ -542,15 +603,14 @@ __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(siz
     const T *Qp = Q + a.p_poff[p];
     const int32_t *E = a.Eidx + a.p_eoff[p];
     T acc[W];
-    if (q == 0) {
+#pragma unroll
+    for (int j = 0; j < W; j++) acc[j] = S::zero();
+    if (q == 0 && (!a.init_lo || (r >= a.init_lo[p] && r < a.init_hi[p]))) {
 #pragma unroll
         for (int j = 0; j < W; j++) {
             const T v = xr[(i64)(c0 + min(j, w - 1)) * ld];
             acc[j] = j < w ? v : S::zero();
         }
-    } else {
-#pragma unroll
-        for (int j = 0; j < W; j++) acc[j] = S::zero();
     }
     // this wave's share of the gather list, in groups of four columns, with the next two groups' loads in flight
     // (three register sets used in rotation, so no copy waits on a load); the lookahead reads up to eight entries
@@ -966,6 +1026,8 @@ static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmod
         a.p_poff = d.p_poff;
         a.p_doff = d.p_doff;
         a.Eidx = d.Eidx;
+        a.init_lo = star_rows ? d.p_rowA_lo : nullptr;
+        a.init_hi = star_rows ? d.p_rowA_hi : nullptr;
         const bool atomic = !star_rows;
         switch (li.cls) {
         case 0: launch_list<S, 1>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
@@ -994,7 +1056,11 @@ template <class S> struct StarRun {
         T *X = nullptr;
         HIPCHK(hipMallocAsync((void **)&X, std::max<i64>(1, n * n) * sizeof(T), st));
         Timer t1(ctx, 1);
-        if (n > 0) k_identity<S><<<(unsigned)std::min<i64>(n, 65536), NT, 0, st>>>(X, n);
+        const DevPlan &d = fac->plan;
+        const i64 np = fac->sym->splan->np;
+        if (np > 0)
+            k_identity_panels<S><<<dim3((unsigned)np, PANEL_W), NT, 0, st>>>(X, n, d.p_c0, d.p_w, d.p_rowA_lo,
+                                                                           d.p_rowA_hi, d.p_rowB_lo, d.p_rowB_hi);
         LAUNCHCHK();
         std::string e = run_sweeps<S>(ctx, fac, true, 0, X, n, true, n, fac->Upack);
         if (!e.empty()) return e;

@@ -199,6 +199,22 @@ def random_digraph(n: int, p: float, seed: int, lo: int = 1, hi: int = 100, dtyp
     return from_arcs(n, src, dst, w, "min", f"digraph{n}")
 
 
+def disjoint_union(parts: list[Graph], isolated: int = 0, seed: int = SEED_BASE, name: str = "") -> Graph:
+    """The disjoint union of ``parts`` plus ``isolated`` vertices without arcs, with the vertices relabelled by a
+    seeded permutation so that the components interleave."""
+    n = sum(g.n for g in parts) + isolated
+    lab = np.argsort(uniform_float(seed, n), kind="stable")
+    src, dst, w, base = [], [], [], 0
+    for g in parts:
+        cols = np.repeat(np.arange(g.n), np.diff(g.colptr))
+        src.append(lab[base + g.rowval])
+        dst.append(lab[base + cols])
+        w.append(g.nzval)
+        base += g.n
+    dtype = parts[0].nzval.dtype if parts else np.float64
+    return from_arcs(n, np.concatenate(src), np.concatenate(dst), np.concatenate(w).astype(dtype), "min", name)
+
+
 def dense_minplus(rows: int, cols: int, seed: int, inf_frac: float = 0.1, lo: int = 0, hi: int = 1000,
                   dtype=np.float32) -> np.ndarray:
     """Column-major (Fortran order) matrix of uniform integers in [lo, hi] with a fraction ``inf_frac`` set to

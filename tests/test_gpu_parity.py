@@ -34,6 +34,8 @@ def graphs():
         "grid17x13": W.grid((17, 13)),
         "grid6x7x5": W.grid((6, 7, 5)),
         "rgg700": W.rgg(700, seed=21),
+        "components": W.disjoint_union([W.grid((9, 7)), W.random_digraph(60, 0.05, 4), W.rgg(200, seed=5),
+                                        W.grid((3, 4, 2))], isolated=5, name="components"),
     }
 
 

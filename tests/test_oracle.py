@@ -68,6 +68,19 @@ def test_oracle_star_vs_floyd_warshall(n, p, seed, s):
         assert_star_equal(s, C, ref)
 
 
+@pytest.mark.parametrize("s", [O.MINPLUS, O.MAXMIN, O.ORAND, O.PLUSPROD])
+def test_oracle_star_of_disconnected_graph(s):
+    """Eleven components (grids, a random digraph, a geometric graph, isolated vertices) with interleaved labels:
+    entries between components are the semiring zero."""
+    dtype = dtype_for(s)
+    g = weighted(W.disjoint_union([W.grid((9, 7)), W.random_digraph(60, 0.05, 4), W.rgg(200, seed=5),
+                                   W.grid((3, 4, 2))], isolated=5), s, dtype)
+    ref = O.plusprod_inverse(g.dense(0.0)) if s == O.PLUSPROD else O.floyd_warshall(s, g.dense(O.zero(s, dtype)))
+    sym = P.symbolic(g)
+    C = O.star(O.factor(s, oracle_sym(sym), g.colptr, g.rowval, g.nzval))
+    assert_star_equal(s, C, ref)
+
+
 def readme_graph():
     """sparse([1, 1, 2, 3, 4, 4], [2, 3, 4, 2, 1, 5], [3.0, 8.0, 1.0, 4.0, 2.0, 7.0], 5, 5) (README.md:73)."""
     return W.from_arcs(5, np.array([1, 1, 2, 3, 4, 4]) - 1, np.array([2, 3, 4, 2, 1, 5]) - 1,
