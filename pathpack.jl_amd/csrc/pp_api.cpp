@@ -5,9 +5,11 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdio>
 #include <cstring>
 #include <new>
 #include <string>
+#include <thread>
 
 #include "../../include/pathpack_hip.h"
 #include "pp_internal.h"
@@ -35,7 +37,8 @@ pp_sym::~pp_sym() {
 }
 
 pp_fac::~pp_fac() {
-    for (void *p : plan.owned) hipFree(p);   // one block: the plans and the factor arrays
+    // one block (stream-ordered pool of the context's stream): the plans and the factor arrays
+    for (void *p : plan.owned) hipFreeAsync(p, ctx->stream);
 }
 
 static bool supported(int semiring, int dtype) {
@@ -194,26 +197,24 @@ pp_status pp_sym_destroy(pp_sym *sym) {
 
 // ===== factor =====
 
+// The factor and sweep plans of a structure (a cache of the immutable structure), built on two threads.
 static std::string ensure_plans(const pp_sym *csym) {
-    pp_sym *sym = const_cast<pp_sym *>(csym);   // plans are a cache of the immutable structure
-    if (!sym->fplan) {
-        auto *f = new pp::FactorPlan;
-        std::string e = pp::build_factor_plan(sym->S, *f);
-        if (!e.empty()) {
-            delete f;
-            return e;
-        }
-        sym->fplan = f;
+    pp_sym *sym = const_cast<pp_sym *>(csym);
+    if (sym->fplan && sym->splan) return "";
+    auto *f = sym->fplan ? nullptr : new pp::FactorPlan;
+    auto *s = sym->splan ? nullptr : new pp::SweepPlan;
+    std::string ef, es;
+    std::thread t;
+    if (s) t = std::thread([&] { es = pp::build_sweep_plan(sym->S, *s); });
+    if (f) ef = pp::build_factor_plan(sym->S, *f);
+    if (t.joinable()) t.join();
+    if (!ef.empty() || !es.empty()) {
+        delete f;
+        delete s;
+        return ef.empty() ? es : ef;
     }
-    if (!sym->splan) {
-        auto *s = new pp::SweepPlan;
-        std::string e = pp::build_sweep_plan(sym->S, *sym->fplan, *s);
-        if (!e.empty()) {
-            delete s;
-            return e;
-        }
-        sym->splan = s;
-    }
+    if (f) sym->fplan = f;
+    if (s) sym->splan = s;
     return "";
 }
 
@@ -317,7 +318,7 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *sym, int semiring, int
     for (const Part &q : parts)
         if (q.bytes) std::memcpy((char *)ctx->staging + q.off, q.src, q.bytes);
     void *block = nullptr;
-    if (hipMalloc(&block, total) != hipSuccess) {
+    if (hipMallocAsync(&block, total, st) != hipSuccess) {
         delete fac;
         return fail(ctx, PP_ENOMEM, "pp_factor: hipMalloc of the factor failed");
     }

@@ -100,7 +100,7 @@ struct SweepPlan {
 };
 
 std::string build_factor_plan(const Symbolic &S, FactorPlan &P);
-std::string build_sweep_plan(const Symbolic &S, const FactorPlan &F, SweepPlan &P);
+std::string build_sweep_plan(const Symbolic &S, SweepPlan &P);
 
 // Device copies of the plans.
 struct DevPlan {

@@ -131,7 +131,7 @@ std::string build_factor_plan(const Symbolic &S, FactorPlan &P) {
     return "";
 }
 
-std::string build_sweep_plan(const Symbolic &S, const FactorPlan &F, SweepPlan &P) {
+std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
     const i64 nf = S.nf;
     // panels
     std::vector<i64> first(nf), last(nf);
@@ -156,7 +156,7 @@ std::string build_sweep_plan(const Symbolic &S, const FactorPlan &F, SweepPlan &
     std::vector<i64> root(nf);
     for (i64 f = nf - 1; f >= 0; f--) root[f] = S.parent[f] >= 0 ? root[S.parent[f]] : f;
     for (i64 f = 0; f < nf; f++) {
-        const i64 Rp = S.Rptr[f], nn = F.nn[f], nj = F.nj[f];
+        const i64 Rp = S.Rptr[f], nn = S.Rptr[f + 1] - Rp, nj = nn + (S.Sptr[f + 1] - S.Sptr[f]);
         first[f] = P.np;
         for (i64 k = 0; k * PANEL_W < nn; k++) {
             const i64 c0 = Rp + k * PANEL_W, w = std::min<i64>(PANEL_W, nn - k * PANEL_W);
@@ -187,12 +187,10 @@ std::string build_sweep_plan(const Symbolic &S, const FactorPlan &F, SweepPlan &
     P.Eidx.insert(P.Eidx.end(), EIDX_PAD, 0);
     // forward levels (leaves to root) and backward levels (root to leaves)
     std::vector<i64> lvA(P.np, 0), lvB(P.np, 0);
-    std::vector<i64> endA(nf, -1);
+    std::vector<i64> baseA(nf, 0);   // fronts are in postorder: a front's children come before it
     for (i64 f = 0; f < nf; f++) {
-        i64 base = 0;
-        for (i64 q = F.chptr[f]; q < F.chptr[f + 1]; q++) base = std::max(base, endA[F.chidx[q]] + 1);
-        for (i64 p = first[f]; p <= last[f]; p++) lvA[p] = base + (p - first[f]);
-        endA[f] = lvA[last[f]];
+        for (i64 p = first[f]; p <= last[f]; p++) lvA[p] = baseA[f] + (p - first[f]);
+        if (S.parent[f] >= 0) baseA[S.parent[f]] = std::max(baseA[S.parent[f]], lvA[last[f]] + 1);
     }
     std::vector<i64> endB(nf, -1);   // level of the front's first panel (the last one visited)
     for (i64 f = nf - 1; f >= 0; f--) {

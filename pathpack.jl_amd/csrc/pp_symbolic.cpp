@@ -25,6 +25,26 @@ struct Adj {
     std::vector<i32> adj;
 };
 
+// Threads for the host analysis: up to 16 (PP_SYMBOLIC_THREADS overrides), one for small graphs.
+int analysis_threads(i64 n) {
+    int threads = (int)std::min<unsigned>(16, std::max(1u, std::thread::hardware_concurrency()));
+    if (const char *e = std::getenv("PP_SYMBOLIC_THREADS")) threads = std::max(1, std::atoi(e));
+    return n < 20000 ? 1 : threads;
+}
+
+// fn(lo, hi) over [0, count) in contiguous blocks on `threads` threads (the caller's thread takes the first block)
+template <class Fn> void parallel_for(i64 count, int threads, Fn fn) {
+    threads = (int)std::max<i64>(1, std::min<i64>(threads, count / 1024));
+    if (threads <= 1) {
+        fn((i64)0, count);
+        return;
+    }
+    std::vector<std::thread> pool;
+    for (int t = 1; t < threads; t++) pool.emplace_back([&, t] { fn(count * t / threads, count * (t + 1) / threads); });
+    fn((i64)0, count / threads);
+    for (auto &th : pool) th.join();
+}
+
 // Symmetric pattern of A without the diagonal, neighbours sorted.
 std::string symmetrize(i64 n, const i64 *colptr, const i64 *rowval, Adj &G) {
     if (n < 0 || n > (i64)0x7fffffff) return "n out of range";
@@ -94,6 +114,7 @@ struct ND {
                                    order(g.n, -1) {}
 
     // BFS inside item id from root; returns the number of levels; fills queue[0..cnt) and level[]
+    std::atomic<i64> bfs_work{0};
     int bfs(std::vector<i32> &queue, i32 id, i32 root, i64 &cnt, std::vector<i64> &lptr) {
         lptr.clear();
         cnt = 0;
@@ -115,6 +136,7 @@ struct ND {
         for (i64 k = 1; k < cnt; k++)
             if (level[queue[k]] != level[queue[k - 1]]) lptr.push_back(k);
         lptr.push_back(cnt);
+        bfs_work += cnt;
         nlev = (int)lptr.size() - 1;
         return nlev;
     }
@@ -338,12 +360,16 @@ struct ND {
         for (int t = 1; t < nthreads; t++) pool.emplace_back(work);
         work();
         for (auto &th : pool) th.join();
+        if (std::getenv("PP_NDDBG")) std::fprintf(stderr, "bfs work %ld\n", (long)bfs_work.load());
     }
 };
 
 // ===== elimination tree and postorder (Liu 1986, path compression) =====
 
-void etree_postorder(const Adj &G, const std::vector<i64> &perm, std::vector<i64> &post_perm) {
+// post_perm: a postorder of the elimination tree of perm (the children of a node in increasing order);
+// post_parent: the elimination tree in the postorder's labels.
+void etree_postorder(const Adj &G, const std::vector<i64> &perm, std::vector<i64> &post_perm,
+                     std::vector<i64> &post_parent) {
     const i64 n = G.n;
     std::vector<i64> invp(n);
     for (i64 k = 0; k < n; k++) invp[perm[k]] = k;
@@ -374,6 +400,7 @@ void etree_postorder(const Adj &G, const std::vector<i64> &perm, std::vector<i64
         }
     post_perm.clear();
     post_perm.reserve(n);
+    std::vector<i64> post(n);   // postorder label of each label of perm
     std::vector<i64> stack;
     for (i64 r = 0; r < n; r++) {
         if (parent[r] != -1) continue;
@@ -386,10 +413,14 @@ void etree_postorder(const Adj &G, const std::vector<i64> &perm, std::vector<i64
                 stack.push_back(c);
             } else {
                 stack.pop_back();
+                post[v] = (i64)post_perm.size();
                 post_perm.push_back(perm[v]);
             }
         }
     }
+    post_parent.assign(n, -1);
+    for (i64 j = 0; j < n; j++)
+        if (parent[j] >= 0) post_parent[post[j]] = post[parent[j]];
 }
 
 // ===== column counts of L (Gilbert, Ng & Peyton, "An efficient algorithm to compute row and column counts for
@@ -401,29 +432,10 @@ void etree_postorder(const Adj &G, const std::vector<i64> &perm, std::vector<i64
 // previous leaf (found with a disjoint-set forest over the nodes already visited); each leaf of the tree counts 1
 // and each non-root node subtracts 1 from its parent.  The column count of j (with the diagonal) is then the sum of
 // these weights over the subtree of j.  O(nnz(A) a(n)).
-void column_counts(const Adj &G, const std::vector<i64> &perm, std::vector<i64> &parent, std::vector<i64> &cc) {
+void column_counts(const Adj &G, const std::vector<i64> &perm, const std::vector<i64> &parent, std::vector<i64> &cc) {
     const i64 n = G.n;
     std::vector<i64> invp(n);
     for (i64 k = 0; k < n; k++) invp[perm[k]] = k;
-    // elimination tree in the new labels
-    parent.assign(n, -1);
-    std::vector<i64> anc(n, -1);
-    for (i64 j = 0; j < n; j++) {
-        const i64 v = perm[j];
-        for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) {
-            i64 r = invp[G.adj[p]];
-            if (r >= j) continue;
-            while (anc[r] != -1 && anc[r] != j) {
-                const i64 t = anc[r];
-                anc[r] = j;
-                r = t;
-            }
-            if (anc[r] == -1) {
-                anc[r] = j;
-                parent[r] = j;
-            }
-        }
-    }
     // first descendant of every node (labels are a postorder, so a subtree is the range [first[j], j])
     std::vector<i64> first(n, -1);
     for (i64 k = 0; k < n; k++)
@@ -577,56 +589,43 @@ std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, st
         out.Dptr[f + 1] = out.Dptr[f] + nn * nn;
         out.Lptr[f + 1] = out.Lptr[f] + nn * na;
     }
-    // where each stored entry lands: the front of min(i, j) (new labels), local positions in its bag.  Front by
-    // front with a position map of its bag: the entries of its residual's columns (row in the bag), then -- through
-    // the transpose -- those of its residual's rows whose column lies in its separator.
+    // where each stored entry (i, j) lands (new labels): the front f of min(i, j), at the local positions of i and j
+    // in bag(f) = res(f) then sep(f) (a separator position by binary search in the sorted sep(f)); in parallel over
+    // the columns of A
     out.nnz = colptr[n];
     out.entry_front.resize(out.nnz);
     out.entry_row.resize(out.nnz);
     out.entry_col.resize(out.nnz);
-    std::vector<i64> rowptr(n + 1, 0);
-    for (i64 p = 0; p < out.nnz; p++) rowptr[rowval[p] + 1]++;
-    for (i64 i = 0; i < n; i++) rowptr[i + 1] += rowptr[i];
-    std::vector<i64> rowent(out.nnz), fill(rowptr.begin(), rowptr.end() - 1);
-    for (i64 c = 0; c < n; c++)
-        for (i64 p = colptr[c]; p < colptr[c + 1]; p++) rowent[fill[rowval[p]]++] = p;   // CSC position, by row
-    std::vector<i64> colof(out.nnz);
-    for (i64 c = 0; c < n; c++)
-        for (i64 p = colptr[c]; p < colptr[c + 1]; p++) colof[p] = c;
-    std::vector<int32_t> pos(n, -1);
-    i64 placed = 0;
-    for (i64 f = 0; f < nf; f++) {
-        const i64 r0 = out.Rptr[f], r1 = out.Rptr[f + 1], nn = r1 - r0;
-        const i64 s0 = out.Sptr[f], s1 = out.Sptr[f + 1];
-        for (i64 v = r0; v < r1; v++) pos[v] = (int32_t)(v - r0);
-        for (i64 q = s0; q < s1; q++) pos[out.Stgt[q]] = (int32_t)(nn + q - s0);
-        for (i64 j = r0; j < r1; j++) {
-            const i64 c = out.perm[j];
-            for (i64 p = colptr[c]; p < colptr[c + 1]; p++) {   // entry (i, j): front f when i >= r0
+    std::vector<i32> fof(n);
+    for (i64 f = 0; f < nf; f++)
+        for (i64 v = out.Rptr[f]; v < out.Rptr[f + 1]; v++) fof[v] = (i32)f;
+    std::atomic<bool> outside(false);
+    parallel_for(n, analysis_threads(n), [&](i64 c0, i64 c1) {
+        for (i64 c = c0; c < c1; c++) {
+            const i64 j = out.invp[c];
+            for (i64 p = colptr[c]; p < colptr[c + 1]; p++) {
                 const i64 i = out.invp[rowval[p]];
-                if (i < r0) continue;
-                if (pos[i] < 0) return "an entry of A falls outside the structure";
+                const i64 lo = std::min(i, j), hi = std::max(i, j);
+                const i64 f = fof[lo], r0 = out.Rptr[f], r1 = out.Rptr[f + 1];
+                i64 lhi;
+                if (hi < r1) {
+                    lhi = hi - r0;
+                } else {
+                    const i64 *s0 = out.Stgt.data() + out.Sptr[f], *s1 = out.Stgt.data() + out.Sptr[f + 1];
+                    const i64 *q = std::lower_bound(s0, s1, hi);
+                    if (q == s1 || *q != hi) {
+                        outside = true;
+                        continue;
+                    }
+                    lhi = (r1 - r0) + (q - s0);
+                }
                 out.entry_front[p] = f;
-                out.entry_row[p] = pos[i];
-                out.entry_col[p] = (i32)(j - r0);
-                placed++;
-            }
-            const i64 orow = out.perm[j];   // entries (j, i) with i after the residual: front f
-            for (i64 q = rowptr[orow]; q < rowptr[orow + 1]; q++) {
-                const i64 p = rowent[q];
-                const i64 i = out.invp[colof[p]];
-                if (i < r1) continue;
-                if (pos[i] < 0) return "an entry of A falls outside the structure";
-                out.entry_front[p] = f;
-                out.entry_row[p] = (i32)(j - r0);
-                out.entry_col[p] = pos[i];
-                placed++;
+                out.entry_row[p] = (i32)(i == lo ? lo - r0 : lhi);
+                out.entry_col[p] = (i32)(j == lo ? lo - r0 : lhi);
             }
         }
-        for (i64 v = r0; v < r1; v++) pos[v] = -1;
-        for (i64 q = s0; q < s1; q++) pos[out.Stgt[q]] = -1;
-    }
-    if (placed != out.nnz) return "internal error: entries not placed";
+    });
+    if (outside) return "an entry of A falls outside the structure";
     stage("  entries", ts);
     work_counts(n, out.Rptr, out.Sptr, out.parent, out.madds_factor, out.madds_star, out.madds_rhs, out.nnzL);
     return "";
@@ -669,10 +668,7 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
     std::vector<i64> perm0(n);
     if (opts.ordering == 0) {
         ND nd(G, opts.nd_leaf);
-        int threads = (int)std::min<unsigned>(16, std::max(1u, std::thread::hardware_concurrency()));
-        if (const char *e = std::getenv("PP_SYMBOLIC_THREADS")) threads = std::max(1, std::atoi(e));
-        if (n < 20000) threads = 1;
-        nd.run(threads);
+        nd.run(analysis_threads(n));
         perm0 = nd.order;
     } else if (opts.ordering == 1) {
         std::iota(perm0.begin(), perm0.end(), 0);
@@ -689,12 +685,12 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
     double ts = t0;
     stage("symmetrize + order", ts);
     // 2. postordered elimination tree
-    std::vector<i64> perm1;
-    etree_postorder(G, perm0, perm1);
+    std::vector<i64> perm1, pcol;
+    etree_postorder(G, perm0, perm1, pcol);
     stage("etree + postorder", ts);
     // 3. column counts, then fundamental supernodes: j + 1 continues j's supernode when it is j's parent, has no
     //    other child, and its column holds exactly one entry fewer
-    std::vector<i64> pcol, ccol;
+    std::vector<i64> ccol;
     column_counts(G, perm1, pcol, ccol);
     std::vector<i64> nchild(n, 0);
     for (i64 j = 0; j < n; j++)
