@@ -7,8 +7,13 @@ supernodes), the device factorization and the device star, with A's values alrea
 HBM.  `value` is semiring Gop/s = 1e-9 * madds_alg / step seconds, where madds_alg is the multiply-add count of the
 exact (unamalgamated) factor of the same ordering (the reference's per-front formulas).  One JSON line on stdout.
 
-Other configurations (--config 1, 4, 5, gemm, getrf) are the other workloads of the benchmark suite; the default is the
-headline one.
+Other configurations of the benchmark suite (one JSON line each, same keys):
+    --config 1    MinPlus mstar, directed 64 x 64 grid, Float64 (wall time of a small case)
+    --config 2a   dense MinPlus GEMM C <- min(C, A + B), 8192^3, Float32 (pp_sgemx; % of VALU peak)
+    --config 2b   batched front LU + stars, 16384 fronts of 64 x 64, Float32 (pp_getrf_star_batched)
+    --config 4    MaxMin lmul! of 1024 unit columns on a random geometric graph, n = 65536, Float32
+    --config 5    PlusProd rmul! of 512 unit rows on the directed 256 x 256 grid, Float64
+The default is the headline configuration 3.
 """
 
 from __future__ import annotations
@@ -30,12 +35,41 @@ for sub in ("pathpack.jl_amd", "oracle"):
 import pathpack_hip as P  # noqa: E402
 from pathpack_hip import workloads as W  # noqa: E402
 
-VALU_PEAK_MADD = 26.2e12   # MinPlus f32: 2 v_add_f32 + 1 v_min3_f32 per 2 multiply-adds; 256 CU x 4 SIMD x 16 x 2.4 GHz
+# MI355X published FP32 vector rate: 157.3 TFLOP/s = 78.6e12 lane FMAs/s (256 CU x 4 SIMD x 32 lanes x 2.4 GHz), one
+# full-rate VALU instruction per lane and clock.  A MinPlus / MaxPlus Float32 multiply-add costs 1.5 such instructions
+# (v_add_f32, v_add_f32, v_min3_f32 per two; packed FP32 is not used), so the VALU peak is 52.4e12 madds/s.  The VALU
+# probe (--calibrate-valu) runs the compiled two-madd sequence at 63.8e12 lane instructions/s (81 % of 78.6e12).
+VALU_PEAK_MADD = 78.6e12 / 1.5
 HBM_PEAK = 8.0e12
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per mstar of a kernel family, from the committed rocprofv3 --pmc summary (a line
+    `traffic_bytes_per_star <kernel> <bytes>`), or None."""
+    try:
+        with open(os.path.join(PROFILES, "memory_traffic_mstar_minplus_grid32x32x32.md")) as f:
+            for line in f:
+                parts = line.replace("`", " ").split()
+                if len(parts) == 3 and parts[0] == "traffic_bytes_per_star" and parts[1] == kernel:
+                    return float(parts[2])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def factor_device(s, sym, dnz, ctx):
+    """mlu with the values already in HBM (pp_factor_device)."""
+    import ctypes
+
+    h = ctypes.c_void_p()
+    dt = {np.dtype(np.float32): 0, np.dtype(np.float64): 1, np.dtype(np.int32): 2}[dnz.dtype]
+    ctx.check(P.lib().pp_factor_device(ctx.handle, sym.handle, s.id, dt, ctypes.c_void_p(dnz.ptr), ctypes.byref(h)))
+    return P.Factorization(s, sym, dnz.dtype, h, ctx)
 
 
 def step_mstar(g, dnz, out, ctx, timing):
@@ -44,11 +78,7 @@ def step_mstar(g, dnz, out, ctx, timing):
     t0 = time.perf_counter()
     sym = P.symbolic(g)
     t1 = time.perf_counter()
-    import ctypes
-
-    h = ctypes.c_void_p()
-    ctx.check(P.lib().pp_factor_device(ctx.handle, sym.handle, 0, 0, ctypes.c_void_p(dnz.ptr), ctypes.byref(h)))
-    F = P.Factorization(P.MinPlus(), sym, np.float32, h, ctx)
+    F = factor_device(P.MinPlus(), sym, dnz, ctx)
     t2 = time.perf_counter()
     ph_f = ctx.timing() if timing else None
     P.Matrix(F, out=out)
@@ -99,17 +129,12 @@ def cpu_baseline(g, sym, budget_s=15.0):
 
 
 def bench_mstar(args):
-    cfg = args.config
+    cfg = int(args.config)
     g = W.config_graph(cfg)
-    if cfg == 1:
-        g = g.astype(np.float64)
     ctx = P.context(0)
     ctx.set_timing(args.timing)
     dnz = P.DeviceArray.from_numpy(np.ascontiguousarray(g.nzval).reshape(-1, 1))
     out = P.DeviceArray((g.n, g.n), g.nzval.dtype)
-    assert g.nzval.dtype == np.float32 or cfg == 1
-    if cfg == 1:
-        raise SystemExit("--config 1 is Float64; use the parity tests")
     log(f"bench: {g.name} n={g.n} nnz={g.nnz} warmup={args.warmup} steps={args.steps}")
     for i in range(args.warmup):
         t, sym, ph, F = step_mstar(g, dnz, out, ctx, args.timing)
@@ -127,8 +152,16 @@ def bench_mstar(args):
     madds = st["madds_factor_alg"] + st["madds_star_alg"]
     value = madds / T / 1e9
     ph = {k: float(np.mean([p[k] for p in phases])) for k in phases[0]}
+    if cfg == 3:
+        metric = "mstar sec + semiring Gop/s, MinPlus 3D grid n=32768; % VALU/HBM roofline"
+        workload = (f"MinPlus mstar, directed 32x32x32 grid, n=32768, 6-neighbour arcs both ways, "
+                    f"weights U{{1..100}} Float32 (SplitMix64 seed 0x5EED+3); star left in HBM")
+    else:
+        metric = "mstar sec + semiring Gop/s, MinPlus 2D grid n=4096 (Float64)"
+        workload = (f"MinPlus mstar, directed 64x64 grid, n=4096, 4-neighbour arcs both ways, weights U{{1..100}} "
+                    f"Float64 (SplitMix64 seed 0x5EED+1); star left in HBM")
     result = {
-        "metric": "mstar sec + semiring Gop/s, MinPlus 3D grid n=32768; % VALU/HBM roofline",
+        "metric": metric,
         "value": round(value, 2),
         "unit": "semiring Gop/s",
         "n_gpus": 1,
@@ -138,27 +171,27 @@ def bench_mstar(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32" if g.nzval.dtype == np.float32 else "f64",
         "data": "synthetic",
-        "config": {"workload": f"MinPlus mstar, directed 32x32x32 grid, n=32768, 6-neighbour arcs both ways, "
-                               f"weights U{{1..100}} Float32 (SplitMix64 seed 0x5EED+3); star left in HBM",
+        "config": {"workload": workload,
                    "n": g.n, "nnz": g.nnz, "fronts": sym.nf, "madds_alg": madds,
                    "madds_executed": st["madds_factor"] + st["madds_star"], "nnzL_alg": st["nnzL_alg"],
                    "mstar_s": round(T, 5)},
         "phases_ms": {k: round(v * 1e3, 3) for k, v in ph.items()},
     }
-    if args.timing:
+    if args.timing and cfg == 3:
         # dominant kernel family: the X <- X L* sweep (k_sweep_bwd); algorithmic work n * nnz(L) madds
         n = g.n
         lstar_madds = n * st["nnzL_alg"]
         t_l = ph["star_Lstar_s"]
         ach = lstar_madds / t_l
         result["roofline"] = {"bound": "valu", "kernel": "k_sweep_bwd (X <- X L*, all launches of one star)",
-                              "achieved": round(ach / 1e12, 4), "peak": VALU_PEAK_MADD / 1e12, "unit": "Tmadd/s",
-                              "frac": round(ach / VALU_PEAK_MADD, 4), "traffic": None,
+                              "achieved": round(ach / 1e12, 4), "peak": round(VALU_PEAK_MADD / 1e12, 2),
+                              "unit": "Tmadd/s", "frac": round(ach / VALU_PEAK_MADD, 4),
+                              "traffic": measured_traffic("k_sweep_bwd"),
                               "algorithmic_madds": lstar_madds, "seconds": round(t_l, 6),
                               "output_floor_GBps": round(4.0 * n * n / T / 1e9, 1)}
-    if not args.no_cpu:
+    if not args.no_cpu and cfg == 3:
         cb = cpu_baseline(g, sym, budget_s=args.cpu_budget)
         result["cpu_baseline"] = {"value": round(madds / cb["est_mstar_s"] / 1e9, 3), "unit": "semiring Gop/s",
                                   "cores": cb["threads"], "kind": "port",
@@ -171,19 +204,205 @@ def bench_mstar(args):
     print(json.dumps(result), flush=True)
 
 
+def timed(fn, ctx, steps, warmup):
+    """Mean seconds of fn() over `steps` calls after `warmup` calls, each bracketed by stream synchronisation."""
+    for _ in range(warmup):
+        fn()
+    ctx.synchronize()
+    ts = []
+    for _ in range(steps):
+        ctx.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        ctx.synchronize()
+        ts.append(time.perf_counter() - t0)
+    return float(np.mean(ts))
+
+
+def base_result(args, metric, value, unit, T, dtype, workload, extra):
+    r = {"metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": args.steps,
+         "warmup": args.warmup, "ms_per_step": round(T * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+         "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": {"workload": workload}}
+    r["config"].update(extra)
+    return r
+
+
+def bench_gemm(args):
+    """2a: C <- min(C, A + B), M = N = K = 8192, Float32, A/B/C ~ U{0..1000} with 10 % +Inf."""
+    import ctypes
+    import oracle as O
+
+    N = 8192
+    seed = W.SEED_BASE + 2
+    A = W.dense_minplus(N, N, seed)
+    B = W.dense_minplus(N, N, seed + 10)
+    C = W.dense_minplus(N, N, seed + 20)
+    ctx = P.context(0)
+    dA, dB, dC = P.DeviceArray.from_numpy(A), P.DeviceArray.from_numpy(B), P.DeviceArray.from_numpy(C)
+
+    def run():
+        ctx.check(P.lib().pp_sgemx(ctx.handle, 0, 0, N, N, N, ctypes.c_void_p(dA.ptr), N, ctypes.c_void_p(dB.ptr), N,
+                                   ctypes.c_void_p(dC.ptr), N))
+
+    T = timed(run, ctx, args.steps, args.warmup)
+    madds = float(N) ** 3
+    r = base_result(args, "semiring GEMM Gop/s, MinPlus 8192^3 Float32; % VALU roofline", madds / T / 1e9,
+                    "semiring Gop/s", T, "f32",
+                    "dense MinPlus GEMM C <- min(C, A + B), M=N=K=8192, entries U{0..1000} with 10% +Inf "
+                    "(SplitMix64 seeds 0x5EED+2, +12, +22), operands in HBM", {"m": N, "n": N, "k": N})
+    r["roofline"] = {"bound": "valu", "kernel": "k_gemm_tiled<MinPlus<float>, 8, 8>", "achieved": round(madds / T / 1e12, 3),
+                     "peak": round(VALU_PEAK_MADD / 1e12, 2), "unit": "Tmadd/s", "frac": round(madds / T / VALU_PEAK_MADD, 4),
+                     "traffic": None}
+    if not args.no_cpu:
+        # the oracle's OpenMP GEMM on a 1024 x 1024 block of C with the full K
+        mb = 1024
+        t0 = time.perf_counter()
+        O.sgemx(O.MINPLUS, np.asfortranarray(A[:mb, :]), np.asfortranarray(B[:, :mb]), np.asfortranarray(C[:mb, :mb]))
+        tc = time.perf_counter() - t0
+        r["cpu_baseline"] = {"value": round(float(mb) * mb * N / tc / 1e9, 3), "unit": "semiring Gop/s",
+                             "cores": O.num_threads(), "kind": "port",
+                             "sample": f"oracle sgemx on a {mb}x{mb} block of C with K={N} ({tc:.1f} s)"}
+    print(json.dumps(r), flush=True)
+
+
+def bench_getrf(args):
+    """2b: 16384 independent 64 x 64 Float32 fronts: LU + L* + U* (pp_getrf_star_batched)."""
+    import ctypes
+    import oracle as O
+
+    nb, batch = 64, 16384
+    seed = W.SEED_BASE + 2
+    A3 = np.asfortranarray(W.dense_minplus(nb, nb * batch, seed + 30)).reshape(nb, nb, batch, order="F")
+    idx = np.arange(nb)
+    A3[idx, idx, :] = 0.0   # front b is A3[:, :, b]; its diagonal is 0
+    A = A3.reshape(nb, nb * batch, order="F")
+    ctx = P.context(0)
+    d0 = P.DeviceArray.from_numpy(A)
+    dA = P.DeviceArray(A.shape, np.float32)
+    dL = P.DeviceArray(A.shape, np.float32)
+    dU = P.DeviceArray(A.shape, np.float32)
+
+    def run():
+        ctx.check(P.lib().pp_copy(ctx.handle, ctypes.c_void_p(dA.ptr), ctypes.c_void_p(d0.ptr), dA.nbytes))
+        ctx.check(P.lib().pp_getrf_star_batched(ctx.handle, 0, 0, nb, batch, ctypes.c_void_p(dA.ptr),
+                                                ctypes.c_void_p(dL.ptr), ctypes.c_void_p(dU.ptr)))
+
+    T = timed(run, ctx, args.steps, args.warmup)
+    per = nb ** 3 / 3 + 2 * nb ** 3 / 6
+    madds = per * batch
+    r = base_result(args, "batched front LU + stars Gop/s, 16384 x 64x64 Float32", madds / T / 1e9, "semiring Gop/s",
+                    T, "f32", "16384 independent 64x64 MinPlus fronts, entries U{0..1000} with 10% +Inf, diagonal 0 "
+                    "(SplitMix64 seed 0x5EED+32); A <- L+U, TL <- L*, TU <- U*; step includes a 268 MB device copy "
+                    "restoring A", {"nb": nb, "batch": batch, "madds_per_front": per})
+    r["roofline"] = {"bound": "valu", "kernel": "k_getrf_star<MinPlus<float>>", "achieved": round(madds / T / 1e12, 4),
+                     "peak": round(VALU_PEAK_MADD / 1e12, 2), "unit": "Tmadd/s", "frac": round(madds / T / VALU_PEAK_MADD, 4),
+                     "traffic": None, "hbm_floor_ms": round(4.0 * A.size * 4 / HBM_PEAK * 1e3, 3)}
+    if not args.no_cpu:
+        sb = 512
+        t0 = time.perf_counter()
+        flat = A.ravel(order="F")[:sb * nb * nb]
+        O.getrf_star_batched(O.MINPLUS, flat.reshape(sb, nb, nb))   # front b at [b] (column-major: [b, j, i])
+        tc = time.perf_counter() - t0
+        r["cpu_baseline"] = {"value": round(per * sb / tc / 1e9, 3), "unit": "semiring Gop/s",
+                             "cores": O.num_threads(), "kind": "port", "sample": f"oracle on {sb} of the fronts"}
+    print(json.dumps(r), flush=True)
+
+
+def bench_solve(args, cfg):
+    """4: MaxMin lmul! with 1024 unit columns on the RGG n=65536 (Float32); 5: PlusProd rmul! with 512 unit rows on
+    the 256 x 256 grid (Float64).  mlu once; a step restores B (device copy) and applies the solve."""
+    import ctypes
+    import oracle as O
+
+    g = W.config_graph(cfg)
+    n = g.n
+    ctx = P.context(0)
+    ctx.set_timing(True)
+    left = cfg == 4
+    s = P.MaxMin() if left else P.PlusProd()
+    nrhs = 1024 if left else 512
+    src = (W.splitmix64(W.SEED_BASE + cfg + 100, nrhs) % np.uint64(n)).astype(np.int64)
+    if left:
+        B = np.full((n, nrhs), -np.inf, np.float32, order="F")
+        B[src, np.arange(nrhs)] = np.inf
+    else:
+        B = np.zeros((nrhs, n), np.float64, order="F")
+        B[np.arange(nrhs), src] = 1.0
+    t0 = time.perf_counter()
+    sym = P.symbolic(g)
+    t_sym = time.perf_counter() - t0
+    dnz = P.DeviceArray.from_numpy(np.ascontiguousarray(g.nzval).reshape(-1, 1))
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    F = factor_device(s, sym, dnz, ctx)
+    ctx.synchronize()
+    t_fac = time.perf_counter() - t0
+    d0 = P.DeviceArray.from_numpy(B)
+    dB = P.DeviceArray(B.shape, B.dtype)
+    fn = P.lib().pp_lmul if left else P.lib().pp_rmul
+    ld = B.shape[0]
+
+    def run():
+        ctx.check(P.lib().pp_copy(ctx.handle, ctypes.c_void_p(dB.ptr), ctypes.c_void_p(d0.ptr), dB.nbytes))
+        ctx.check(fn(ctx.handle, F.handle, ctypes.c_void_p(dB.ptr), ld, nrhs, 1))
+
+    T = timed(run, ctx, args.steps, args.warmup)
+    t_dev = ctx.timing()[4]
+    st = sym.stats()
+    madds = st["madds_rhs_alg"] * nrhs
+    name = "lmul!" if left else "rmul!"
+    r = base_result(args, f"{name} sec + semiring Gop/s, {s.name} {nrhs} RHS, n={n}", madds / T / 1e9,
+                    "semiring Gop/s", T, "f32" if left else "f64",
+                    (f"MaxMin lmul! of 1024 unit columns (+Inf at a seeded source, -Inf elsewhere) on a random "
+                     f"geometric graph n=65536, mean degree 8, capacities U{{1..1000}} Float32 (seed 0x5EED+4)"
+                     if left else
+                     f"PlusProd rmul! of 512 unit rows (1 at a seeded source) on the directed 256x256 grid, weights "
+                     f"U(0,0.2) Float64 (seed 0x5EED+5)") + "; B in HBM, restored by a device copy in each step",
+                    {"n": n, "nrhs": nrhs, "madds_alg": madds, "fronts": sym.nf})
+    r["phases_ms"] = {"symbolic_s": round(t_sym * 1e3, 3), "factor_s": round(t_fac * 1e3, 3),
+                      "solve_device_s": round(t_dev * 1e3, 3)}
+    if not args.no_cpu:
+        k = 32
+        e = sym.export()
+        osym = O.Sym(n, e["Rptr"], e["Sptr"], e["Stgt"], e["perm"])
+        Fo = O.factor(O.MAXMIN if left else O.PLUSPROD, osym, g.colptr, g.rowval, g.nzval)
+        Bs = np.asfortranarray(B[:, :k] if left else B[:k, :])
+        t0 = time.perf_counter()
+        (O.lmul if left else O.rmul)(Fo, Bs)
+        tc = time.perf_counter() - t0
+        r["cpu_baseline"] = {"value": round(st["madds_rhs_alg"] * k / tc / 1e9, 3), "unit": "semiring Gop/s",
+                             "cores": O.num_threads(), "kind": "port",
+                             "sample": f"oracle {name} on {k} of the {nrhs} right-hand sides"}
+    print(json.dumps(r), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--config", default="3", choices=["1", "2a", "2b", "3", "4", "5"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-timing", dest="timing", action="store_false")
+    ap.add_argument("--calibrate-valu", action="store_true",
+                    help="only run the VALU probe (pp_calibrate_valu): v_add_f32 and MinPlus multiply-add rates")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MiB",
                     help="only run the plain copy kernel (pp_copy) over this many MiB: the calibration of the memory "
                          "counters FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
+    if args.calibrate_valu:
+        import ctypes
+
+        ctx = P.context(0)
+        out = {}
+        for kind, name in ((0, "v_add_f32"), (1, "minplus_madd2")):
+            sec, ins = ctypes.c_double(), ctypes.c_double()
+            ctx.check(P.lib().pp_calibrate_valu(ctx.handle, kind, 200000, ctypes.byref(sec), ctypes.byref(ins)))
+            out[name] = {"seconds": sec.value, "lane_instr_per_s": ins.value / sec.value}
+        out["minplus_madd_per_s"] = out["minplus_madd2"]["lane_instr_per_s"] * 16 / 26
+        print(json.dumps(out))
+        return
     if args.calibrate_copy:
         import ctypes
 
@@ -199,7 +418,14 @@ def main():
         print(json.dumps({"error": "this benchmark runs on one GPU: the star's row blocks would shard across GPUs "
                                    "with a replicated factor, which this build does not implement"}))
         sys.exit(2)
-    bench_mstar(args)
+    if args.config in ("1", "3"):
+        bench_mstar(args)
+    elif args.config == "2a":
+        bench_gemm(args)
+    elif args.config == "2b":
+        bench_getrf(args)
+    else:
+        bench_solve(args, int(args.config))
 
 
 if __name__ == "__main__":

@@ -158,6 +158,13 @@ pp_status pp_copy(pp_ctx *ctx, void *dst_device, const void *src_device, size_t 
 
 /* ===== measurement ===== */
 
+/* VALU throughput probe (replaces nothing in the reference; the calibration of the VALU roofline): every lane of
+ * 8 workgroups per CU runs `iters` iterations of eight independent chains of (kind 0) v_add_f32 or (kind 1) the
+ * Float32 MinPlus double multiply-add of the kernels (two v_add_f32 and one v_min3_f32; plus two v_mov_b32 per
+ * eight of them in the probe's loop).  Returns the kernel's seconds (HIP events) and the lane instructions it
+ * executed. */
+pp_status pp_calibrate_valu(pp_ctx *ctx, int kind, int64_t iters, double *seconds, double *lane_instr);
+
 /* Per-phase device time of the last pp_factor / pp_star / pp_lmul / pp_rmul on ctx, in seconds (HIP events on the
  * context's stream): t[0] factor total, t[1] star U* sweep, t[2] star L* sweep, t[3] star relabel, t[4] solve,
  * t[5] host-side setup of the last call, t[6] the dominant sweep kernel's summed duration, t[7] its launch count.

@@ -529,6 +529,15 @@ pp_status pp_copy(pp_ctx *ctx, void *dst, const void *src, size_t bytes) {
     return PP_OK;
 }
 
+pp_status pp_calibrate_valu(pp_ctx *ctx, int kind, int64_t iters, double *seconds, double *lane_instr) {
+    if (!ctx || !seconds || !lane_instr) return fail(ctx, PP_EINVAL, "pp_calibrate_valu: null argument");
+    if (kind < 0 || kind > 1 || iters < 1 || iters > (1 << 24)) return fail(ctx, PP_EINVAL, "pp_calibrate_valu: bad kind / iters");
+    CHECK_HIP(ctx, hipSetDevice(ctx->device));
+    std::string e = pp::device_valu_peak(ctx, kind, (int)iters, seconds, lane_instr);
+    if (!e.empty()) return fail(ctx, PP_EHIP, "pp_calibrate_valu: " + e);
+    return PP_OK;
+}
+
 pp_status pp_set_timing(pp_ctx *ctx, int on) {
     if (!ctx) return fail(nullptr, PP_EINVAL, "pp_set_timing: null context");
     ctx->timing = on;

@@ -36,6 +36,64 @@ std::string device_copy(pp_ctx *ctx, void *dst, const void *src, size_t bytes) {
     return e == hipSuccess ? "" : std::string("kernel launch: ") + hipGetErrorString(e);
 }
 
+// VALU throughput probe: eight independent chains per lane of (kind 0) v_add_f32, or (kind 1) the MinPlus Float32
+// double multiply-add of the sweeps and GEMMs, min3(p + q_i, r + q_7-i, acc_i) = v_add_f32, v_add_f32, v_min3_f32
+// (the chains' inputs change every iteration, so nothing is hoisted).  Lane instructions per lane and iteration, as
+// compiled for gfx950: 8 v_add_f32 (kind 0); 16 v_add_f32, 8 v_min3_f32 and the 2 v_mov_b32 that carry p and r
+// (kind 1).
+template <int KIND> __global__ __launch_bounds__(256) void k_valu_peak(float *__restrict__ out, int iters, float s0) {
+    float acc[8], q[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        acc[i] = s0 * (float)(threadIdx.x + i);
+        q[i] = s0 + (float)i;
+    }
+    float p = acc[0], r = acc[1];
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (KIND == 0) acc[i] = acc[i] + q[i];
+            else acc[i] = MinPlus<float>::muladd2(p, q[i], r, q[7 - i], acc[i]);
+        }
+        if (KIND != 0) {
+            p = acc[0];
+            r = acc[1];
+        }
+    }
+    float t = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) t += acc[i];
+    out[blockIdx.x * 256 + threadIdx.x] = t;
+}
+
+std::string device_valu_peak(pp_ctx *ctx, int kind, int iters, double *seconds, double *lane_instr) {
+    const int blocks = ctx->num_cu * 8;
+    float *out = nullptr;
+    hipStream_t st = ctx->stream;
+    if (hipMallocAsync((void **)&out, (size_t)blocks * 256 * sizeof(float), st) != hipSuccess) return "hipMallocAsync failed";
+    hipEvent_t e0, e1;
+    hipEventCreate(&e0);
+    hipEventCreate(&e1);
+    auto launch = [&](int it) {
+        if (kind == 0) k_valu_peak<0><<<blocks, 256, 0, st>>>(out, it, 1e-3f);
+        else k_valu_peak<1><<<blocks, 256, 0, st>>>(out, it, 1e-3f);
+    };
+    launch(iters / 10 + 1);   // warm-up
+    hipEventRecord(e0, st);
+    launch(iters);
+    hipEventRecord(e1, st);
+    hipError_t e = hipEventSynchronize(e1);
+    float ms = 0;
+    hipEventElapsedTime(&ms, e0, e1);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    hipFreeAsync(out, st);
+    if (e != hipSuccess) return std::string("valu probe: ") + hipGetErrorString(e);
+    *seconds = ms * 1e-3;
+    *lane_instr = (double)blocks * 256 * (double)iters * (kind == 0 ? 8 : 26);
+    return "";
+}
+
 #define PP_DISPATCH(sr, dt, EXPR)                                        \
     do {                                                                 \
         std::string err_;                                                \

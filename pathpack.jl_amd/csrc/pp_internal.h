@@ -161,5 +161,6 @@ std::string device_lmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 
 std::string device_sgemx(pp_ctx *ctx, int sr, int dt, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B,
                          i64 ldb, void *C, i64 ldc);
 std::string device_getrf_star_batched(pp_ctx *ctx, int sr, int dt, i64 nb, i64 batch, void *A, void *TL, void *TU);
+std::string device_valu_peak(pp_ctx *ctx, int kind, int iters, double *seconds, double *lane_instr);
 std::string device_copy(pp_ctx *ctx, void *dst, const void *src, size_t bytes);
 }  // namespace pp

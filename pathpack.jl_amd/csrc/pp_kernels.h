@@ -331,6 +331,144 @@ __global__ __launch_bounds__(NT) void k_gemm(typename S::value_type *__restrict_
                  (int)min<i64>(GT, n - c0), (int)k);
 }
 
+// 16-byte vectors of each element type, and of their int32 indices
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+template <class T> struct Vec16;
+template <> struct Vec16<float> { typedef f32x4 type; typedef i32x4 idx; };
+template <> struct Vec16<double> { typedef f64x2 type; typedef i32x2 idx; };
+template <> struct Vec16<int32_t> { typedef i32x4 type; typedef i32x4 idx; };
+
+// ===== dense semiring GEMM: C <- C (+) A (x) B (sgemx!, dense/sgemx.jl:26-60; generic loop :606-635) =====
+//
+// Workgroups of 256 threads (16 x 16) own a BM x BN tile of C (BM = 16 TM, BN = 16 TN; 128 x 128 for 4-byte
+// elements, 64 x 64 for 8-byte ones), each thread a TM x TN register block whose rows are groups of four, 64 rows
+// apart, and likewise its columns (16-byte LDS reads without bank conflicts).  K runs in steps of BK = 16 through
+// two LDS buffers: the next step's A and B tiles are loaded into registers while the current step is computed, then
+// stored into the other buffer (one barrier per step).  Two k at a time go into each accumulator (muladd2: v_min3 /
+// v_max3 for the tropical semirings, 1.5 VALU instructions per multiply-add).  Out-of-range rows, columns and k
+// read the semiring zero.
+constexpr int GBK = 16;
+
+template <class S, int TM, int TN>
+__global__ __launch_bounds__(256) void k_gemm_tiled(typename S::value_type *__restrict__ C, i64 ldc,
+                                                    const typename S::value_type *__restrict__ A, i64 lda,
+                                                    const typename S::value_type *__restrict__ B, i64 ldb, i64 m,
+                                                    i64 n, i64 k) {
+    typedef typename S::value_type T;
+    constexpr int BM = 16 * TM, BN = 16 * TN, BK = GBK, PAD = 4;
+    constexpr int AL = BM * BK / 256, BL = BN * BK / 256;   // tile elements per thread
+    __shared__ __attribute__((aligned(16))) T As[2][BK][BM];
+    __shared__ __attribute__((aligned(16))) T Bs[2][BK][BN + PAD];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const i64 r0 = (i64)blockIdx.x * BM, c0 = (i64)blockIdx.y * BN;
+    T ra[AL], rb[BL];
+    // 16-byte loads when the tile is inside the matrices and the columns are 16-byte aligned (uniform)
+    typedef typename Vec16<T>::type V;
+    constexpr int VW = 16 / (int)sizeof(T);
+    const bool vec = r0 + BM <= m && c0 + BN <= n && lda % VW == 0 && ldb % VW == 0 &&
+                     ((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0;
+    auto gload = [&](i64 k0) {
+        if (vec && k0 + BK <= k) {
+#pragma unroll
+            for (int q = 0; q < AL / VW; q++) {
+                const int e = (tid + 256 * q) * VW, r = e % BM, kk = e / BM;
+                const V v = *reinterpret_cast<const V *>(A + (r0 + r) + (k0 + kk) * lda);
+#pragma unroll
+                for (int u = 0; u < VW; u++) ra[q * VW + u] = v[u];
+            }
+#pragma unroll
+            for (int q = 0; q < BL / VW; q++) {
+                const int e = (tid + 256 * q) * VW, kk = e % BK, c = e / BK;
+                const V v = *reinterpret_cast<const V *>(B + (k0 + kk) + (c0 + c) * ldb);
+#pragma unroll
+                for (int u = 0; u < VW; u++) rb[q * VW + u] = v[u];
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < AL / VW; q++)
+#pragma unroll
+                for (int u = 0; u < VW; u++) {
+                    const int e = (tid + 256 * q) * VW + u, r = e % BM, kk = e / BM;
+                    ra[q * VW + u] = (r0 + r < m && k0 + kk < k) ? A[(r0 + r) + (k0 + kk) * lda] : S::zero();
+                }
+#pragma unroll
+            for (int q = 0; q < BL / VW; q++)
+#pragma unroll
+                for (int u = 0; u < VW; u++) {
+                    const int e = (tid + 256 * q) * VW + u, kk = e % BK, c = e / BK;
+                    rb[q * VW + u] = (c0 + c < n && k0 + kk < k) ? B[(k0 + kk) + (c0 + c) * ldb] : S::zero();
+                }
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < AL / VW; q++) {
+            const int e = (tid + 256 * q) * VW;
+            V v;
+#pragma unroll
+            for (int u = 0; u < VW; u++) v[u] = ra[q * VW + u];
+            *reinterpret_cast<V *>(&As[buf][e / BM][e % BM]) = v;
+        }
+#pragma unroll
+        for (int q = 0; q < BL / VW; q++)
+#pragma unroll
+            for (int u = 0; u < VW; u++) {
+                const int e = (tid + 256 * q) * VW + u;
+                Bs[buf][e % BK][e / BK] = rb[q * VW + u];
+            }
+    };
+    // row i of the register block: 64 (i / 4) + 4 tx + i % 4; column j likewise with ty
+    auto rowof = [&](int i) { return 64 * (i >> 2) + 4 * tx + (i & 3); };
+    auto colof = [&](int j) { return 64 * (j >> 2) + 4 * ty + (j & 3); };
+    T acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const i64 r = r0 + rowof(i), c = c0 + colof(j);
+            acc[i][j] = (r < m && c < n) ? C[r + c * ldc] : S::zero();
+        }
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    int buf = 0;
+    for (i64 k0 = 0; k0 < k; k0 += BK) {
+        const bool more = k0 + BK < k;
+        if (more) gload(k0 + BK);
+#pragma unroll 1
+        for (int kk = 0; kk < BK; kk += 2) {
+            T a0[TM], a1[TM], b0[TN], b1[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                a0[i] = As[buf][kk][rowof(i)];
+                a1[i] = As[buf][kk + 1][rowof(i)];
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                b0[j] = Bs[buf][kk][colof(j)];
+                b1[j] = Bs[buf][kk + 1][colof(j)];
+            }
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) acc[i][j] = S::muladd2(a0[i], b0[j], a1[i], b1[j], acc[i][j]);
+        }
+        if (more) sstore(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const i64 r = r0 + rowof(i), c = c0 + colof(j);
+            if (r < m && c < n) C[r + c * ldc] = acc[i][j];
+        }
+}
+
 // ===== factor extraction: the reference layout and the sweep packs =====
 
 // LD (nn x nn at Dptr), LL (na x nn at Lptr), UL (nn x na at Lptr); one workgroup per (front, EXTRACT_COLS columns)
@@ -707,14 +845,6 @@ __global__ __launch_bounds__(NT) void k_relabel(const T *__restrict__ X, i64 n, 
 constexpr int RELABEL_LDS = 131072;
 constexpr int RELABEL_NT = 1024;
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef double f64x2 __attribute__((ext_vector_type(2)));
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
-template <class T> struct Vec16;
-template <> struct Vec16<float> { typedef f32x4 type; typedef i32x4 idx; };
-template <> struct Vec16<double> { typedef f64x2 type; typedef i32x2 idx; };
-template <> struct Vec16<int32_t> { typedef i32x4 type; typedef i32x4 idx; };
 
 template <class T>
 __global__ __launch_bounds__(RELABEL_NT) void k_relabel_lds(const T *__restrict__ X, i64 n, T *__restrict__ C, i64 ldc,
@@ -925,6 +1055,19 @@ template <class S> struct FactorRun {
     }
 };
 
+// LDS of the backward kernel's split-K combine
+template <class T, int W> constexpr i64 bwd_lds(int ks) { return (i64)(ks > 1 ? ks - 1 : 1) * W * TILE_ROWS * sizeof(T); }
+
+template <class S, int W, int KS>
+static void launch_bwd(unsigned grid, int dmode, typename S::value_type *X, i64 ld, const SweepArgs &a,
+                       const typename S::value_type *D, const typename S::value_type *Pk, hipStream_t st) {
+    typedef typename S::value_type T;
+    if constexpr (bwd_lds<T, W>(KS) <= 98304) {
+        if (dmode == 0) k_sweep_bwd<S, W, 0, KS><<<grid, 64 * KS, 0, st>>>(X, ld, a, D, Pk);
+        else k_sweep_bwd<S, W, 1, KS><<<grid, 64 * KS, 0, st>>>(X, ld, a, D, Pk);
+    }
+}
+
 template <class S, int W>
 static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type *X, i64 ld, const SweepArgs &base,
                         const SweepPlan &Wp, const SweepPlan::List &li, bool star_rows, i64 nrows, const void *Dpack,
@@ -977,23 +1120,17 @@ static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type
             grid = (unsigned)(li.cnt * ((ntile + 7) / 8) * 8);
         }
         // split each row tile's gather list over KS waves when the list has too few tiles to fill the chip (about
-        // 4096 waves), keeping at least 32 gather columns per wave
+        // 4096 waves), keeping at least 32 gather columns per wave and the split's LDS within 96 KiB
         const i64 tiles_total = li.cnt * ntile, emean = li.esum / std::max<i64>(1, li.cnt);
         int ks = 1;
-        while (ks < 8 && tiles_total * ks < 4096 && emean >= 64 * ks) ks *= 2;
+        while (ks < 8 && tiles_total * ks < 4096 && emean >= 64 * ks && bwd_lds<T, W>(2 * ks) <= 98304) ks *= 2;
         if (grid) {
-#define PP_BWD(KS)                                                                                             \
-    do {                                                                                                         \
-        if (dmode == 0) k_sweep_bwd<S, W, 0, KS><<<grid, 64 * KS, 0, st>>>(X, ld, a, D, Pk);                     \
-        else k_sweep_bwd<S, W, 1, KS><<<grid, 64 * KS, 0, st>>>(X, ld, a, D, Pk);                                \
-    } while (0)
             switch (ks) {
-            case 1: PP_BWD(1); break;
-            case 2: PP_BWD(2); break;
-            case 4: PP_BWD(4); break;
-            default: PP_BWD(8); break;
+            case 1: launch_bwd<S, W, 1>(grid, dmode, X, ld, a, D, Pk, st); break;
+            case 2: launch_bwd<S, W, 2>(grid, dmode, X, ld, a, D, Pk, st); break;
+            case 4: launch_bwd<S, W, 4>(grid, dmode, X, ld, a, D, Pk, st); break;
+            default: launch_bwd<S, W, 8>(grid, dmode, X, ld, a, D, Pk, st); break;
             }
-#undef PP_BWD
         }
     }
 }
@@ -1141,8 +1278,9 @@ template <class S> struct GemmRun {
     std::string run() {
         typedef typename S::value_type T;
         if (m == 0 || n == 0) return "";
-        dim3 g((unsigned)((m + GT - 1) / GT), (unsigned)((n + GT - 1) / GT));
-        k_gemm<S><<<g, NT, 0, ctx->stream>>>((T *)C, ldc, (const T *)A, lda, (const T *)B, ldb, m, n, k);
+        constexpr int TM = sizeof(T) == 4 ? 8 : 4, BM = 16 * TM;
+        dim3 g((unsigned)((m + BM - 1) / BM), (unsigned)((n + BM - 1) / BM));
+        k_gemm_tiled<S, TM, TM><<<g, 256, 0, ctx->stream>>>((T *)C, ldc, (const T *)A, lda, (const T *)B, ldb, m, n, k);
         LAUNCHCHK();
         return "";
     }

@@ -19,7 +19,8 @@ EXPORTS = [
     "pp_symbolic", "pp_symbolic_given", "pp_sym_size", "pp_sym_export", "pp_sym_stats", "pp_sym_destroy",
     "pp_factor", "pp_factor_device", "pp_fac_export", "pp_fac_destroy",
     "pp_star", "pp_lmul", "pp_rmul", "pp_sgemx", "pp_getrf_star_batched",
-    "pp_buffer_alloc", "pp_buffer_free", "pp_upload", "pp_download", "pp_copy", "pp_set_timing", "pp_get_timing",
+    "pp_buffer_alloc", "pp_buffer_free", "pp_upload", "pp_download", "pp_copy", "pp_calibrate_valu", "pp_set_timing",
+    "pp_get_timing",
 ]
 
 
@@ -96,6 +97,8 @@ def lib() -> ctypes.CDLL:
         L.pp_upload.argtypes = [c_vp, c_vp, c_vp, ctypes.c_size_t]
         L.pp_download.argtypes = [c_vp, c_vp, c_vp, ctypes.c_size_t]
         L.pp_copy.argtypes = [c_vp, c_vp, c_vp, ctypes.c_size_t]
+        L.pp_calibrate_valu.argtypes = [c_vp, ctypes.c_int, c_i64, ctypes.POINTER(ctypes.c_double),
+                                        ctypes.POINTER(ctypes.c_double)]
         L.pp_set_timing.argtypes = [c_vp, ctypes.c_int]
         L.pp_get_timing.argtypes = [c_vp, ctypes.POINTER(ctypes.c_double)]
         _lib = L

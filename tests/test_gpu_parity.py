@@ -155,10 +155,13 @@ def test_grid64_star_vs_dijkstra():
     assert np.array_equal(D, O.dijkstra_rows(g))
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (37, 23, 19), (64, 64, 64), (130, 67, 200), (257, 129, 33)])
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (37, 23, 19), (64, 64, 64), (130, 67, 200), (257, 129, 33),
+                                   (256, 384, 96), (384, 260, 100), (512, 512, 512)])
 @pytest.mark.parametrize("s", [O.MINPLUS, O.MAXMIN, O.PLUSPROD])
-def test_sgemx_matches_oracle(m, n, k, s):
-    dtype = np.float32
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_sgemx_matches_oracle(m, n, k, s, dtype):
+    """Sizes with whole 128 x 128 (64 x 64 for Float64) tiles and 16-byte aligned columns take the vector-load path;
+    ragged edges, a k that is not a multiple of the K step, and odd leading dimensions take the guarded one."""
     rng = np.random.default_rng(m * 1000 + n)
     A = rng.integers(0, 1000, (m, k)).astype(dtype)
     B = rng.integers(0, 1000, (k, n)).astype(dtype)
@@ -171,11 +174,13 @@ def test_sgemx_matches_oracle(m, n, k, s):
     ref = O.sgemx(s, A, B, C)
     ctx = P.context(0)
     dA, dB, dC = P.DeviceArray.from_numpy(A), P.DeviceArray.from_numpy(B), P.DeviceArray.from_numpy(C)
-    ctx.check(P.lib().pp_sgemx(ctx.handle, s, 0, m, n, k, dA.ptr, m, dB.ptr, k, dC.ptr, m))
+    dt = 0 if dtype == np.float32 else 1
+    ctx.check(P.lib().pp_sgemx(ctx.handle, s, dt, m, n, k, dA.ptr, m, dB.ptr, k, dC.ptr, m))
     ctx.synchronize()
     got = dC.numpy()
     if s == O.PLUSPROD:
-        assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)) < 1e-5
+        tol = 1e-5 if dtype == np.float32 else 1e-12
+        assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)) < tol
     else:
         assert np.array_equal(bits(got), bits(ref))
 
