@@ -32,7 +32,7 @@ constexpr int SMALL_NJ = 64;   // fronts up to this size are factorized in one w
 constexpr int MID_NJ = 128;    // ... and up to this size too, in a workgroup with a larger LDS block
 constexpr int ASM_BLOCK = 16;  // parent columns per extend-add workgroup
 constexpr int EXTRACT_COLS = 32;  // frontal columns per factor-extraction workgroup
-constexpr int EIDX_PAD = 16;      // zero entries after the last gather list: sweeps read up to 12 entries ahead
+constexpr int EIDX_PAD = 32;      // zero entries after the last gather list: sweeps read up to 16 entries ahead
 constexpr int NB = 32;         // pivot block of the blocked front factorization
 constexpr int PANEL_W = 32;    // widest sweep panel
 constexpr int NCLASS = 6;      // sweep width classes 1, 2, 4, 8, 16, 32

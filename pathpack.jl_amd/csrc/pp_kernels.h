@@ -35,6 +35,7 @@ namespace pp {
 
 constexpr int NT = 256;
 
+
 static inline unsigned grid1(i64 work, int per = NT) {
     i64 g = (work + per - 1) / per;
     return (unsigned)std::max<i64>(1, std::min<i64>(g, 1 << 20));
@@ -706,20 +707,23 @@ __global__ __launch_bounds__(NT) void k_fwd_scatter(typename S::value_type *__re
 }
 
 // Locate (panel, row tile) of a backward / solve workgroup.  With a prefix (star rows): panel-major over each
-// panel's own rows.  Without (one row range [row_base, row_base + nrows) for the whole list): XCD-aware tile-major
-// order -- workgroups are dealt to the 8 XCDs round-robin, so XCD x gets the tiles t = x mod 8, each with all panels
-// of the list, and the gathered columns of a row tile are reused from that XCD's L2.
+// panel's own rows.  Without (one row range [row_base, row_base + nrows) for the whole list): workgroups are dealt to
+// the 8 XCDs round-robin, so XCD x gets the tiles t = x mod 8; within an XCD the workgroups run panel by panel, so a
+// CU's consecutive workgroups share the panel's pack in its scalar cache, and neighbouring panels of the list (the
+// children of one front share their parent's columns) meet in the XCD's L2.
 __device__ inline void locate_tile(const SweepArgs &a, int np, int &pi, int &tile) {
     const int bid = blockIdx.x;
     if (a.pre) {
         pi = search(a.pre, np, bid);
         tile = bid - a.pre[pi];
     } else {
-        const int xcd = bid & 7, local = bid >> 3;
-        tile = (local / np) * 8 + xcd;
-        pi = local - (local / np) * np;
+        const int xcd = bid & 7, local = bid >> 3, tpx = (int)(gridDim.x >> 3) / np;
+        pi = local / tpx;
+        tile = (local - pi * tpx) * 8 + xcd;
     }
 }
+
+constexpr int BWD_NSET = 5;
 
 template <class S, int W, int DMODE, int KSPLIT>
 __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(sizeof(typename S::value_type) == 4 ? 4 : 2))) void k_sweep_bwd(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
@@ -750,9 +754,9 @@ __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(siz
             acc[j] = j < w ? v : S::zero();
         }
     }
-    // this wave's share of the gather list, in groups of four columns, with the next two groups' loads in flight
-    // (three register sets used in rotation, so no copy waits on a load); the lookahead reads up to eight entries
-    // past the share, into the following lists or the zero padding after the last one
+    // this wave's share of the gather list, in groups of four columns, with the next BWD_NSET - 1 groups' loads in
+    // flight (register sets used in rotation, so no copy waits on a load); the lookahead reads up to
+    // 4 (BWD_NSET - 1) entries past the share, into the following lists or the zero padding after the last one
     const int ng = e >> 2;
     const int g0 = (int)(((i64)ng * q) / KSPLIT), g1 = (int)(((i64)ng * (q + 1)) / KSPLIT);
     const int kt = 4 * g1, kend = q == KSPLIT - 1 ? e : kt;
@@ -772,25 +776,22 @@ __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(siz
     };
     const int ngw = g1 - g0;
     if (ngw > 0) {
-        T A[4], B[4], C[4];
-        ld4(ep, A);
-        ld4(ep + 4, B);
+        T xs[BWD_NSET][4];
+#pragma unroll
+        for (int u = 0; u + 1 < BWD_NSET; u++) ld4(ep + 4 * u, xs[u]);
         int g = 0;
-        for (; g + 3 <= ngw; g += 3) {
-            ld4(ep + 8, C);
-            mad4(A, qp);
-            ld4(ep + 12, A);
-            mad4(B, qp + 4 * W);
-            ld4(ep + 16, B);
-            mad4(C, qp + 8 * W);
-            ep += 12;
-            qp += 12 * W;
+        for (; g + BWD_NSET <= ngw; g += BWD_NSET) {
+#pragma unroll
+            for (int u = 0; u < BWD_NSET; u++) {
+                ld4(ep + 4 * (u + BWD_NSET - 1), xs[(u + BWD_NSET - 1) % BWD_NSET]);
+                mad4(xs[u], qp + 4 * u * W);
+            }
+            ep += 4 * BWD_NSET;
+            qp += 4 * BWD_NSET * W;
         }
-        if (g < ngw) {
-            mad4(A, qp);
-            qp += 4 * W;
-            if (g + 1 < ngw) mad4(B, qp);
-        }
+#pragma unroll
+        for (int u = 0; u + 1 < BWD_NSET; u++)
+            if (g + u < ngw) mad4(xs[u], qp + 4 * u * W);
     }
     for (int k = kt; k < kend; k++) {
         const T v0 = xr[(i64)E[k] * ld];
@@ -1119,7 +1120,7 @@ static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type
             ntile = (a.nrows + TILE_ROWS - 1) / TILE_ROWS;
             grid = (unsigned)(li.cnt * ((ntile + 7) / 8) * 8);
         }
-        // split each row tile's gather list over KS waves when the list has too few tiles to fill the chip (about
+        // split each row tile's gather list over ks waves when the list has too few tiles to fill the chip (about
         // 4096 waves), keeping at least 32 gather columns per wave and the split's LDS within 96 KiB
         const i64 tiles_total = li.cnt * ntile, emean = li.esum / std::max<i64>(1, li.cnt);
         int ks = 1;
