@@ -114,7 +114,6 @@ struct ND {
                                    order(g.n, -1) {}
 
     // BFS inside item id from root; returns the number of levels; fills queue[0..cnt) and level[]
-    std::atomic<i64> bfs_work{0};
     int bfs(std::vector<i32> &queue, i32 id, i32 root, i64 &cnt, std::vector<i64> &lptr) {
         lptr.clear();
         cnt = 0;
@@ -136,7 +135,6 @@ struct ND {
         for (i64 k = 1; k < cnt; k++)
             if (level[queue[k]] != level[queue[k - 1]]) lptr.push_back(k);
         lptr.push_back(cnt);
-        bfs_work += cnt;
         nlev = (int)lptr.size() - 1;
         return nlev;
     }
@@ -260,7 +258,7 @@ struct ND {
         // the separator level
         int sl = -1;
         i64 ssz = 1LL << 60, sbal = 1LL << 60;
-        const i64 minside = (i64)(0.3 * (double)sz);
+        const i64 minside = (i64)(0.35 * (double)sz);
         for (int k = 1; k + 1 < nlev; k++) {
             i64 a = lptr[k], s = lptr[k + 1] - lptr[k], b = sz - a - s;
             if (a < minside || b < minside) continue;
@@ -360,7 +358,6 @@ struct ND {
         for (int t = 1; t < nthreads; t++) pool.emplace_back(work);
         work();
         for (auto &th : pool) th.join();
-        if (std::getenv("PP_NDDBG")) std::fprintf(stderr, "bfs work %ld\n", (long)bfs_work.load());
     }
 };
 
