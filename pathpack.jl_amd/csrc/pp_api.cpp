@@ -5,7 +5,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -226,8 +228,18 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *sym, int semiring, int
     if (!supported(semiring, dtype)) return fail(ctx, PP_EUNSUPPORTED, "pp_factor: unsupported semiring / element type");
     if (sym->S.nnz > 0 && !nzval) return fail(ctx, PP_EINVAL, "pp_factor: null nzval");
     CHECK_HIP(ctx, hipSetDevice(ctx->device));
+    const bool htime = std::getenv("PP_SYMTIME") != nullptr;   // host phases of pp_factor to stderr
+    auto hnow = [] { return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count(); };
+    double th = hnow();
+    auto hstage = [&](const char *what) {
+        if (!htime) return;
+        const double t = hnow();
+        std::fprintf(stderr, "pp_factor: %-28s %8.2f ms\n", what, (t - th) * 1e3);
+        th = t;
+    };
     std::string e = ensure_plans(sym);
     if (!e.empty()) return fail(ctx, PP_EINVAL, "pp_factor: " + e);
+    hstage("plans");
     const pp::FactorPlan &P = *sym->fplan;
     const pp::SweepPlan &W = *sym->splan;
     const pp::Symbolic &S = sym->S;
@@ -315,8 +327,10 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *sym, int semiring, int
         }
         ctx->staging_bytes = plan_bytes;
     }
+    hstage("layout + staging alloc");
     for (const Part &q : parts)
         if (q.bytes) std::memcpy((char *)ctx->staging + q.off, q.src, q.bytes);
+    hstage("staging copy");
     void *block = nullptr;
     if (hipMallocAsync(&block, total, st) != hipSuccess) {
         delete fac;
@@ -348,8 +362,11 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *sym, int semiring, int
         }
         dnz = tmpnz;
     }
+    hstage("alloc + upload issue");
     e = pp::device_factor(ctx, fac, dnz);
+    hstage("launches");
     hipError_t se = hipStreamSynchronize(st);
+    hstage("device wait");
     if (tmpnz) hipFree(tmpnz);
     if (!e.empty() || se != hipSuccess) {
         delete fac;

@@ -36,7 +36,6 @@ constexpr int EIDX_PAD = 32;      // zero entries after the last gather list: sw
 constexpr int NB = 32;         // pivot block of the blocked front factorization
 constexpr int PANEL_W = 32;    // widest sweep panel
 constexpr int NCLASS = 6;      // sweep width classes 1, 2, 4, 8, 16, 32
-constexpr int TRSM_ROWS = 256;   // rows per forward-solve workgroup (one per thread)
 constexpr int TILE_ROWS = 64;    // rows per scatter / backward workgroup (one per lane, 4 waves)
 constexpr int SCATTER_T = 128;   // extension columns per scatter workgroup
 
@@ -86,9 +85,9 @@ struct SweepPlan {
     struct List {
         int cls;                     // width class
         i64 off, cnt;                // panel ids in plist
-        // offsets into `tiles` of per-panel prefix sums (cnt + 1 entries each): forward-solve tiles and scatter
-        // units (tiles x chunks) over the star's forward rows, backward tiles over its backward rows, chunks
-        i64 pA256, pAu, pB64, pC;
+        // offsets into `tiles` of per-panel prefix sums (cnt + 1 entries each): forward units (tiles x chunks)
+        // over the star's forward rows, backward tiles over its backward rows, chunks
+        i64 pAu, pB64, pC;
         i64 esum;                    // sum of the panels' gather-list lengths
         bool uniB;                   // every panel of the list has the same backward rows [rowB_lo, rowB_hi)
         int32_t rowB_lo, rowB_hi;

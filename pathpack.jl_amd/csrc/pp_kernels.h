@@ -528,8 +528,8 @@ __global__ __launch_bounds__(NT) void k_build_packs(const typename S::value_type
 // ===== sweeps over the rows of X (X column-major, ld rows) =====
 //
 // Forward (leaves to root), one panel with columns c_0..c_{w-1}:
-//   x_j <- (x_j (+) sum_{i<j} x_i (x) D(i,j)) (x) star(D(j,j))?          (k_fwd_trsm)
-//   X[:, E_t] <- X[:, E_t] (+) sum_j x_j (x) P(j,t)                        (k_fwd_scatter)
+//   x_j <- (x_j (+) sum_{i<j} x_i (x) D(i,j)) (x) star(D(j,j))?          (k_fwd; stored by k_sweep_bwd)
+//   X[:, E_t] <- X[:, E_t] (+) sum_j x_j (x) P(j,t)                        (k_fwd)
 // Backward (root to leaves):
 //   x_j <- x_j (+) sum_t X[:, E_t] (x) Q(t,j),   then   x_j <- (x_j (+) sum_{i>j} x_i (x) D(i,j)) (x) star(D(j,j))?
 // DMODE 0 reads the panel block as stored (U upper with star for forward, L strict lower unit for backward);
@@ -542,7 +542,7 @@ __global__ __launch_bounds__(NT) void k_build_packs(const typename S::value_type
 struct SweepArgs {
     const int32_t *plist;            // the list's panel ids
     const int32_t *pre;              // per-panel prefix of work units over each panel's own rows (null: rows [0, nrows))
-    const int32_t *cpre;             // per-panel prefix of target chunks (k_fwd_scatter, rows [0, nrows))
+    const int32_t *cpre;             // per-panel prefix of target chunks (k_fwd, rows [0, nrows))
     int32_t np, nrows, row_base;     // without a prefix: rows [row_base, row_base + nrows)
     const int32_t *p_c0, *p_w, *p_e, *p_chunks, *row_lo, *row_hi;
     const i64 *p_eoff, *p_poff, *p_doff;
@@ -580,44 +580,17 @@ template <class S> __device__ inline void atomic_plus(typename S::value_type *ad
     }
 }
 
-template <class S, int W, int DMODE>
-__global__ __launch_bounds__(NT) void k_fwd_trsm(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
-                                                 const typename S::value_type *__restrict__ Dpack) {
+// Forward step of one panel for a 64-row tile and a chunk of at most SCATTER_T targets: wave 0 solves the rows'
+// panel columns (x <- x D*, DMODE as above), the solution goes through LDS, and the four waves scatter it into the
+// chunk's targets, X[:, E_t] <- X[:, E_t] (+) sum_j x_j (x) P(j, t).  The solution is not stored: the workgroups of
+// the other chunks read the same unsolved columns, and no later forward step reads them; the backward sweep solves
+// them again as it loads them (the same operations in the same order).
+template <class S, int W, bool ATOMIC, int DMODE>
+__global__ __launch_bounds__(NT) void k_fwd(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
+                                            const typename S::value_type *__restrict__ Dpack,
+                                            const typename S::value_type *__restrict__ P) {
     typedef typename S::value_type T;
-    int pi, tile;
-    if (a.pre) {
-        pi = search(a.pre, a.np, blockIdx.x);
-        tile = blockIdx.x - a.pre[pi];
-    } else {
-        pi = blockIdx.x % a.np;
-        tile = blockIdx.x / a.np;
-    }
-    const int p = a.plist[pi];
-    const int lo = a.pre ? a.row_lo[p] : 0, hi = a.pre ? a.row_hi[p] : a.nrows;
-    const int r = lo + tile * TRSM_ROWS + threadIdx.x;
-    if (r >= hi) return;
-    const int w = a.p_w[p], c0 = a.p_c0[p];
-    const T *D = Dpack + a.p_doff[p];
-    T x[W];
-#pragma unroll
-    for (int j = 0; j < W; j++) x[j] = j < w ? X[(i64)(c0 + j) * ld + r] : S::zero();
-#pragma unroll
-    for (int j = 0; j < W; j++) {
-        T acc = x[j];
-#pragma unroll
-        for (int i = 0; i < j; i++) acc = S::muladd(x[i], DMODE == 0 ? D[i + j * W] : D[j + i * W], acc);
-        if (DMODE == 0 && !S::integral) acc = S::prod(acc, S::star(D[j + j * W]));
-        x[j] = acc;
-    }
-#pragma unroll
-    for (int j = 0; j < W; j++)
-        if (j < w) X[(i64)(c0 + j) * ld + r] = x[j];
-}
-
-template <class S, int W, bool ATOMIC>
-__global__ __launch_bounds__(NT) void k_fwd_scatter(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
-                                                    const typename S::value_type *__restrict__ P) {
-    typedef typename S::value_type T;
+    __shared__ T xsh[W][TILE_ROWS];
     int pi, tile, chunk;
     if (a.pre) {
         pi = search(a.pre, a.np, blockIdx.x);
@@ -636,14 +609,38 @@ __global__ __launch_bounds__(NT) void k_fwd_scatter(typename S::value_type *__re
     const int lo = a.pre ? a.row_lo[p] : 0, hi = a.pre ? a.row_hi[p] : a.nrows;
     const int lane = threadIdx.x & 63;
     const int q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // the wave: uniform, so pack loads are scalar
+    if (lo + tile * TILE_ROWS >= hi) return;                          // (whole workgroup)
     const int r = lo + tile * TILE_ROWS + lane;
-    if (r >= hi) return;
+    const bool valid = r < hi;
     const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
+    T x[W];
+    if (q == 0) {
+        const T *D = Dpack + a.p_doff[p];
+        const T *xr0 = X + (valid ? r : hi - 1);
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            const T v = xr0[(i64)(c0 + min(j, w - 1)) * ld];
+            x[j] = j < w ? v : S::zero();
+        }
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            T acc = x[j];
+#pragma unroll
+            for (int i = 0; i < j; i++) acc = S::muladd(x[i], DMODE == 0 ? D[i + j * W] : D[j + i * W], acc);
+            if (DMODE == 0 && !S::integral) acc = S::prod(acc, S::star(D[j + j * W]));
+            x[j] = acc;
+        }
+#pragma unroll
+        for (int j = 0; j < W; j++) xsh[j][lane] = x[j];
+    }
+    __syncthreads();
+    if (!valid) return;
+    if (q != 0) {
+#pragma unroll
+        for (int j = 0; j < W; j++) x[j] = xsh[j][lane];
+    }
     const T *Pp = P + a.p_poff[p];
     const int32_t *E = a.Eidx + a.p_eoff[p];
-    T x[W];
-#pragma unroll
-    for (int j = 0; j < W; j++) x[j] = j < w ? X[(i64)(c0 + j) * ld + r] : S::zero();
     const int t1 = min(e, (chunk + 1) * SCATTER_T);
     if (ATOMIC) {
         for (int t = chunk * SCATTER_T + q; t < t1; t += 4) {
@@ -744,14 +741,24 @@ __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(siz
     const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
     const T *Qp = Q + a.p_poff[p];
     const int32_t *E = a.Eidx + a.p_eoff[p];
+    const T *D = Dpack + a.p_doff[p];
     T acc[W];
 #pragma unroll
     for (int j = 0; j < W; j++) acc[j] = S::zero();
     if (q == 0 && (!a.init_lo || (r >= a.init_lo[p] && r < a.init_hi[p]))) {
+        // the panel's columns as the forward sweep left them, unsolved: finish its step x <- x D* here
 #pragma unroll
         for (int j = 0; j < W; j++) {
             const T v = xr[(i64)(c0 + min(j, w - 1)) * ld];
             acc[j] = j < w ? v : S::zero();
+        }
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            T s = acc[j];
+#pragma unroll
+            for (int i = 0; i < j; i++) s = S::muladd(acc[i], DMODE == 0 ? D[i + j * W] : D[j + i * W], s);
+            if (DMODE == 0 && !S::integral) s = S::prod(s, S::star(D[j + j * W]));
+            acc[j] = s;
         }
     }
     // this wave's share of the gather list, in groups of four columns, with the next BWD_NSET - 1 groups' loads in
@@ -811,7 +818,6 @@ __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(siz
 #pragma unroll
             for (int j = 0; j < W; j++) acc[j] = S::plus(acc[j], red[qq][j][lane]);
     }
-    const T *D = Dpack + a.p_doff[p];
 #pragma unroll
     for (int j = W - 1; j >= 0; j--) {
         T s = acc[j];
@@ -1078,20 +1084,8 @@ static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type
     const int32_t *tiles = base.pre;   // device copy of Wp.tiles
     SweepArgs a = base;
     if (fwd) {
-        // triangular solves of the panels' own columns
+        // one launch per list: the panels' own columns solved and scattered, per (64-row tile, target chunk)
         unsigned grid;
-        if (star_rows) {
-            a.pre = tiles + li.pA256;
-            grid = (unsigned)Wp.tiles[li.pA256 + li.cnt];
-        } else {
-            a.pre = nullptr;
-            grid = (unsigned)(li.cnt * ((nrows + TRSM_ROWS - 1) / TRSM_ROWS));
-        }
-        if (grid) {
-            if (dmode == 0) k_fwd_trsm<S, W, 0><<<grid, NT, 0, st>>>(X, ld, a, D);
-            else k_fwd_trsm<S, W, 1><<<grid, NT, 0, st>>>(X, ld, a, D);
-        }
-        // scatter into the extension columns
         a.cpre = tiles + li.pC;
         if (star_rows) {
             a.pre = tiles + li.pAu;
@@ -1101,8 +1095,13 @@ static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type
             grid = (unsigned)(((nrows + TILE_ROWS - 1) / TILE_ROWS) * Wp.tiles[li.pC + li.cnt]);
         }
         if (grid) {
-            if (atomic) k_fwd_scatter<S, W, true><<<grid, NT, 0, st>>>(X, ld, a, Pk);
-            else k_fwd_scatter<S, W, false><<<grid, NT, 0, st>>>(X, ld, a, Pk);
+            if (atomic) {
+                if (dmode == 0) k_fwd<S, W, true, 0><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+                else k_fwd<S, W, true, 1><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+            } else {
+                if (dmode == 0) k_fwd<S, W, false, 0><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+                else k_fwd<S, W, false, 1><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+            }
         }
     } else {
         unsigned grid;

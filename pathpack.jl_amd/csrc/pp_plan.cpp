@@ -221,7 +221,6 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
                 return off;
             };
             auto tiles_of = [&](i64 lo, i64 hi, i64 rows) { return (hi - lo + rows - 1) / rows; };
-            li.pA256 = prefix([&](int32_t p) { return tiles_of(P.rowA_lo[p], P.rowA_hi[p], TRSM_ROWS); });
             li.pAu = prefix([&](int32_t p) { return tiles_of(P.rowA_lo[p], P.rowA_hi[p], TILE_ROWS) * P.chunks[p]; });
             li.pB64 = prefix([&](int32_t p) { return tiles_of(P.rowB_lo[p], P.rowB_hi[p], TILE_ROWS); });
             li.pC = prefix([&](int32_t p) { return (i64)P.chunks[p]; });
