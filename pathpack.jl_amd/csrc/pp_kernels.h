@@ -613,13 +613,32 @@ __global__ __launch_bounds__(NT) void k_fwd(typename S::value_type *__restrict__
     const int r = lo + tile * TILE_ROWS + lane;
     const bool valid = r < hi;
     const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
+    const T *Pp = P + a.p_poff[p];
+    const int32_t *E = a.Eidx + a.p_eoff[p];
+    const int t1 = min(e, (chunk + 1) * SCATTER_T);
+    // the wave's targets t = tb + 4 i, in groups of four; the first two groups' loads are issued before the solve
+    // (they do not depend on it), and later the next two groups' loads stay in flight (three register sets in
+    // rotation).  The targets of a panel are distinct columns, so a load never meets a pending store.  Loads past
+    // the last target repeat it and are dropped.
+    const int tb = chunk * SCATTER_T + q;
+    const int ng = tb < t1 ? ((t1 - tb + 3) / 4 + 3) / 4 : 0;
+    T *xr = X + (valid ? r : hi - 1);
+    auto ldg = [&](int g, T(&v)[4]) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = xr[(i64)E[min(tb + 4 * (4 * g + u), t1 - 1)] * ld];
+        __builtin_amdgcn_sched_barrier(0);   // issue the loads here, ahead of the arithmetic that follows
+    };
+    T A[4], B[4], C[4];
+    if (!ATOMIC && ng > 0) {
+        ldg(0, A);
+        ldg(1, B);
+    }
     T x[W];
     if (q == 0) {
         const T *D = Dpack + a.p_doff[p];
-        const T *xr0 = X + (valid ? r : hi - 1);
 #pragma unroll
         for (int j = 0; j < W; j++) {
-            const T v = xr0[(i64)(c0 + min(j, w - 1)) * ld];
+            const T v = xr[(i64)(c0 + min(j, w - 1)) * ld];
             x[j] = j < w ? v : S::zero();
         }
 #pragma unroll
@@ -639,11 +658,8 @@ __global__ __launch_bounds__(NT) void k_fwd(typename S::value_type *__restrict__
 #pragma unroll
         for (int j = 0; j < W; j++) x[j] = xsh[j][lane];
     }
-    const T *Pp = P + a.p_poff[p];
-    const int32_t *E = a.Eidx + a.p_eoff[p];
-    const int t1 = min(e, (chunk + 1) * SCATTER_T);
     if (ATOMIC) {
-        for (int t = chunk * SCATTER_T + q; t < t1; t += 4) {
+        for (int t = tb; t < t1; t += 4) {
             const T *pc = Pp + (i64)t * W;
             T v = S::zero();
             if (W == 1) {
@@ -656,18 +672,7 @@ __global__ __launch_bounds__(NT) void k_fwd(typename S::value_type *__restrict__
         }
         return;
     }
-    // the wave's targets t = tb + 4 i, in groups of four with the next two groups' loads in flight (three register
-    // sets in rotation); the targets of a panel are distinct columns, so a load never meets a pending store.  Loads
-    // past the last target repeat it and are dropped.
-    const int tb = chunk * SCATTER_T + q;
-    if (tb >= t1) return;
-    const int ng = ((t1 - tb + 3) / 4 + 3) / 4;
-    T *xr = X + r;
-    auto ldg = [&](int g, T(&v)[4]) {
-#pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = xr[(i64)E[min(tb + 4 * (4 * g + u), t1 - 1)] * ld];
-        __builtin_amdgcn_sched_barrier(0);   // issue the loads here, ahead of the arithmetic that follows
-    };
+    if (ng == 0) return;
     auto upd = [&](int g, const T(&v)[4]) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -685,9 +690,6 @@ __global__ __launch_bounds__(NT) void k_fwd(typename S::value_type *__restrict__
             }
         }
     };
-    T A[4], B[4], C[4];
-    ldg(0, A);
-    ldg(1, B);
     int g = 0;
     for (; g + 3 <= ng; g += 3) {
         ldg(g + 2, C);
