@@ -523,6 +523,121 @@ std::string supernodal(const Adj &G, const std::vector<i64> &perm, const std::ve
     return "";
 }
 
+// The same with the front tree known in advance (parent[f] > f, fronts in postorder): disjoint subtrees are
+// independent, so the fronts below a cut of the tree run on `threads` threads (one subtree after another, each in
+// postorder, into per-thread buffers), then the fronts above the cut in postorder.  The result equals supernodal()'s.
+std::string supernodal_tree(const Adj &G, const std::vector<i64> &perm, const std::vector<i64> &Rptr,
+                            const std::vector<i64> &parent_in, int threads, std::vector<i64> &Sptr,
+                            std::vector<i32> &Stgt, std::vector<i64> &parent) {
+    const i64 n = G.n, nf = (i64)Rptr.size() - 1;
+    if (threads <= 1 || nf < 64) return supernodal(G, perm, Rptr, Sptr, Stgt, parent);
+    std::vector<i64> invp(n);
+    for (i64 k = 0; k < n; k++) invp[perm[k]] = k;
+    std::vector<i64> chead(nf, -1), cnext(nf, -1), ctail(nf, -1), first(nf), size(nf);
+    for (i64 f = 0; f < nf; f++) {
+        const i64 p = parent_in[f];
+        if (p >= 0) {
+            if (p <= f) return supernodal(G, perm, Rptr, Sptr, Stgt, parent);
+            if (ctail[p] < 0) chead[p] = f;
+            else cnext[ctail[p]] = f;
+            ctail[p] = f;
+        }
+    }
+    for (i64 f = 0; f < nf; f++) first[f] = f;
+    for (i64 f = 0; f < nf; f++)
+        if (parent_in[f] >= 0) first[parent_in[f]] = std::min(first[parent_in[f]], first[f]);
+    for (i64 f = 0; f < nf; f++) size[f] = Rptr[f + 1] - Rptr[first[f]];   // vertices in the subtree
+    // cut: split every subtree larger than n / (4 threads) into its children; the split fronts form the top
+    const i64 limit = std::max<i64>(1, n / (4 * (i64)threads));
+    std::vector<i64> tasks, stack;
+    std::vector<char> top(nf, 0);
+    for (i64 f = 0; f < nf; f++)
+        if (parent_in[f] < 0) stack.push_back(f);
+    while (!stack.empty()) {
+        const i64 f = stack.back();
+        stack.pop_back();
+        if (size[f] <= limit || chead[f] < 0) {
+            tasks.push_back(f);
+        } else {
+            top[f] = 1;
+            for (i64 c = chead[f]; c >= 0; c = cnext[c]) stack.push_back(c);
+        }
+    }
+    std::sort(tasks.begin(), tasks.end(), [&](i64 a, i64 b) { return size[a] > size[b]; });
+    // per front: (buffer, offset, length) of its separator
+    std::vector<int32_t> fbuf(nf, -1);
+    std::vector<i64> foff(nf, 0), flen(nf, 0);
+    std::vector<std::vector<i32>> bufs(threads + 1);
+    std::atomic<bool> bad(false);
+    auto front = [&](i64 f, std::vector<i32> &out, int bid, std::vector<i32> &mark, std::vector<i32> &buf) {
+        const i64 r0 = Rptr[f], r1 = Rptr[f + 1];
+        buf.clear();
+        for (i64 v = r0; v < r1; v++) {
+            const i64 ov = perm[v];
+            for (i64 q = G.xadj[ov]; q < G.xadj[ov + 1]; q++) {
+                const i64 u = invp[G.adj[q]];
+                if (u >= r1 && mark[u] != (i32)f) {
+                    mark[u] = (i32)f;
+                    buf.push_back((i32)u);
+                }
+            }
+        }
+        for (i64 c = chead[f]; c >= 0; c = cnext[c]) {
+            const i32 *sc = bufs[fbuf[c]].data() + foff[c];
+            for (i64 k = 0; k < flen[c]; k++) {
+                const i64 u = sc[k];
+                if (u < r0) bad = true;
+                if (u >= r1 && mark[u] != (i32)f) {
+                    mark[u] = (i32)f;
+                    buf.push_back((i32)u);
+                }
+            }
+        }
+        std::sort(buf.begin(), buf.end());
+        fbuf[f] = bid;
+        foff[f] = (i64)out.size();
+        flen[f] = (i64)buf.size();
+        out.insert(out.end(), buf.begin(), buf.end());
+    };
+    std::atomic<i64> next(0);
+    auto worker = [&](int t) {
+        std::vector<i32> mark(n, -1), buf;
+        while (true) {
+            const i64 k = next.fetch_add(1);
+            if (k >= (i64)tasks.size()) break;
+            const i64 root = tasks[k];
+            for (i64 f = first[root]; f <= root; f++) front(f, bufs[t], t, mark, buf);
+        }
+    };
+    {
+        std::vector<std::thread> pool;
+        for (int t = 1; t < threads; t++) pool.emplace_back(worker, t);
+        worker(0);
+        for (auto &th : pool) th.join();
+    }
+    {
+        std::vector<i32> mark(n, -1), buf;
+        for (i64 f = 0; f < nf; f++)
+            if (top[f]) front(f, bufs[threads], threads, mark, buf);
+    }
+    if (bad) return "front structure is not a postorder of its tree";
+    Sptr.assign(nf + 1, 0);
+    for (i64 f = 0; f < nf; f++) Sptr[f + 1] = Sptr[f] + flen[f];
+    Stgt.resize(Sptr[nf]);
+    for (i64 f = 0; f < nf; f++)
+        std::copy(bufs[fbuf[f]].begin() + foff[f], bufs[fbuf[f]].begin() + foff[f] + flen[f], Stgt.begin() + Sptr[f]);
+    // the tree the separators define must be the one given
+    parent.assign(nf, -1);
+    std::vector<i64> fof(n);
+    for (i64 f = 0; f < nf; f++)
+        for (i64 v = Rptr[f]; v < Rptr[f + 1]; v++) fof[v] = f;
+    for (i64 f = 0; f < nf; f++) {
+        parent[f] = flen[f] ? fof[Stgt[Sptr[f]]] : -1;
+        if (parent[f] != parent_in[f]) return supernodal(G, perm, Rptr, Sptr, Stgt, parent);
+    }
+    return "";
+}
+
 double now() {
     return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
 }
@@ -558,11 +673,12 @@ void work_counts(i64 n, const std::vector<i64> &Rptr, const std::vector<i64> &Sp
 }
 
 std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, std::vector<i64> perm,
-                   std::vector<i64> Rptr, Symbolic &out) {
+                   std::vector<i64> Rptr, Symbolic &out, const std::vector<i64> *tree = nullptr) {
     std::vector<i64> Sptr, parent;
     std::vector<i32> Stgt;
     double ts = now();
-    std::string err = supernodal(G, perm, Rptr, Sptr, Stgt, parent);
+    std::string err = tree ? supernodal_tree(G, perm, Rptr, *tree, analysis_threads(n), Sptr, Stgt, parent)
+                           : supernodal(G, perm, Rptr, Sptr, Stgt, parent);
     if (!err.empty()) return err;
     stage("  separators", ts);
     const i64 nf = (i64)Rptr.size() - 1;
@@ -721,7 +837,7 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
         out.nnzL_alg = l;
     }
     if (!opts.amalgamate) {
-        err = finish(G, n, colptr, rowval, perm1, R1, out);
+        err = finish(G, n, colptr, rowval, perm1, R1, out, &par1);
         out.seconds_total = now() - t0;
         return err;
     }
@@ -782,7 +898,7 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
             i64 top = members[s].back();
             if (par1[top] >= 0) mkids[root[par1[top]]].push_back(s);
         }
-    std::vector<i64> perm2, R2;
+    std::vector<i64> perm2, R2, fid(ns, -1);
     perm2.reserve(n);
     R2.push_back(0);
     std::vector<std::pair<i64, size_t>> stack;
@@ -800,14 +916,22 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
             } else {
                 for (i64 mem : members[m])
                     for (i64 v = R1[mem]; v < R1[mem + 1]; v++) perm2.push_back(perm1[v]);
+                fid[m] = (i64)R2.size() - 1;
                 R2.push_back((i64)perm2.size());
                 stack.pop_back();
             }
         }
     }
     if ((i64)perm2.size() != n) return "internal error: amalgamation lost vertices";
+    // the merged tree in the final numbering: a merged front's parent holds its top member's parent
+    std::vector<i64> tree2((i64)R2.size() - 1, -1);
+    for (i64 s = 0; s < ns; s++)
+        if (is_root[s]) {
+            const i64 top = members[s].back();
+            if (par1[top] >= 0) tree2[fid[s]] = fid[root[par1[top]]];
+        }
     stage("amalgamation", ts);
-    err = finish(G, n, colptr, rowval, perm2, R2, out);
+    err = finish(G, n, colptr, rowval, perm2, R2, out, &tree2);
     stage("final structure + entries", ts);
     out.seconds_total = now() - t0;
     return err;
