@@ -5,7 +5,6 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -39,8 +38,9 @@ pp_sym::~pp_sym() {
 }
 
 pp_fac::~pp_fac() {
-    // one block (stream-ordered pool of the context's stream): the plans and the factor arrays
+    // the blocks (stream-ordered pool of the context's stream): the plans and the factor arrays
     for (void *p : plan.owned) hipFreeAsync(p, ctx->stream);
+    if (fronts) hipFreeAsync(fronts, ctx->stream);
 }
 
 static bool supported(int semiring, int dtype) {
@@ -89,6 +89,7 @@ pp_status pp_destroy(pp_ctx *ctx) {
     for (auto &e : ctx->ev)
         if (e) hipEventDestroy(e);
     if (ctx->staging) hipHostFree(ctx->staging);
+    if (ctx->staging2) hipHostFree(ctx->staging2);
     delete ctx;
     return PP_OK;
 }
@@ -199,179 +200,191 @@ pp_status pp_sym_destroy(pp_sym *sym) {
 
 // ===== factor =====
 
-// The factor and sweep plans of a structure (a cache of the immutable structure), built on two threads.
-static std::string ensure_plans(const pp_sym *csym) {
-    pp_sym *sym = const_cast<pp_sym *>(csym);
-    if (sym->fplan && sym->splan) return "";
-    auto *f = sym->fplan ? nullptr : new pp::FactorPlan;
-    auto *s = sym->splan ? nullptr : new pp::SweepPlan;
-    std::string ef, es;
-    std::thread t;
-    if (s) t = std::thread([&] { es = pp::build_sweep_plan(sym->S, *s); });
-    if (f) ef = pp::build_factor_plan(sym->S, *f);
-    if (t.joinable()) t.join();
-    if (!ef.empty() || !es.empty()) {
-        delete f;
-        delete s;
-        return ef.empty() ? es : ef;
+// Device-plan upload: the host arrays of one block are laid out at 256-byte offsets, copied into a pinned staging
+// buffer and uploaded by one asynchronous copy; the bytes placed after them (the factor arrays) are not uploaded.
+struct Upload {
+    struct Part { const void *src; size_t bytes; size_t off; void **dst; };
+    std::vector<Part> parts;
+    size_t total = 0;
+    size_t place(size_t bytes) {
+        const size_t off = total;
+        total += (std::max<size_t>(bytes, 1) + 255) & ~size_t(255);
+        return off;
     }
-    if (f) sym->fplan = f;
-    if (s) sym->splan = s;
-    return "";
-}
+    template <class V, class P> void add(const V &vec, P **ptr) {
+        const size_t bytes = vec.size() * sizeof(vec[0]);
+        parts.push_back({vec.data(), bytes, place(bytes), (void **)ptr});
+    }
+    // allocate the block (stream-ordered pool), stage and upload the parts; the block's address into *block
+    std::string run(hipStream_t st, void *&staging, size_t &staging_bytes, size_t plan_bytes, void **block) {
+        if (staging_bytes < plan_bytes) {
+            if (staging) hipHostFree(staging);
+            staging = nullptr;
+            staging_bytes = 0;
+            if (hipHostMalloc(&staging, plan_bytes, hipHostMallocDefault) != hipSuccess)
+                return "pinned staging allocation failed";
+            staging_bytes = plan_bytes;
+        }
+        for (const Part &q : parts)
+            if (q.bytes) std::memcpy((char *)staging + q.off, q.src, q.bytes);
+        if (hipMallocAsync(block, total, st) != hipSuccess) return "hipMallocAsync of the factor failed";
+        for (const Part &q : parts) *q.dst = q.bytes ? (void *)((char *)*block + q.off) : nullptr;
+        if (hipMemcpyAsync(*block, staging, plan_bytes, hipMemcpyHostToDevice, st) != hipSuccess)
+            return "upload of the plans failed";
+        return "";
+    }
+};
 
-static pp_status factor_common(pp_ctx *ctx, const pp_sym *sym, int semiring, int dtype, const void *nzval,
+static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, int dtype, const void *nzval,
                                bool on_device, pp_fac **out) {
     if (!ctx) return fail(nullptr, PP_EINVAL, "pp_factor: null context");
-    if (!sym || !out) return fail(ctx, PP_EINVAL, "pp_factor: null argument");
+    if (!csym || !out) return fail(ctx, PP_EINVAL, "pp_factor: null argument");
     *out = nullptr;
     if (!supported(semiring, dtype)) return fail(ctx, PP_EUNSUPPORTED, "pp_factor: unsupported semiring / element type");
-    if (sym->S.nnz > 0 && !nzval) return fail(ctx, PP_EINVAL, "pp_factor: null nzval");
+    if (csym->S.nnz > 0 && !nzval) return fail(ctx, PP_EINVAL, "pp_factor: null nzval");
     CHECK_HIP(ctx, hipSetDevice(ctx->device));
-    const bool htime = std::getenv("PP_SYMTIME") != nullptr;   // host phases of pp_factor to stderr
-    auto hnow = [] { return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count(); };
-    double th = hnow();
-    auto hstage = [&](const char *what) {
-        if (!htime) return;
-        const double t = hnow();
-        std::fprintf(stderr, "pp_factor: %-28s %8.2f ms\n", what, (t - th) * 1e3);
-        th = t;
-    };
-    std::string e = ensure_plans(sym);
-    if (!e.empty()) return fail(ctx, PP_EINVAL, "pp_factor: " + e);
-    hstage("plans");
-    const pp::FactorPlan &P = *sym->fplan;
-    const pp::SweepPlan &W = *sym->splan;
+    pp_sym *sym = const_cast<pp_sym *>(csym);   // the plans are a cache of the immutable structure
     const pp::Symbolic &S = sym->S;
     const size_t es = (size_t)pp::dtype_size(dtype);
-    // device memory needed at the peak: the frontal arena, the factor in both layouts, the plans, the values
+    // The sweep plan is built on a second thread while this one builds the factor plan and the device factorizes;
+    // it is needed only for the packs at the end.
+    pp::SweepPlan *splan = sym->splan ? nullptr : new pp::SweepPlan;
+    std::string es_err;
+    std::thread sweep_thread;
+    if (splan) sweep_thread = std::thread([&] { es_err = pp::build_sweep_plan(S, *splan); });
+    auto join_sweep = [&]() -> std::string {
+        if (!sweep_thread.joinable()) return "";
+        sweep_thread.join();
+        if (!es_err.empty()) {
+            delete splan;
+            splan = nullptr;
+            return es_err;
+        }
+        sym->splan = splan;
+        splan = nullptr;
+        return "";
+    };
+    auto failj = [&](pp_status code, const std::string &msg) {
+        join_sweep();
+        return fail(ctx, code, msg);
+    };
+    if (!sym->fplan) {
+        auto *f = new pp::FactorPlan;
+        std::string e = pp::build_factor_plan(S, *f);
+        if (!e.empty()) {
+            delete f;
+            return failj(PP_EINVAL, "pp_factor: " + e);
+        }
+        sym->fplan = f;
+    }
+    const pp::FactorPlan &P = *sym->fplan;
+    // device memory at the peak (the packs are checked again once their size is known)
     const size_t nD = (size_t)S.Dptr[S.nf], nL = (size_t)S.Lptr[S.nf];
-    const size_t need = es * ((size_t)P.arena + nD + 2 * nL + (size_t)W.ndpack + 2 * (size_t)W.npack + (size_t)S.nnz) +
+    const size_t need = es * ((size_t)P.arena + nD + 2 * nL + (size_t)S.nnz) +
                         sizeof(i64) * (3 * (size_t)S.nnz + 6 * (size_t)S.nf + 2 * (size_t)S.n) +
-                        sizeof(int32_t) * (W.Eidx.size() + W.plist.size() + W.tiles.size() + 16 * (size_t)W.np +
-                                           P.ftask.size() + P.stask.size() + P.flist.size() + P.atask.size() +
+                        sizeof(int32_t) * (P.ftask.size() + P.stask.size() + P.flist.size() + P.atask.size() +
                                            P.relpos.size());
     size_t freeb = 0, totalb = 0;
-    CHECK_HIP(ctx, hipMemGetInfo(&freeb, &totalb));
+    if (hipMemGetInfo(&freeb, &totalb) != hipSuccess) return failj(PP_EHIP, "pp_factor: hipMemGetInfo failed");
     if (need > freeb)
-        return fail(ctx, PP_ENOMEM, "pp_factor: needs " + std::to_string(need) + " bytes of device memory, " +
-                                        std::to_string(freeb) + " free");
+        return failj(PP_ENOMEM, "pp_factor: needs " + std::to_string(need) + " bytes of device memory, " +
+                                    std::to_string(freeb) + " free");
     pp_fac *fac = new (std::nothrow) pp_fac;
-    if (!fac) return fail(ctx, PP_ENOMEM, "pp_factor: out of host memory");
+    if (!fac) return failj(PP_ENOMEM, "pp_factor: out of host memory");
     fac->ctx = ctx;
     fac->sym = sym;
     fac->semiring = semiring;
     fac->dtype = dtype;
     hipStream_t st = ctx->stream;
     pp::DevPlan &d = fac->plan;
-    // One device block holds the plans (uploaded by one copy from pinned staging) and the factor arrays.
-    std::vector<int32_t> invp32(S.invp.begin(), S.invp.end());
-    struct Part { const void *src; size_t bytes; size_t off; void **dst; };
-    std::vector<Part> parts;
-    size_t total = 0;
-    auto place = [&](size_t bytes) {
-        const size_t off = total;
-        total += (std::max<size_t>(bytes, 1) + 255) & ~size_t(255);
-        return off;
-    };
-    auto plan_part = [&](const auto &vec, auto **ptr) {
-        const size_t bytes = vec.size() * sizeof(vec[0]);
-        parts.push_back({vec.data(), bytes, place(bytes), (void **)ptr});
-    };
-    plan_part(P.nn, &d.nn);
-    plan_part(P.na, &d.na);
-    plan_part(P.nj, &d.nj);
-    plan_part(P.relpos, &d.relpos);
-    plan_part(P.chptr, &d.chptr);
-    plan_part(P.chidx, &d.chidx);
-    plan_part(P.Foff, &d.Foff);
-    plan_part(P.Sptr32, &d.Sptr);
-    plan_part(P.entry_pos, &d.entry_pos);
-    plan_part(P.flist, &d.flist);
-    plan_part(P.atask, &d.atask);
-    plan_part(P.etask, &d.etask);
-    plan_part(P.ftask, &d.ftask);
-    plan_part(P.stask, &d.stask);
-    plan_part(S.Dptr, &d.Dptr);
-    plan_part(S.Lptr, &d.Lptr);
-    plan_part(S.Rptr, &d.Rptr);
-    plan_part(W.front, &d.p_front);
-    plan_part(W.c0, &d.p_c0);
-    plan_part(W.w, &d.p_w);
-    plan_part(W.e, &d.p_e);
-    plan_part(W.lo_ext, &d.p_lo);
-    plan_part(W.chunks, &d.p_chunks);
-    plan_part(W.eoff, &d.p_eoff);
-    plan_part(W.poff, &d.p_poff);
-    plan_part(W.doff, &d.p_doff);
-    plan_part(W.rowA_lo, &d.p_rowA_lo);
-    plan_part(W.rowA_hi, &d.p_rowA_hi);
-    plan_part(W.rowB_lo, &d.p_rowB_lo);
-    plan_part(W.rowB_hi, &d.p_rowB_hi);
-    plan_part(W.Eidx, &d.Eidx);
-    plan_part(W.plist, &d.plist);
-    plan_part(W.tiles, &d.tiles);
-    plan_part(S.perm, &d.perm);
-    plan_part(S.invp, &d.invp);
-    plan_part(invp32, &d.invp32);
-    const size_t plan_bytes = total;
-    const size_t oLD = place(nD * es), oLL = place(nL * es), oUL = place(nL * es), oD = place(W.ndpack * es),
-                 oU = place(W.npack * es), oL = place(W.npack * es);
-    if (ctx->staging_bytes < plan_bytes) {
-        if (ctx->staging) hipHostFree(ctx->staging);
-        ctx->staging = nullptr;
-        ctx->staging_bytes = 0;
-        if (hipHostMalloc(&ctx->staging, plan_bytes, hipHostMallocDefault) != hipSuccess) {
-            delete fac;
-            return fail(ctx, PP_ENOMEM, "pp_factor: pinned staging allocation failed");
-        }
-        ctx->staging_bytes = plan_bytes;
-    }
-    hstage("layout + staging alloc");
-    for (const Part &q : parts)
-        if (q.bytes) std::memcpy((char *)ctx->staging + q.off, q.src, q.bytes);
-    hstage("staging copy");
-    void *block = nullptr;
-    if (hipMallocAsync(&block, total, st) != hipSuccess) {
+    auto failf = [&](pp_status code, const std::string &msg) {
+        hipStreamSynchronize(st);
         delete fac;
-        return fail(ctx, PP_ENOMEM, "pp_factor: hipMalloc of the factor failed");
-    }
-    d.owned.push_back(block);
-    for (const Part &q : parts) *q.dst = q.bytes ? (void *)((char *)block + q.off) : nullptr;
-    fac->LD = (char *)block + oLD;
-    fac->LL = (char *)block + oLL;
-    fac->UL = (char *)block + oUL;
-    fac->Dpack = (char *)block + oD;
-    fac->Upack = (char *)block + oU;
-    fac->Lpack = (char *)block + oL;
-    if (hipMemcpyAsync(block, ctx->staging, plan_bytes, hipMemcpyHostToDevice, st) != hipSuccess) {
-        delete fac;
-        return fail(ctx, PP_EHIP, "pp_factor: upload of the plans failed");
-    }
+        return failj(code, msg);
+    };
+    // block 1: the factor plan and the factor in the reference layout
+    Upload u1;
+    u1.add(P.nn, &d.nn);
+    u1.add(P.na, &d.na);
+    u1.add(P.nj, &d.nj);
+    u1.add(P.relpos, &d.relpos);
+    u1.add(P.chptr, &d.chptr);
+    u1.add(P.chidx, &d.chidx);
+    u1.add(P.Foff, &d.Foff);
+    u1.add(P.Sptr32, &d.Sptr);
+    u1.add(P.entry_pos, &d.entry_pos);
+    u1.add(P.flist, &d.flist);
+    u1.add(P.atask, &d.atask);
+    u1.add(P.etask, &d.etask);
+    u1.add(P.ftask, &d.ftask);
+    u1.add(P.stask, &d.stask);
+    u1.add(S.Dptr, &d.Dptr);
+    u1.add(S.Lptr, &d.Lptr);
+    u1.add(S.Rptr, &d.Rptr);
+    const size_t plan1 = u1.total;
+    const size_t oLD = u1.place(nD * es), oLL = u1.place(nL * es), oUL = u1.place(nL * es);
+    void *block1 = nullptr;
+    std::string e = u1.run(st, ctx->staging, ctx->staging_bytes, plan1, &block1);
+    if (!e.empty()) return failf(PP_ENOMEM, "pp_factor: " + e);
+    d.owned.push_back(block1);
+    fac->LD = (char *)block1 + oLD;
+    fac->LL = (char *)block1 + oLL;
+    fac->UL = (char *)block1 + oUL;
     const void *dnz = nzval;
     void *tmpnz = nullptr;
     if (!on_device && S.nnz > 0) {
-        if (hipMalloc(&tmpnz, S.nnz * es) != hipSuccess) {
-            delete fac;
-            return fail(ctx, PP_ENOMEM, "pp_factor: hipMalloc of the values failed");
-        }
+        if (hipMallocAsync(&tmpnz, S.nnz * es, st) != hipSuccess) return failf(PP_ENOMEM, "pp_factor: hipMalloc of the values failed");
         if (hipMemcpyAsync(tmpnz, nzval, S.nnz * es, hipMemcpyHostToDevice, st) != hipSuccess) {
-            hipFree(tmpnz);
-            delete fac;
-            return fail(ctx, PP_EHIP, "pp_factor: upload of the values failed");
+            hipFreeAsync(tmpnz, st);
+            return failf(PP_EHIP, "pp_factor: upload of the values failed");
         }
         dnz = tmpnz;
     }
-    hstage("alloc + upload issue");
     e = pp::device_factor(ctx, fac, dnz);
-    hstage("launches");
+    if (tmpnz) hipFreeAsync(tmpnz, st);
+    if (!e.empty()) return failf(PP_EHIP, "pp_factor: " + e);
+    // block 2: the sweep plan, the permutation and the sweep packs (built from the fronts before they are freed)
+    e = join_sweep();
+    if (!e.empty()) return failf(PP_EINVAL, "pp_factor: " + e);
+    const pp::SweepPlan &W = *sym->splan;
+    std::vector<int32_t> invp32(S.invp.begin(), S.invp.end());
+    Upload u2;
+    u2.add(W.front, &d.p_front);
+    u2.add(W.c0, &d.p_c0);
+    u2.add(W.w, &d.p_w);
+    u2.add(W.e, &d.p_e);
+    u2.add(W.lo_ext, &d.p_lo);
+    u2.add(W.chunks, &d.p_chunks);
+    u2.add(W.eoff, &d.p_eoff);
+    u2.add(W.poff, &d.p_poff);
+    u2.add(W.doff, &d.p_doff);
+    u2.add(W.rowA_lo, &d.p_rowA_lo);
+    u2.add(W.rowA_hi, &d.p_rowA_hi);
+    u2.add(W.rowB_lo, &d.p_rowB_lo);
+    u2.add(W.rowB_hi, &d.p_rowB_hi);
+    u2.add(W.Eidx, &d.Eidx);
+    u2.add(W.plist, &d.plist);
+    u2.add(W.tiles, &d.tiles);
+    u2.add(S.perm, &d.perm);
+    u2.add(S.invp, &d.invp);
+    u2.add(invp32, &d.invp32);
+    const size_t plan2 = u2.total;
+    const size_t oD = u2.place(W.ndpack * es), oU = u2.place(W.npack * es), oL = u2.place(W.npack * es);
+    if (hipMemGetInfo(&freeb, &totalb) != hipSuccess) return failf(PP_EHIP, "pp_factor: hipMemGetInfo failed");
+    if (u2.total > freeb)
+        return failf(PP_ENOMEM, "pp_factor: the sweep packs need " + std::to_string(u2.total) + " bytes of device memory, " +
+                                    std::to_string(freeb) + " free");
+    void *block2 = nullptr;
+    e = u2.run(st, ctx->staging2, ctx->staging2_bytes, plan2, &block2);
+    if (!e.empty()) return failf(PP_ENOMEM, "pp_factor: " + e);
+    d.owned.push_back(block2);
+    fac->Dpack = (char *)block2 + oD;
+    fac->Upack = (char *)block2 + oU;
+    fac->Lpack = (char *)block2 + oL;
+    e = pp::device_factor_packs(ctx, fac);
     hipError_t se = hipStreamSynchronize(st);
-    hstage("device wait");
-    if (tmpnz) hipFree(tmpnz);
-    if (!e.empty() || se != hipSuccess) {
-        delete fac;
-        return fail(ctx, PP_EHIP, "pp_factor: " + (e.empty() ? std::string(hipGetErrorString(se)) : e));
-    }
+    if (!e.empty() || se != hipSuccess)
+        return failf(PP_EHIP, "pp_factor: " + (e.empty() ? std::string(hipGetErrorString(se)) : e));
     *out = fac;
     return PP_OK;
 }
@@ -563,7 +576,16 @@ pp_status pp_set_timing(pp_ctx *ctx, int on) {
 
 pp_status pp_get_timing(const pp_ctx *ctx, double *t) {
     if (!ctx || !t) return fail(nullptr, PP_EINVAL, "pp_get_timing: null argument");
-    std::copy(ctx->t, ctx->t + 8, t);
+    pp_ctx *c = const_cast<pp_ctx *>(ctx);   // the times of recorded slots are read lazily
+    for (int s = 0; s < 8; s++)
+        if (c->pending[s]) {
+            float ms = 0;
+            if (hipEventSynchronize(c->ev[2 * s + 1]) == hipSuccess &&
+                hipEventElapsedTime(&ms, c->ev[2 * s], c->ev[2 * s + 1]) == hipSuccess)
+                c->t[s] = ms * 1e-3;
+            c->pending[s] = false;
+        }
+    std::copy(c->t, c->t + 8, t);
     return PP_OK;
 }
 

@@ -11,6 +11,7 @@
 namespace pp {
 
 template <class S> std::string factor_impl(pp_ctx *ctx, pp_fac *fac, const void *nz);
+template <class S> std::string packs_impl(pp_ctx *ctx, pp_fac *fac);
 template <class S> std::string star_impl(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc);
 template <class S> std::string solve_impl(pp_ctx *ctx, const pp_fac *fac, void *B, i64 ldb, i64 nrhs, bool left);
 template <class S>
@@ -105,6 +106,8 @@ std::string device_valu_peak(pp_ctx *ctx, int kind, int iters, double *seconds, 
 std::string device_factor(pp_ctx *ctx, pp_fac *fac, const void *d_nzval) {
     PP_DISPATCH(fac->semiring, fac->dtype, factor_impl<S>(ctx, fac, d_nzval));
 }
+
+std::string device_factor_packs(pp_ctx *ctx, pp_fac *fac) { PP_DISPATCH(fac->semiring, fac->dtype, packs_impl<S>(ctx, fac)); }
 
 std::string device_star(pp_ctx *ctx, const pp_fac *fac, void *d_out, i64 ldc) {
     PP_DISPATCH(fac->semiring, fac->dtype, star_impl<S>(ctx, fac, d_out, ldc));

@@ -136,9 +136,12 @@ struct pp_ctx {
     std::string err;
     int timing = 0;
     double t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    hipEvent_t ev[8] = {};
-    void *staging = nullptr;        // pinned host staging for host outputs
+    hipEvent_t ev[16] = {};          // start and stop event of each timing slot
+    bool pending[8] = {};            // a slot's events are recorded and its time not yet read
+    void *staging = nullptr;        // pinned host staging of the factor plan
     size_t staging_bytes = 0;
+    void *staging2 = nullptr;       // pinned host staging of the sweep plan
+    size_t staging2_bytes = 0;
 };
 
 struct pp_fac {
@@ -148,12 +151,14 @@ struct pp_fac {
     pp::DevPlan plan;
     void *LD = nullptr, *LL = nullptr, *UL = nullptr;     // reference layout
     void *Dpack = nullptr, *Upack = nullptr, *Lpack = nullptr;
+    void *fronts = nullptr;          // the frontal arena between the factorization and the packs
     ~pp_fac();
 };
 
 namespace pp {
 // Numeric drivers (pp_device.hip).  Return "" or an error message.
-std::string device_factor(pp_ctx *ctx, pp_fac *fac, const void *d_nzval);
+std::string device_factor(pp_ctx *ctx, pp_fac *fac, const void *d_nzval);   // up to the reference layout
+std::string device_factor_packs(pp_ctx *ctx, pp_fac *fac);                 // the sweep packs; frees the fronts
 std::string device_star(pp_ctx *ctx, const pp_fac *fac, void *d_out, i64 ldc);
 std::string device_rmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs);
 std::string device_lmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs);

@@ -996,21 +996,15 @@ __global__ __launch_bounds__(NT) void k_getrf_star(typename S::value_type *__res
 
 // ===== drivers =====
 
-struct Timer {
-    pp_ctx *ctx;
-    int slot;
-    Timer(pp_ctx *c, int s) : ctx(c), slot(s) {
-        if (ctx->timing) hipEventRecord(ctx->ev[0], ctx->stream);
-    }
-    void stop() {
-        if (!ctx->timing) return;
-        hipEventRecord(ctx->ev[1], ctx->stream);
-        hipEventSynchronize(ctx->ev[1]);
-        float ms = 0;
-        hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[1]);
-        ctx->t[slot] = ms * 1e-3;
-    }
-};
+// Timing slots: events on the context's stream, read by pp_get_timing (no synchronization here).
+inline void timer_start(pp_ctx *ctx, int slot) {
+    if (ctx->timing) hipEventRecord(ctx->ev[2 * slot], ctx->stream);
+}
+inline void timer_stop(pp_ctx *ctx, int slot) {
+    if (!ctx->timing) return;
+    hipEventRecord(ctx->ev[2 * slot + 1], ctx->stream);
+    ctx->pending[slot] = true;
+}
 
 template <class S> struct FactorRun {
     pp_ctx *ctx;
@@ -1021,12 +1015,12 @@ template <class S> struct FactorRun {
     std::string run() {
         typedef typename S::value_type T;
         const FactorPlan &P = *fac->sym->fplan;
-        const SweepPlan &W = *fac->sym->splan;
         const DevPlan &d = fac->plan;
         hipStream_t st = ctx->stream;
-        Timer tm(ctx, 0);
+        timer_start(ctx, 0);
         T *F = nullptr;
         HIPCHK(hipMallocAsync((void **)&F, std::max<i64>(1, P.arena) * sizeof(T), st));
+        fac->fronts = F;
         k_fill<T><<<grid1(P.arena), NT, 0, st>>>(F, P.arena, S::zero());
         LAUNCHCHK();
         if (fac->sym->S.nnz > 0)
@@ -1049,17 +1043,34 @@ template <class S> struct FactorRun {
             }
             LAUNCHCHK();
         }
-        const i64 nf = P.nf;
         if (P.etask.size())
             k_extract_ref<T><<<(unsigned)(P.etask.size() / 2), NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.Dptr, d.Lptr, d.etask,
                                                                             (T *)fac->LD, (T *)fac->LL, (T *)fac->UL);
+        LAUNCHCHK();
+        return "";
+    }
+};
+
+// The sweep packs from the factored fronts, then the fronts are freed (the end of the factorization's timing).
+template <class S> struct PacksRun {
+    pp_ctx *ctx;
+    pp_fac *fac;
+    std::string err;
+    void operator()() { err = run(); }
+    std::string run() {
+        typedef typename S::value_type T;
+        const SweepPlan &W = *fac->sym->splan;
+        const DevPlan &d = fac->plan;
+        hipStream_t st = ctx->stream;
+        T *F = (T *)fac->fronts;
         if (W.np > 0)
             k_build_packs<S><<<(unsigned)W.np, NT, 0, st>>>(F, d.Foff, d.nj, d.Rptr, d.p_front, d.p_c0, d.p_w, d.p_e,
                                                             d.p_lo, d.p_poff, d.p_doff, (T *)fac->Dpack,
                                                             (T *)fac->Upack, (T *)fac->Lpack);
         LAUNCHCHK();
         HIPCHK(hipFreeAsync(F, st));
-        tm.stop();
+        fac->fronts = nullptr;
+        timer_stop(ctx, 0);
         return "";
     }
 };
@@ -1194,7 +1205,7 @@ template <class S> struct StarRun {
         hipStream_t st = ctx->stream;
         T *X = nullptr;
         HIPCHK(hipMallocAsync((void **)&X, std::max<i64>(1, n * n) * sizeof(T), st));
-        Timer t1(ctx, 1);
+        timer_start(ctx, 1);
         const DevPlan &d = fac->plan;
         const i64 np = fac->sym->splan->np;
         if (np > 0)
@@ -1203,12 +1214,12 @@ template <class S> struct StarRun {
         LAUNCHCHK();
         std::string e = run_sweeps<S>(ctx, fac, true, 0, X, n, true, n, fac->Upack);
         if (!e.empty()) return e;
-        t1.stop();
-        Timer t2(ctx, 2);
+        timer_stop(ctx, 1);
+        timer_start(ctx, 2);
         e = run_sweeps<S>(ctx, fac, false, 0, X, n, true, n, fac->Lpack);
         if (!e.empty()) return e;
-        t2.stop();
-        Timer t3(ctx, 3);
+        timer_stop(ctx, 2);
+        timer_start(ctx, 3);
         if (n > 0) {
             constexpr i64 VW = 16 / sizeof(T);
             if (n * (i64)sizeof(T) <= RELABEL_LDS && n % VW == 0 && ldc % VW == 0 && ((uintptr_t)out & 15) == 0)
@@ -1218,7 +1229,7 @@ template <class S> struct StarRun {
                 k_relabel<T><<<(unsigned)n, NT, 0, st>>>(X, n, (T *)out, ldc, fac->plan.invp);
         }
         LAUNCHCHK();
-        t3.stop();
+        timer_stop(ctx, 3);
         HIPCHK(hipFreeAsync(X, st));
         return "";
     }
@@ -1239,7 +1250,7 @@ template <class S> struct SolveRun {
         if (n == 0 || nrhs == 0) return "";
         T *Y = nullptr;
         HIPCHK(hipMallocAsync((void **)&Y, n * nrhs * sizeof(T), st));
-        Timer tm(ctx, 4);
+        timer_start(ctx, 4);
         std::string e;
         if (!left) {
             // rmul!: B (nrhs x n) <- B A*: U forward, then L backward (chordal/sgetrs.jl:29-51)
@@ -1260,7 +1271,7 @@ template <class S> struct SolveRun {
             k_transpose_perm<T><<<g, NT, 0, st>>>((T *)B, ldb, Y, n, nrhs, fac->plan.invp, 1);
         }
         LAUNCHCHK();
-        tm.stop();
+        timer_stop(ctx, 4);
         HIPCHK(hipFreeAsync(Y, st));
         return "";
     }
@@ -1305,6 +1316,11 @@ template <class S> struct GetrfStarRun {
 
 template <class S> std::string factor_impl(pp_ctx *ctx, pp_fac *fac, const void *nz) {
     FactorRun<S> r{ctx, fac, nz};
+    r();
+    return r.err;
+}
+template <class S> std::string packs_impl(pp_ctx *ctx, pp_fac *fac) {
+    PacksRun<S> r{ctx, fac};
     r();
     return r.err;
 }

@@ -98,7 +98,7 @@ std::string symmetrize(i64 n, const i64 *colptr, const i64 *rowval, Adj &G) {
 // A work item is a vertex subset (all vertices v with part[v] == id) that owns the output positions
 // [hi - size, hi).  A connected item is split by one level of a breadth-first level structure rooted at a
 // pseudo-peripheral vertex (George & Liu, "Computer Solution of Large Sparse Positive Definite Systems", 1981):
-// the level with the fewest vertices among those leaving at least 30% of the item on each side.  The separator
+// the level with the fewest vertices among those leaving at least 35% of the item on each side.  The separator
 // takes the last positions; the two sides recurse.  Small items are ordered by minimum degree.
 
 struct ND {
