@@ -40,7 +40,6 @@ pp_sym::~pp_sym() {
 pp_fac::~pp_fac() {
     // the blocks (stream-ordered pool of the context's stream): the plans and the factor arrays
     for (void *p : plan.owned) hipFreeAsync(p, ctx->stream);
-    if (fronts) hipFreeAsync(fronts, ctx->stream);
 }
 
 static bool supported(int semiring, int dtype) {
@@ -282,7 +281,7 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     const size_t nD = (size_t)S.Dptr[S.nf], nL = (size_t)S.Lptr[S.nf];
     const size_t need = es * ((size_t)P.arena + nD + 2 * nL + (size_t)S.nnz) +
                         sizeof(i64) * (3 * (size_t)S.nnz + 6 * (size_t)S.nf + 2 * (size_t)S.n) +
-                        sizeof(int32_t) * (P.ftask.size() + P.stask.size() + P.flist.size() + P.atask.size() +
+                        sizeof(int32_t) * (P.stask.size() + P.flist.size() + P.atask.size() + P.etask.size() +
                                            P.relpos.size());
     size_t freeb = 0, totalb = 0;
     if (hipMemGetInfo(&freeb, &totalb) != hipSuccess) return failj(PP_EHIP, "pp_factor: hipMemGetInfo failed");
@@ -316,7 +315,6 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     u1.add(P.flist, &d.flist);
     u1.add(P.atask, &d.atask);
     u1.add(P.etask, &d.etask);
-    u1.add(P.ftask, &d.ftask);
     u1.add(P.stask, &d.stask);
     u1.add(S.Dptr, &d.Dptr);
     u1.add(S.Lptr, &d.Lptr);
@@ -343,7 +341,7 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     e = pp::device_factor(ctx, fac, dnz);
     if (tmpnz) hipFreeAsync(tmpnz, st);
     if (!e.empty()) return failf(PP_EHIP, "pp_factor: " + e);
-    // block 2: the sweep plan, the permutation and the sweep packs (built from the fronts before they are freed)
+    // block 2: the sweep plan, the permutation and the sweep packs (built from the factor)
     e = join_sweep();
     if (!e.empty()) return failf(PP_EINVAL, "pp_factor: " + e);
     const pp::SweepPlan &W = *sym->splan;

@@ -4,10 +4,11 @@
 // sep(f)) has a fixed place in one arena.  Fronts are grouped by height in the front tree (leaves 0); a height level
 // runs: extend-add of the children's update blocks F_c[nn_c:, nn_c:] into the parents (one workgroup per parent
 // column block, children one after another), then the partial LU of the fronts' first nn pivots.  Fronts with
-// nj <= MID_NJ are factorized by one workgroup in LDS; larger fronts take blocked steps of NB pivots: a panel kernel (LU of the
-// NB x NB diagonal block in LDS + triangular solves of the row and column panels) and a batched semiring GEMM on
-// the trailing block.  Afterwards the factor values are copied into the reference's storage layout and into
-// per-panel packs for the sweeps.
+// nj <= SMALL_NJ are factorized by one workgroup in LDS and their factor values copied into the reference's storage
+// layout afterwards; larger fronts take blocked steps of NB pivots, one launch per step over the 64 x 64 tiles of all
+// the level's trailing blocks (each tile factors the NB x NB diagonal block, solves its share of the row and column
+// panels and updates itself), and the steps write the factor values into the reference layout directly.  The
+// per-panel packs of the sweeps are built from the reference layout.
 //
 // Sweep plan.  Each front's residual is cut into panels of at most PANEL_W columns.  A panel p of front f covers
 // the permuted columns [c0, c0 + w); its "extension" E_p is the rest of the residual after the panel followed by
@@ -28,8 +29,7 @@
 
 namespace pp {
 
-constexpr int SMALL_NJ = 64;   // fronts up to this size are factorized in one workgroup's LDS ...
-constexpr int MID_NJ = 128;    // ... and up to this size too, in a workgroup with a larger LDS block
+constexpr int SMALL_NJ = 64;   // fronts up to this size are factorized in one workgroup's LDS
 constexpr int ASM_BLOCK = 16;  // parent columns per extend-add workgroup
 constexpr int EXTRACT_COLS = 32;  // frontal columns per factor-extraction workgroup
 constexpr int EIDX_PAD = 32;      // zero entries after the last gather list: sweeps read up to 16 entries ahead
@@ -56,21 +56,18 @@ struct FactorPlan {
     std::vector<i64> entry_pos;      // arena position of each stored entry of A
     // schedule
     struct Step {
-        i64 panel_off, panel_cnt;    // (front, chunk) pairs in ftask
-        i64 schur_off, schur_cnt;    // (front, ti, tj) triples in stask
+        i64 off, cnt;                // (front, pivot offset, ti, tj) tile tasks in stask
     };
     struct Level {
         i64 asm_off, asm_cnt;        // extend-add tasks (front, first parent column) in atask
         i64 small_off, small_cnt;    // fronts with nj <= SMALL_NJ, in flist
-        i64 mid_off, mid_cnt;        // fronts with SMALL_NJ < nj <= MID_NJ, in flist
-        std::vector<Step> steps;     // blocked steps for the large fronts
+        std::vector<Step> steps;     // blocked steps for the larger fronts
     };
     std::vector<Level> levels;
     std::vector<int32_t> flist;      // front lists of all levels
     std::vector<int32_t> atask;      // (front, first column) per extend-add task: 2 ints
-    std::vector<int32_t> etask;      // (front, first column) per extraction task: 2 ints
-    std::vector<int32_t> ftask;      // (front, step offset, chunk) per panel task: 3 ints
-    std::vector<int32_t> stask;      // (front, step offset, ti, tj) per Schur task: 4 ints
+    std::vector<int32_t> etask;      // (front, first column) per extraction task of a small front: 2 ints
+    std::vector<int32_t> stask;      // (front, step offset, ti, tj) per step tile: 4 ints
     i64 max_nj = 0;
 };
 
@@ -106,7 +103,7 @@ struct DevPlan {
     // factor
     int32_t *nn = nullptr, *na = nullptr, *nj = nullptr, *relpos = nullptr, *chptr = nullptr, *chidx = nullptr;
     i64 *Foff = nullptr, *Sptr = nullptr, *entry_pos = nullptr;
-    int32_t *flist = nullptr, *ftask = nullptr, *stask = nullptr, *atask = nullptr, *etask = nullptr;
+    int32_t *flist = nullptr, *stask = nullptr, *atask = nullptr, *etask = nullptr;
     i64 *Dptr = nullptr, *Lptr = nullptr, *Rptr = nullptr;
     // sweeps
     int32_t *p_front = nullptr, *p_c0 = nullptr, *p_w = nullptr, *p_e = nullptr, *p_lo = nullptr, *p_chunks = nullptr;
@@ -151,7 +148,6 @@ struct pp_fac {
     pp::DevPlan plan;
     void *LD = nullptr, *LL = nullptr, *UL = nullptr;     // reference layout
     void *Dpack = nullptr, *Upack = nullptr, *Lpack = nullptr;
-    void *fronts = nullptr;          // the frontal arena between the factorization and the packs
     ~pp_fac();
 };
 

@@ -160,41 +160,67 @@ template <class T> __device__ inline T bcast_lane(T v, int src) {
     }
 }
 
-// large fronts, step at pivot `off`: LU of the b x b diagonal block (redundantly in every chunk), then the chunk's
-// rows of the column panel (L <- L U_kk*, right upper non-unit) and columns of the row panel (U <- L_kk* U, left
-// lower unit).
+// Fronts with nj > SMALL_NJ, step at pivot `off` (b = min(NB, nn - off) pivots, trailing block from m0 = off + b):
+// one workgroup per 64 x 64 tile (ti, tj) of the trailing block, which
+//   - factors the b x b diagonal block D in registers (wave 0; every tile does it),
+//   - solves its 64 rows of the column panel, L <- A U_D* (wave 1), and its 64 columns of the row panel,
+//     U <- L_D* A (wave 2), into LDS,
+//   - applies the Schur update of its tile, A <- A (+) L (x) U (all waves; sgemx_mt!, chordal/sgetrf.jl:146).
+// The solved panels and D are final factor entries: the tiles of the first tile column / row store them straight
+// into the reference layout (LD, LL, UL), not into the arena, whose panel entries other tiles of the step still
+// read.  The arena keeps only the trailing blocks, down to the update matrix for the parent.
 //
-// The block is padded to NB x NB by repeating its last row and column.  A real entry (i, j < b) only ever meets
-// real entries: the LU updates it with pivots k < min(i, j), and a real unknown j of the solves reads unknowns
-// i < j and block entries D[i, j] with i, j < b.  The padded entries and unknowns hold whatever the same arithmetic
-// gives and are never stored.
+// D is padded to NB x NB by repeating its last row and column.  A real entry (i, j < b) only ever meets real
+// entries: the LU updates it with pivots k < min(i, j), and a real unknown j of the solves reads unknowns i < j
+// and block entries D[i, j] with i, j < b.  The padded entries and unknowns hold whatever the same arithmetic gives
+// and are never stored or used by the update (which runs over k < b).
 template <class S>
-__global__ __launch_bounds__(NT) void k_front_panel(typename S::value_type *__restrict__ F, const i64 *__restrict__ Foff,
-                                                    const int32_t *__restrict__ nn, const int32_t *__restrict__ nj,
-                                                    const int32_t *__restrict__ tasks) {
+__global__ __launch_bounds__(NT) void k_front_step(typename S::value_type *__restrict__ F, const i64 *__restrict__ Foff,
+                                                   const int32_t *__restrict__ nn, const int32_t *__restrict__ nj,
+                                                   const i64 *__restrict__ Dptr, const i64 *__restrict__ Lptr,
+                                                   typename S::value_type *__restrict__ LD,
+                                                   typename S::value_type *__restrict__ LL,
+                                                   typename S::value_type *__restrict__ UL,
+                                                   const int32_t *__restrict__ tasks) {
     typedef typename S::value_type T;
-    constexpr int LD = NB + 1;
-    __shared__ T D[NB * LD];
-    const int32_t *t = tasks + 3 * (i64)blockIdx.x;
-    const int f = t[0], off = t[1], chunk = t[2];
-    const int n = nj[f];
-    const int b = min(NB, nn[f] - off);
-    const int m0 = off + b;
+    constexpr int LDd = NB + 1, TG = 64;
+    __shared__ T Dl[NB * LDd];
+    __shared__ T Ls[NB][TG];   // the tile's rows of L, by pivot column
+    __shared__ T Us[NB][TG];   // the tile's columns of U, by pivot row
+    const int32_t *t = tasks + 4 * (i64)blockIdx.x;
+    const int f = t[0], off = t[1], ti = t[2], tj = t[3];
+    const int n = nj[f], a = nn[f];
+    const int b = min(NB, a - off), m0 = off + b;
     T *A = F + Foff[f];
-    const int r = m0 + chunk * NT + threadIdx.x;
-    const bool act = r < n;
-    const int rr = act ? r : n - 1;
-    // all loads are issued before the diagonal LU: the thread's row of the column panel and its column of the row
-    // panel, and wave 0's rows of the block
-    T x[NB], y[NB];
+    const int r0 = m0 + ti * TG, c0 = m0 + tj * TG;
+    const int mr = max(0, min(TG, n - r0)), mc = max(0, min(TG, n - c0));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    // the tile of the trailing block, 4 x 4 per thread (rows 4 tx + i, columns 4 ty + j)
+    T acc[4][4];
 #pragma unroll
-    for (int j = 0; j < NB; j++) x[j] = A[rr + (i64)(off + min(j, b - 1)) * n];
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int i = 0; i < NB; i++) y[i] = A[(off + min(i, b - 1)) + (i64)rr * n];
-    if (threadIdx.x < 64) {
-        // LU of the block in registers (dense/sgetrf.jl:151-175, the operations of lds_lu in the same order): lane i
-        // holds row i (lanes NB.. repeat lanes 0..NB-1), and pivot row k is read from lane k
-        const int i = threadIdx.x & (NB - 1);
+        for (int j = 0; j < 4; j++) {
+            const int r = 4 * tx + i, c = 4 * ty + j;
+            acc[i][j] = (r < mr && c < mc) ? A[(r0 + r) + (i64)(c0 + c) * n] : S::zero();
+        }
+    // the panel rows (wave 1) and columns (wave 2) of this tile; lanes past the end repeat the last one
+    T v[NB];
+    if (wave == 1 && mr > 0) {
+        const int r = r0 + min(lane, mr - 1);
+#pragma unroll
+        for (int j = 0; j < NB; j++) v[j] = A[r + (i64)(off + min(j, b - 1)) * n];
+    }
+    if (wave == 2 && mc > 0) {
+        const int c = c0 + min(lane, mc - 1);
+#pragma unroll
+        for (int i = 0; i < NB; i++) v[i] = A[(off + min(i, b - 1)) + (i64)c * n];
+    }
+    if (wave == 0) {
+        // LU of D in registers (dense/sgetrf.jl:151-175, the operations of lds_lu in the same order): lane i holds
+        // row i (lanes NB.. repeat lanes 0..NB-1), and pivot row k is read from lane k
+        const int i = lane & (NB - 1);
         const int ic = min(i, b - 1);
         T d[NB];
 #pragma unroll
@@ -208,50 +234,97 @@ __global__ __launch_bounds__(NT) void k_front_panel(typename S::value_type *__re
             }
 #pragma unroll
             for (int j = k + 1; j < NB; j++) {
-                const T v = S::muladd(d[k], bcast_lane(d[j], k), d[j]);
-                d[j] = below ? v : d[j];
+                const T w = S::muladd(d[k], bcast_lane(d[j], k), d[j]);
+                d[j] = below ? w : d[j];
             }
         }
-        if (threadIdx.x < NB) {
+        if (lane < NB) {
 #pragma unroll
-            for (int j = 0; j < NB; j++) D[i + j * LD] = d[j];
-            if (chunk == 0 && i < b) {
+            for (int j = 0; j < NB; j++) Dl[i + j * LDd] = d[j];
+            if (ti == 0 && tj == 0 && i < b) {
+                T *dst = LD + Dptr[f] + (off + i) + (i64)off * a;
 #pragma unroll
                 for (int j = 0; j < NB; j++)
-                    if (j < b) A[(off + i) + (i64)(off + j) * n] = d[j];
+                    if (j < b) dst[(i64)j * a] = d[j];
             }
         }
     }
     __syncthreads();
-    if (act) {
-        // row r of the column panel: x <- x U_kk*
+    if (wave == 1 && mr > 0) {
+        // rows of the column panel: x <- x U_D*
 #pragma unroll
         for (int j = 0; j < NB; j++) {
-            T acc = x[j];
+            T s = v[j];
 #pragma unroll
-            for (int i = 0; i < j; i++) acc = S::muladd(x[i], D[i + j * LD], acc);
-            if (!S::integral) acc = S::prod(acc, S::star(D[j + j * LD]));
-            x[j] = acc;
+            for (int i = 0; i < j; i++) s = S::muladd(v[i], Dl[i + j * LDd], s);
+            if (!S::integral) s = S::prod(s, S::star(Dl[j + j * LDd]));
+            v[j] = s;
             // compiler barrier: column j is computed before the LDS reads of column j + 1 are issued, which bounds
-            // the live registers (otherwise all D reads are hoisted and the arithmetic sunk, and the kernel spills)
-            asm volatile("" : "+v"(x[j])::"memory");
+            // the live registers
+            asm volatile("" : "+v"(v[j])::"memory");
         }
 #pragma unroll
-        for (int j = 0; j < NB; j++)
-            if (j < b) A[r + (i64)(off + j) * n] = x[j];
-        // column r of the row panel: y <- L_kk* y
+        for (int j = 0; j < NB; j++) Ls[j][lane] = v[j];
+        if (tj == 0 && lane < mr) {
+            const int r = r0 + lane;
+            T *dst = r < a ? LD + Dptr[f] + r + (i64)off * a : LL + Lptr[f] + (r - a) + (i64)off * (n - a);
+            const i64 ldd = r < a ? a : n - a;
+#pragma unroll
+            for (int j = 0; j < NB; j++)
+                if (j < b) dst[j * ldd] = v[j];
+        }
+    }
+    if (wave == 2 && mc > 0) {
+        // columns of the row panel: y <- L_D* y
 #pragma unroll
         for (int i = 0; i < NB; i++) {
-            T acc = y[i];
+            T s = v[i];
 #pragma unroll
-            for (int k = 0; k < i; k++) acc = S::muladd(D[i + k * LD], y[k], acc);
-            y[i] = acc;
-            asm volatile("" : "+v"(y[i])::"memory");
+            for (int k = 0; k < i; k++) s = S::muladd(Dl[i + k * LDd], v[k], s);
+            v[i] = s;
+            asm volatile("" : "+v"(v[i])::"memory");
         }
 #pragma unroll
-        for (int i = 0; i < NB; i++)
-            if (i < b) A[(off + i) + (i64)r * n] = y[i];
+        for (int i = 0; i < NB; i++) Us[i][lane] = v[i];
+        if (ti == 0 && lane < mc) {
+            const int c = c0 + lane;
+            T *dst = c < a ? LD + Dptr[f] + off + (i64)c * a : UL + Lptr[f] + off + (i64)(c - a) * a;
+#pragma unroll
+            for (int i = 0; i < NB; i++)
+                if (i < b) dst[i] = v[i];
+        }
     }
+    __syncthreads();
+    if (mr == 0 || mc == 0) return;
+    // the Schur update of the tile over the step's b pivots
+    int k = 0;
+    for (; k + 2 <= b; k += 2) {
+        T a0[4], a1[4], b0[4], b1[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            a0[i] = Ls[k][4 * tx + i];
+            a1[i] = Ls[k + 1][4 * tx + i];
+            b0[i] = Us[k][4 * ty + i];
+            b1[i] = Us[k + 1][4 * ty + i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] = S::muladd2(a0[i], b0[j], a1[i], b1[j], acc[i][j]);
+    }
+    if (k < b) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] = S::muladd(Ls[k][4 * tx + i], Us[k][4 * ty + j], acc[i][j]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = 4 * tx + i, c = 4 * ty + j;
+            if (r < mr && c < mc) A[(r0 + r) + (i64)(c0 + c) * n] = acc[i][j];
+        }
 }
 
 // ===== semiring GEMM tile: C[64 x 64] <- C (+) A[64 x k] (x) B[k x 64], column-major operands =====
@@ -304,23 +377,6 @@ __device__ inline void gemm_tile(typename S::value_type *__restrict__ C, i64 ldc
             const int r = tx * 4 + i, c = ty * 4 + j;
             if (r < m && c < n) C[r + c * ldc] = acc[i][j];
         }
-}
-
-// Schur update of the large fronts: F22 <- F22 (+) L_panel (x) U_panel (sgemx_mt!, chordal/sgetrf.jl:146)
-template <class S>
-__global__ __launch_bounds__(NT) void k_front_schur(typename S::value_type *__restrict__ F, const i64 *__restrict__ Foff,
-                                                    const int32_t *__restrict__ nn, const int32_t *__restrict__ nj,
-                                                    const int32_t *__restrict__ tasks) {
-    typedef typename S::value_type T;
-    const int32_t *t = tasks + 4 * (i64)blockIdx.x;
-    const int f = t[0], off = t[1], ti = t[2], tj = t[3];
-    const int n = nj[f];
-    const int b = min(NB, nn[f] - off);
-    const int m0 = off + b;
-    const int r0 = m0 + ti * GT, c0 = m0 + tj * GT;
-    T *A = F + Foff[f];
-    gemm_tile<S>(A + r0 + (i64)c0 * n, n, A + r0 + (i64)off * n, n, A + off + (i64)c0 * n, n, min(GT, n - r0),
-                 min(GT, n - c0), b);
 }
 
 template <class S>
@@ -497,8 +553,12 @@ __global__ __launch_bounds__(NT) void k_extract_ref(const T *__restrict__ F, con
 // Dpack (Wc x Wc) / Upack / Lpack (e x Wc) of every panel, Wc = the panel's width class; padding holds the semiring
 // zero.  One workgroup per panel.
 template <class S>
-__global__ __launch_bounds__(NT) void k_build_packs(const typename S::value_type *__restrict__ F, const i64 *__restrict__ Foff,
-                                                   const int32_t *__restrict__ nj, const i64 *__restrict__ Rptr,
+__global__ __launch_bounds__(NT) void k_build_packs(const typename S::value_type *__restrict__ LD,
+                                                   const typename S::value_type *__restrict__ LL,
+                                                   const typename S::value_type *__restrict__ UL,
+                                                   const i64 *__restrict__ Dptr, const i64 *__restrict__ Lptr,
+                                                   const int32_t *__restrict__ nn, const int32_t *__restrict__ nj,
+                                                   const i64 *__restrict__ Rptr,
                                                    const int32_t *__restrict__ p_front, const int32_t *__restrict__ p_c0,
                                                    const int32_t *__restrict__ p_w, const int32_t *__restrict__ p_e,
                                                    const int32_t *__restrict__ p_lo, const i64 *__restrict__ p_poff,
@@ -510,18 +570,31 @@ __global__ __launch_bounds__(NT) void k_build_packs(const typename S::value_type
     const int f = p_front[p], w = p_w[p], e = p_e[p], lo = p_lo[p];
     int Wc = 1;
     while (Wc < w) Wc <<= 1;
-    const int n = nj[f];
+    const int a = nn[f], c = nj[f] - a;
     const int lj0 = p_c0[p] - (int)Rptr[f];
-    const T *G = F + Foff[f];
+    const T *D = LD + Dptr[f];
+    const T *Lf = LL + Lptr[f];   // c x a
+    const T *Uf = UL + Lptr[f];   // a x c
     const int sh = __builtin_ctz(Wc);
     for (int q = threadIdx.x; q < Wc * Wc; q += NT) {
         const int i = q & (Wc - 1), j = q >> sh;
-        Dpack[p_doff[p] + q] = (i < w && j < w) ? G[(lj0 + i) + (i64)(lj0 + j) * n] : S::zero();
+        Dpack[p_doff[p] + q] = (i < w && j < w) ? D[(lj0 + i) + (i64)(lj0 + j) * a] : S::zero();
     }
     for (int q = threadIdx.x; q < Wc * e; q += NT) {
         const int j = q & (Wc - 1), t = q >> sh;   // element (j, t) at t*Wc + j
-        Upack[p_poff[p] + q] = j < w ? G[(lj0 + j) + (i64)(lo + t) * n] : S::zero();
-        Lpack[p_poff[p] + q] = j < w ? G[(lo + t) + (i64)(lj0 + j) * n] : S::zero();
+        const int col = lo + t;                    // local index of the extension column
+        T u = S::zero(), l = S::zero();
+        if (j < w) {
+            if (col < a) {
+                u = D[(lj0 + j) + (i64)col * a];
+                l = D[col + (i64)(lj0 + j) * a];
+            } else {
+                u = Uf[(lj0 + j) + (i64)(col - a) * a];
+                l = Lf[(col - a) + (i64)(lj0 + j) * c];
+            }
+        }
+        Upack[p_poff[p] + q] = u;
+        Lpack[p_poff[p] + q] = l;
     }
 }
 
@@ -1020,7 +1093,6 @@ template <class S> struct FactorRun {
         timer_start(ctx, 0);
         T *F = nullptr;
         HIPCHK(hipMallocAsync((void **)&F, std::max<i64>(1, P.arena) * sizeof(T), st));
-        fac->fronts = F;
         k_fill<T><<<grid1(P.arena), NT, 0, st>>>(F, P.arena, S::zero());
         LAUNCHCHK();
         if (fac->sym->S.nnz > 0)
@@ -1033,25 +1105,22 @@ template <class S> struct FactorRun {
             if (L.small_cnt)
                 k_front_small<S, SMALL_NJ><<<(unsigned)L.small_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.nj,
                                                                                   d.flist + L.small_off);
-            if (L.mid_cnt)
-                k_front_small<S, MID_NJ><<<(unsigned)L.mid_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.flist + L.mid_off);
-            for (const auto &s : L.steps) {
-                if (s.panel_cnt)
-                    k_front_panel<S><<<(unsigned)s.panel_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.ftask + 3 * s.panel_off);
-                if (s.schur_cnt)
-                    k_front_schur<S><<<(unsigned)s.schur_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.stask + 4 * s.schur_off);
-            }
+            for (const auto &s : L.steps)
+                if (s.cnt)
+                    k_front_step<S><<<(unsigned)s.cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.Dptr, d.Lptr, (T *)fac->LD,
+                                                                    (T *)fac->LL, (T *)fac->UL, d.stask + 4 * s.off);
             LAUNCHCHK();
         }
         if (P.etask.size())
             k_extract_ref<T><<<(unsigned)(P.etask.size() / 2), NT, 0, st>>>(F, d.Foff, d.nn, d.nj, d.Dptr, d.Lptr, d.etask,
                                                                             (T *)fac->LD, (T *)fac->LL, (T *)fac->UL);
         LAUNCHCHK();
+        HIPCHK(hipFreeAsync(F, st));
         return "";
     }
 };
 
-// The sweep packs from the factored fronts, then the fronts are freed (the end of the factorization's timing).
+// The sweep packs from the factor in the reference layout (the end of the factorization's timing).
 template <class S> struct PacksRun {
     pp_ctx *ctx;
     pp_fac *fac;
@@ -1062,14 +1131,12 @@ template <class S> struct PacksRun {
         const SweepPlan &W = *fac->sym->splan;
         const DevPlan &d = fac->plan;
         hipStream_t st = ctx->stream;
-        T *F = (T *)fac->fronts;
         if (W.np > 0)
-            k_build_packs<S><<<(unsigned)W.np, NT, 0, st>>>(F, d.Foff, d.nj, d.Rptr, d.p_front, d.p_c0, d.p_w, d.p_e,
-                                                            d.p_lo, d.p_poff, d.p_doff, (T *)fac->Dpack,
+            k_build_packs<S><<<(unsigned)W.np, NT, 0, st>>>((const T *)fac->LD, (const T *)fac->LL, (const T *)fac->UL,
+                                                            d.Dptr, d.Lptr, d.nn, d.nj, d.Rptr, d.p_front, d.p_c0, d.p_w,
+                                                            d.p_e, d.p_lo, d.p_poff, d.p_doff, (T *)fac->Dpack,
                                                             (T *)fac->Upack, (T *)fac->Lpack);
         LAUNCHCHK();
-        HIPCHK(hipFreeAsync(F, st));
-        fac->fronts = nullptr;
         timer_stop(ctx, 0);
         return "";
     }

@@ -68,16 +68,16 @@ std::string build_factor_plan(const Symbolic &S, FactorPlan &P) {
     }
     std::vector<std::vector<int32_t>> byh(H);
     for (i64 f = 0; f < nf; f++) byh[h[f]].push_back((int32_t)f);
-    P.etask.clear();
+    P.etask.clear();   // the small fronts' factors are copied out of the arena; the steps write theirs directly
     for (i64 f = 0; f < nf; f++)
-        for (int32_t c = 0; c < P.nj[f]; c += EXTRACT_COLS) {
-            P.etask.push_back((int32_t)f);
-            P.etask.push_back(c);
-        }
+        if (P.nj[f] <= SMALL_NJ)
+            for (int32_t c = 0; c < P.nj[f]; c += EXTRACT_COLS) {
+                P.etask.push_back((int32_t)f);
+                P.etask.push_back(c);
+            }
     P.levels.clear();
     P.flist.clear();
     P.atask.clear();
-    P.ftask.clear();
     P.stask.clear();
     for (i64 l = 0; l < H; l++) {
         FactorPlan::Level L;
@@ -93,27 +93,18 @@ std::string build_factor_plan(const Symbolic &S, FactorPlan &P) {
         for (int32_t f : byh[l])
             if (P.nj[f] <= SMALL_NJ) P.flist.push_back(f);
         L.small_cnt = (i64)P.flist.size() - L.small_off;
-        L.mid_off = (i64)P.flist.size();
-        for (int32_t f : byh[l])
-            if (P.nj[f] > SMALL_NJ && P.nj[f] <= MID_NJ) P.flist.push_back(f);
-        L.mid_cnt = (i64)P.flist.size() - L.mid_off;
         i64 maxsteps = 0;
         for (int32_t f : byh[l])
-            if (P.nj[f] > MID_NJ) maxsteps = std::max<i64>(maxsteps, (P.nn[f] + NB - 1) / NB);
+            if (P.nj[f] > SMALL_NJ) maxsteps = std::max<i64>(maxsteps, (P.nn[f] + NB - 1) / NB);
         for (i64 s = 0; s < maxsteps; s++) {
             FactorPlan::Step st;
-            st.panel_off = (i64)P.ftask.size() / 3;
-            st.schur_off = (i64)P.stask.size() / 4;
+            st.off = (i64)P.stask.size() / 4;
             for (int32_t f : byh[l]) {
-                if (P.nj[f] <= MID_NJ || s * NB >= P.nn[f]) continue;
-                i64 off = s * NB, b = std::min<i64>(NB, P.nn[f] - off), m = P.nj[f] - off - b;
-                i64 chunks = std::max<i64>(1, (m + 255) / 256);
-                for (i64 c = 0; c < chunks; c++) {
-                    P.ftask.push_back(f);
-                    P.ftask.push_back((int32_t)off);
-                    P.ftask.push_back((int32_t)c);
-                }
-                i64 T = (m + 63) / 64;
+                if (P.nj[f] <= SMALL_NJ || s * NB >= P.nn[f]) continue;
+                // one task per 64 x 64 tile of the trailing block; a step with no trailing block still has one
+                // task, for its diagonal block
+                const i64 off = s * NB, b = std::min<i64>(NB, P.nn[f] - off), m = P.nj[f] - off - b;
+                const i64 T = std::max<i64>(1, (m + 63) / 64);
                 for (i64 ti = 0; ti < T; ti++)
                     for (i64 tj = 0; tj < T; tj++) {
                         P.stask.push_back(f);
@@ -122,8 +113,7 @@ std::string build_factor_plan(const Symbolic &S, FactorPlan &P) {
                         P.stask.push_back((int32_t)tj);
                     }
             }
-            st.panel_cnt = (i64)P.ftask.size() / 3 - st.panel_off;
-            st.schur_cnt = (i64)P.stask.size() / 4 - st.schur_off;
+            st.cnt = (i64)P.stask.size() / 4 - st.off;
             L.steps.push_back(st);
         }
         P.levels.push_back(std::move(L));
