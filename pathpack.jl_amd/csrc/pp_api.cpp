@@ -363,11 +363,19 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     u2.add(W.Eidx, &d.Eidx);
     u2.add(W.plist, &d.plist);
     u2.add(W.tiles, &d.tiles);
+    u2.add(W.b_boff, &d.b_boff);
+    u2.add(W.b_hoff, &d.b_hoff);
+    u2.add(W.b_kp, &d.b_kp);
+    u2.add(W.b_ep, &d.b_ep);
+    u2.add(W.b_bn, &d.b_bn);
+    u2.add(W.prep, &d.prep);
+    u2.add(W.sunits, &d.sunits);
     u2.add(S.perm, &d.perm);
     u2.add(S.invp, &d.invp);
     u2.add(invp32, &d.invp32);
     const size_t plan2 = u2.total;
     const size_t oD = u2.place(W.ndpack * es), oU = u2.place(W.npack * es), oL = u2.place(W.npack * es);
+    const size_t oB = u2.place(W.nbpack * es), oH = u2.place(W.nhpack * es);
     if (hipMemGetInfo(&freeb, &totalb) != hipSuccess) return failf(PP_EHIP, "pp_factor: hipMemGetInfo failed");
     if (u2.total > freeb)
         return failf(PP_ENOMEM, "pp_factor: the sweep packs need " + std::to_string(u2.total) + " bytes of device memory, " +
@@ -379,6 +387,8 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     fac->Dpack = (char *)block2 + oD;
     fac->Upack = (char *)block2 + oU;
     fac->Lpack = (char *)block2 + oL;
+    fac->Bpack = (char *)block2 + oB;
+    fac->Hpack = (char *)block2 + oH;
     e = pp::device_factor_packs(ctx, fac);
     hipError_t se = hipStreamSynchronize(st);
     if (!e.empty() || se != hipSuccess)

@@ -18,6 +18,19 @@
 // with Wc the panel's width class (the power of two >= w); the padding holds the semiring zero.
 // A forward sweep visits panels leaves to root (each panel after its front's previous panel and after all
 // panels of its children), a backward sweep root to leaves.
+//
+// Star blocks.  For the star, a front with more than PANEL_W columns is cut into blocks of at most BLK_W columns
+// (and panels for a rest of at most PANEL_W columns), which run as register-tiled semiring GEMMs over whole row
+// tiles.  A block b of width w, tile width bn (BLK_W, or BLK_W / 2 when w fits), with diagonal blocks L_bb (unit
+// lower) and U_bb (upper) and extension E_b (as for a panel) carries two packs built at factor time:
+//   Bpack[b]  (kp x bn, k-major, kp = w + e rounded up to BLK_K): rows 0..w-1 hold M_b = U_bb* (x) L_bb*, rows
+//             w + t hold G_b[t, :] = L[E_t, blk] (x) L_bb*;
+//   Hpack[b]  (wp x ep, k-major, wp = w rounded up to BLK_K, ep = e rounded up to BLK_W): H_b = U_bb* (x) U[blk, E].
+// Forward step:  X[R, E] <- X[R, E] (+) X[R, blk] (x) H_b over the rows R of the block's subtree (X[R, blk] as
+// accumulated, unsolved).  Backward step: X[:, blk] <- X[:, blk] (x) M_b (+) X[:, E] (x) G_b over the component's
+// rows, X[:, blk] taken as zero outside R.  In exact arithmetic this is the panel recurrence (U_bb* solves the
+// forward step, L_bb* the backward one).  Block units have ids np .. np + nb - 1 in the per-panel arrays; the solves
+// use the panels only.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -38,6 +51,10 @@ constexpr int PANEL_W = 32;    // widest sweep panel
 constexpr int NCLASS = 6;      // sweep width classes 1, 2, 4, 8, 16, 32
 constexpr int TILE_ROWS = 64;    // rows per scatter / backward workgroup (one per lane, 4 waves)
 constexpr int SCATTER_T = 128;   // extension columns per scatter workgroup
+constexpr int BLK_W = 128;       // widest star block (the GEMM tile's column count)
+constexpr int BLK_K = 16;        // k step of the block GEMMs (pack rows are padded to a multiple)
+constexpr int BLK_CLS = 7;       // list class of star blocks with bn = BLK_W (BLK_CLS + 1: bn = BLK_W / 2)
+constexpr int PREP_T = 64;       // output tile of the block-pack GEMMs
 
 inline int width_class(int w) {
     int c = 0;
@@ -72,15 +89,23 @@ struct FactorPlan {
 };
 
 struct SweepPlan {
-    i64 np = 0;
-    // per panel
+    i64 np = 0;                      // panels (ids 0 .. np-1)
+    i64 nb = 0;                      // star blocks (ids np .. np+nb-1)
+    // per panel, then per block
     std::vector<int32_t> front, c0, w, e, lo_ext, chunks;   // chunks: ceil(e / SCATTER_T), at least 1
     std::vector<i64> eoff, poff, doff;
     std::vector<int32_t> rowA_lo, rowA_hi, rowB_lo, rowB_hi;   // rows of the star sweeps
     std::vector<int32_t> Eidx;       // extension column indices (permuted labels)
     i64 npack = 0, ndpack = 0;
+    // per block (index id - np)
+    std::vector<i64> b_boff, b_hoff;     // Bpack / Hpack offsets
+    std::vector<int32_t> b_kp, b_ep;     // Bpack rows, Hpack row stride
+    std::vector<int32_t> b_bn;           // tile width (Bpack row stride)
+    i64 nbpack = 0, nhpack = 0;
+    std::vector<int32_t> prep;           // block-pack GEMM tiles: (block, part, tile row, tile column)
+    std::vector<int32_t> sunits;         // the star's units: panels of fronts with at most PANEL_W columns, blocks
     struct List {
-        int cls;                     // width class
+        int cls;                     // width class (BLK_CLS, BLK_CLS + 1: star blocks)
         i64 off, cnt;                // panel ids in plist
         // offsets into `tiles` of per-panel prefix sums (cnt + 1 entries each): forward units (tiles x chunks)
         // over the star's forward rows, backward tiles over its backward rows, chunks
@@ -88,8 +113,10 @@ struct SweepPlan {
         i64 esum;                    // sum of the panels' gather-list lengths
         bool uniB;                   // every panel of the list has the same backward rows [rowB_lo, rowB_hi)
         int32_t rowB_lo, rowB_hi;
+        i64 pT[2];                   // block lists: per-block prefix of GEMM tiles for 64 and 128 rows per tile
     };
-    std::vector<List> fwd, bwd;      // in execution order
+    std::vector<List> fwd, bwd;      // in execution order (panels; the solves)
+    std::vector<List> sfwd, sbwd;    // the star's (panels of small fronts and blocks)
     std::vector<int32_t> plist;
     std::vector<int32_t> tiles;      // the prefix sums of all lists
     i64 max_e = 0;
@@ -110,6 +137,8 @@ struct DevPlan {
     i64 *p_eoff = nullptr, *p_poff = nullptr, *p_doff = nullptr;
     int32_t *p_rowA_lo = nullptr, *p_rowA_hi = nullptr, *p_rowB_lo = nullptr, *p_rowB_hi = nullptr;
     int32_t *Eidx = nullptr, *plist = nullptr, *tiles = nullptr;
+    i64 *b_boff = nullptr, *b_hoff = nullptr;
+    int32_t *b_kp = nullptr, *b_ep = nullptr, *b_bn = nullptr, *prep = nullptr, *sunits = nullptr;
     // permutation
     i64 *perm = nullptr, *invp = nullptr;
     int32_t *invp32 = nullptr;
@@ -148,6 +177,7 @@ struct pp_fac {
     pp::DevPlan plan;
     void *LD = nullptr, *LL = nullptr, *UL = nullptr;     // reference layout
     void *Dpack = nullptr, *Upack = nullptr, *Lpack = nullptr;
+    void *Bpack = nullptr, *Hpack = nullptr;             // star blocks
     ~pp_fac();
 };
 

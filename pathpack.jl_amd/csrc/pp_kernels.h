@@ -52,24 +52,26 @@ __global__ void k_scatter_entries(T *__restrict__ F, const i64 *__restrict__ pos
     for (i64 i = blockIdx.x * (i64)NT + threadIdx.x; i < nnz; i += (i64)gridDim.x * NT) F[pos[i]] = val[i];
 }
 
-// X <- I in the semiring (the start of X <- U*), on the entries the sweeps read before writing them: column c of
-// panel p over the rows [alo[p], ahi[p]) of its subtree (every forward write into column c comes from a panel of
+// X <- I in the semiring (the start of X <- U*), on the entries the sweeps read before writing them, for the star's
+// units (panels and blocks) p: column c of p over the rows [alo[p], ahi[p]) of its subtree (every forward write into column c comes from a panel of
 // that subtree; the backward sweep takes the other rows of its component as zero), and over the rows outside the
 // component [blo[p], bhi[p]), which no sweep visits.
 template <class S>
 __global__ __launch_bounds__(NT) void k_identity_panels(typename S::value_type *__restrict__ X, i64 n,
+                                                        const int32_t *__restrict__ units,
                                                         const int32_t *__restrict__ c0, const int32_t *__restrict__ w,
                                                         const int32_t *__restrict__ alo, const int32_t *__restrict__ ahi,
                                                         const int32_t *__restrict__ blo,
                                                         const int32_t *__restrict__ bhi) {
     typedef typename S::value_type T;
-    const int p = blockIdx.x, j = blockIdx.y;
-    if (j >= w[p]) return;
-    const i64 col = c0[p] + j;
-    T *x = X + col * n;
-    for (i64 i = alo[p] + threadIdx.x; i < ahi[p]; i += NT) x[i] = i == col ? S::one() : S::zero();
-    for (i64 i = threadIdx.x; i < blo[p]; i += NT) x[i] = S::zero();
-    for (i64 i = bhi[p] + threadIdx.x; i < n; i += NT) x[i] = S::zero();
+    const int p = units[blockIdx.x];
+    for (int j = blockIdx.y; j < w[p]; j += gridDim.y) {
+        const i64 col = c0[p] + j;
+        T *x = X + col * n;
+        for (i64 i = alo[p] + threadIdx.x; i < ahi[p]; i += NT) x[i] = i == col ? S::one() : S::zero();
+        for (i64 i = threadIdx.x; i < blo[p]; i += NT) x[i] = S::zero();
+        for (i64 i = bhi[p] + threadIdx.x; i < n; i += NT) x[i] = S::zero();
+    }
 }
 
 // ===== extend-add: F_f <- F_f (+) inj M_c inj^T for every child c (sgetrf_send!, chordal/sgetrf.jl:257-290) =====
@@ -908,6 +910,354 @@ __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(siz
     }
 }
 
+// ===== star blocks: fronts with more than PANEL_W columns, in blocks of at most BLK_W columns =====
+//
+// Per block b (columns c_0 .. c_{w-1} of front f, local start cb; extension E_b as for a panel):
+//   Lstar = L_bb* (unit lower), Ustar = U_bb* (upper, with the diagonal stars for non-integral semirings), the two
+//   recurrences the panel kernels run in registers (the forward solve x <- x U_bb*, the backward x <- x L_bb*);
+//   Bpack = [Ustar (x) Lstar; L[E, blk] (x) Lstar] and Hpack = Ustar (x) U[blk, E].
+
+// L[E_t, c_i] and U[c_i, E_t] of block-local column i and extension entry t (frontal local index lo + t), read from
+// the reference layout: LD (nn x nn, L strict lower and U upper), LL (na x nn), UL (nn x na)
+template <class T> struct FrontView {
+    const T *D, *Lf, *Uf;
+    int nn, na, cb, lo;
+    __device__ T L_ext(int t, int i) const {
+        const int col = lo + t;
+        return col < nn ? D[col + (i64)(cb + i) * nn] : Lf[(col - nn) + (i64)(cb + i) * na];
+    }
+    __device__ T U_ext(int i, int t) const {
+        const int col = lo + t;
+        return col < nn ? D[(cb + i) + (i64)col * nn] : Uf[(cb + i) + (i64)(col - nn) * nn];
+    }
+    __device__ T diag(int i, int j) const { return D[(cb + i) + (i64)(cb + j) * nn]; }
+};
+
+template <class T>
+__device__ inline FrontView<T> front_view(const T *LD, const T *LL, const T *UL, const i64 *Dptr, const i64 *Lptr,
+                                          const int32_t *nn, const int32_t *nj, const i64 *Rptr, int f, int c0, int lo) {
+    FrontView<T> v;
+    v.nn = nn[f];
+    v.na = nj[f] - v.nn;
+    v.D = LD + Dptr[f];
+    v.Lf = LL + Lptr[f];
+    v.Uf = UL + Lptr[f];
+    v.cb = c0 - (int)Rptr[f];
+    v.lo = lo;
+    return v;
+}
+
+// One workgroup per block: Lstar (column c per thread) and then Ustar (row r per thread) in LDS, written to
+// `stars` at 2 BLK_W^2 per block (Lstar, then Ustar; column-major, zero outside w x w).  A column of Lstar is zero
+// above its diagonal and a row of Ustar left of it, so each thread starts at its own index.  For 4-byte elements the
+// diagonal block is staged in LDS as well.
+template <class S>
+__global__ __launch_bounds__(NT) void k_blk_stars(const typename S::value_type *__restrict__ LD,
+                                                 const i64 *__restrict__ Dptr, const int32_t *__restrict__ nn,
+                                                 const i64 *__restrict__ Rptr, const int32_t *__restrict__ p_front,
+                                                 const int32_t *__restrict__ p_c0, const int32_t *__restrict__ p_w,
+                                                 int np, typename S::value_type *__restrict__ stars) {
+    typedef typename S::value_type T;
+    constexpr int LDX = BLK_W + 1;
+    constexpr bool DLDS = sizeof(T) == 4;
+    __shared__ T x[BLK_W * LDX];                  // x[k * LDX + thread]
+    __shared__ T dl[DLDS ? BLK_W * LDX : 1];      // dl[i + j * LDX] = diagonal-block entry (i, j)
+    const int id = np + blockIdx.x;
+    const int f = p_front[id], w = p_w[id];
+    const int a = nn[f], cb = p_c0[id] - (int)Rptr[f];
+    const T *Dg = LD + Dptr[f] + cb + (i64)cb * a;   // Dg[i + j a] = diagonal-block entry (i, j)
+    if (DLDS)
+        for (int q = threadIdx.x; q < w * w; q += NT) dl[(q % w) + (q / w) * LDX] = Dg[(q % w) + (i64)(q / w) * a];
+    __syncthreads();
+    auto Dv = [&](int i, int j) -> T { return DLDS ? dl[i + j * LDX] : Dg[i + (i64)j * a]; };
+    T *Ls = stars + (i64)blockIdx.x * 2 * BLK_W * BLK_W, *Us = Ls + BLK_W * BLK_W;
+    const int c = threadIdx.x;
+    // Lstar, column c: y_i = [i == c] (+) sum_{c <= k < i} L(i, k) y_k  (y_k = zero for k < c)
+    if (c < w) {
+        x[c * LDX + c] = S::one();
+        for (int i = c + 1; i < w; i++) {
+            T a0 = S::zero(), a1 = S::zero();
+            int k = c;
+            for (; k + 1 < i; k += 2) {
+                a0 = S::muladd(Dv(i, k), x[k * LDX + c], a0);
+                a1 = S::muladd(Dv(i, k + 1), x[(k + 1) * LDX + c], a1);
+            }
+            if (k < i) a0 = S::muladd(Dv(i, k), x[k * LDX + c], a0);
+            x[i * LDX + c] = S::plus(a0, a1);
+        }
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < BLK_W * BLK_W; q += NT) {
+        const int i = q % BLK_W, j = q / BLK_W;
+        Ls[q] = (i < w && j < w && i >= j) ? x[i * LDX + j] : S::zero();
+    }
+    __syncthreads();
+    // Ustar, row r: y_j = ([j == r] (+) sum_{r <= k < j} y_k U(k, j)) (x) U(j, j)*  (y_j = zero for j < r)
+    if (c < w) {
+        for (int j = c; j < w; j++) {
+            T a0 = S::zero(), a1 = S::zero();
+            int k = c;
+            for (; k + 1 < j; k += 2) {
+                a0 = S::muladd(x[k * LDX + c], Dv(k, j), a0);
+                a1 = S::muladd(x[(k + 1) * LDX + c], Dv(k + 1, j), a1);
+            }
+            if (k < j) a0 = S::muladd(x[k * LDX + c], Dv(k, j), a0);
+            T acc = S::plus(j == c ? S::one() : S::zero(), S::plus(a0, a1));
+            if (!S::integral) acc = S::prod(acc, S::star(Dv(j, j)));
+            x[j * LDX + c] = acc;
+        }
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < BLK_W * BLK_W; q += NT) {
+        const int i = q % BLK_W, j = q / BLK_W;   // Ustar(i, j) = y_j of row i
+        Us[q] = (i < w && j < w && j >= i) ? x[j * LDX + i] : S::zero();
+    }
+}
+
+// The packs, one PREP_T x PREP_T output tile per workgroup, K = w <= BLK_W with both operands in LDS:
+//   part 0: Bpack rows 0..w-1      = Ustar (x) Lstar      (row stride bn)
+//   part 1: Bpack rows w..w+e-1    = L[E, blk] (x) Lstar
+//   part 2: Hpack (w x e, stride ep) = Ustar (x) U[blk, E]
+template <class S>
+__global__ __launch_bounds__(NT) void k_blk_prep(const typename S::value_type *__restrict__ LD,
+                                                const typename S::value_type *__restrict__ LL,
+                                                const typename S::value_type *__restrict__ UL,
+                                                const i64 *__restrict__ Dptr, const i64 *__restrict__ Lptr,
+                                                const int32_t *__restrict__ nn, const int32_t *__restrict__ nj,
+                                                const i64 *__restrict__ Rptr, const int32_t *__restrict__ p_front,
+                                                const int32_t *__restrict__ p_c0, const int32_t *__restrict__ p_w,
+                                                const int32_t *__restrict__ p_e, const int32_t *__restrict__ p_lo,
+                                                int np, const int32_t *__restrict__ tasks,
+                                                const typename S::value_type *__restrict__ stars,
+                                                const i64 *__restrict__ b_boff, const i64 *__restrict__ b_hoff,
+                                                const int32_t *__restrict__ b_ep, const int32_t *__restrict__ b_bn,
+                                                typename S::value_type *__restrict__ Bpack,
+                                                typename S::value_type *__restrict__ Hpack) {
+    typedef typename S::value_type T;
+    constexpr int PT = PREP_T;
+    __shared__ T As[BLK_W][PT];   // As[i][r]
+    __shared__ T Bs[BLK_W][PT];   // Bs[i][c]
+    const int b = tasks[4 * blockIdx.x], part = tasks[4 * blockIdx.x + 1];
+    const int r0 = tasks[4 * blockIdx.x + 2] * PT, q0 = tasks[4 * blockIdx.x + 3] * PT;
+    const int id = np + b, f = p_front[id], w = p_w[id], e = p_e[id];
+    const FrontView<T> fv = front_view(LD, LL, UL, Dptr, Lptr, nn, nj, Rptr, f, p_c0[id], p_lo[id]);
+    const T *Ls = stars + (i64)b * 2 * BLK_W * BLK_W, *Us = Ls + BLK_W * BLK_W;
+    const int rows = part == 1 ? e : w, cols = part == 2 ? e : w;
+    for (int q = threadIdx.x; q < BLK_W * PT; q += NT) {
+        const int r = q % PT, i = q / PT;   // A(r0 + r, i)
+        T v = S::zero();
+        if (i < w && r0 + r < rows) v = part == 1 ? fv.L_ext(r0 + r, i) : Us[(r0 + r) + i * BLK_W];
+        As[i][r] = v;
+    }
+    for (int q = threadIdx.x; q < BLK_W * PT; q += NT) {
+        const int i = q % BLK_W, cc = q / BLK_W;   // B(i, q0 + cc)
+        T v = S::zero();
+        if (i < w && q0 + cc < cols) v = part == 2 ? fv.U_ext(i, q0 + cc) : Ls[i + (q0 + cc) * BLK_W];
+        Bs[i][cc] = v;
+    }
+    __syncthreads();
+    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    T acc[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) acc[u][v] = S::zero();
+    for (int i = 0; i < w; i++) {
+        T av[4], bv[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) av[u] = As[i][4 * tx + u];
+#pragma unroll
+        for (int v = 0; v < 4; v++) bv[v] = Bs[i][4 * ty + v];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[u][v] = S::muladd(av[u], bv[v], acc[u][v]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int r = r0 + 4 * tx + u, cc = q0 + 4 * ty + v;
+            if (r >= rows || cc >= cols) continue;
+            if (part == 0) Bpack[b_boff[b] + (i64)r * b_bn[b] + cc] = acc[u][v];
+            else if (part == 1) Bpack[b_boff[b] + (i64)(w + r) * b_bn[b] + cc] = acc[u][v];
+            else Hpack[b_hoff[b] + (i64)r * b_ep[b] + cc] = acc[u][v];
+        }
+}
+
+struct BlkArgs {
+    const int32_t *ulist;        // the list's unit ids (blocks: id >= np)
+    const int32_t *pre;          // per-unit prefix of GEMM tiles (for this kernel's rows per tile)
+    int32_t nu, np, ntask;
+    i64 nrows;                   // rows of X
+    const int32_t *p_c0, *p_w, *p_e;
+    const int32_t *rlo, *rhi;    // the rows this sweep writes
+    const int32_t *olo, *ohi;    // backward: the rows where the forward sweep left the block's columns
+    const i64 *p_eoff;
+    const int32_t *Eidx;
+    const i64 *b_boff, *b_hoff;
+    const int32_t *b_ep;
+};
+
+// Block step as a semiring GEMM over a BM x BN tile (BM = 16 TM, BN = 16 TN; 256 threads, 16 x 16, each a TM x TN
+// register block whose rows are groups of four, 64 apart, and likewise its columns; K in steps of BLK_K through two
+// LDS buffers with the next step's loads in registers, as k_gemm_tiled).  The backward's BN is the block's tile
+// width bn; the forward's tiles cover BLK_W extension entries.  Row tiles start at multiples of BM; rows outside the
+// sweep's range are computed from in-range memory and not stored.
+//   FWD:  C = X[r, E_t] (t in the tile's 128 extension entries) <- C (+) sum_{k < w} X[r, c_k] (x) Hpack[k, t]
+//   !FWD: X[r, c_j] <- sum_{k < w} X'[r, c_k] (x) Bpack[k, j] (+) sum_{t < e} X[r, E_t] (x) Bpack[w + t, j], with
+//         X' = X on the rows [olo, ohi) and zero elsewhere; a workgroup owns all w columns of its rows, reads them
+//         before it writes them, and no other workgroup touches them.
+// Workgroups are dealt to the 8 XCDs round-robin; XCD x takes the consecutive tiles [x per, (x + 1) per), so
+// neighbouring tiles (the same rows of a forward block, the same pack of a backward block) share its L2.
+template <class S, int TM, int TN, bool FWD>
+__global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict__ X, i64 ld, BlkArgs a,
+                                             const typename S::value_type *__restrict__ Pk) {
+    typedef typename S::value_type T;
+    constexpr int BM = 16 * TM, BN = 16 * TN, BK = BLK_K, PAD = 4;
+    typedef typename Vec16<T>::type V;
+    constexpr int VW = 16 / (int)sizeof(T);
+    constexpr int AQ = BM * BK / (256 * VW), BQ = BN * BK / (256 * VW);   // vectors per thread per k step
+    __shared__ __attribute__((aligned(16))) T As[2][BK][BM];
+    __shared__ __attribute__((aligned(16))) T Bs[2][BK][BN + PAD];
+    const int per = (int)(gridDim.x >> 3);
+    const int task = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+    if (task >= a.ntask) return;
+    const int ui = search(a.pre, a.nu, task);
+    const int u = task - a.pre[ui];
+    const int id = a.ulist[ui], b = id - a.np;
+    const int c0 = a.p_c0[id], w = a.p_w[id], e = a.p_e[id];
+    const int32_t *E = a.Eidx + a.p_eoff[id];
+    const int lo = a.rlo[id], hi = a.rhi[id];
+    int rt = u, ct = 0;
+    if (FWD) {
+        const int nct = (e + BN - 1) / BN;
+        rt = u / nct;
+        ct = u - rt * nct;
+    }
+    const i64 r0 = (i64)(lo / BM) * BM + (i64)rt * BM;
+    const int K = FWD ? w : w + e;
+    const int olo = FWD ? 0 : a.olo[id], ohi = FWD ? 0 : a.ohi[id];
+    const T *B = FWD ? Pk + a.b_hoff[b] + (i64)ct * BN : Pk + a.b_boff[b];
+    const i64 ldb = FWD ? a.b_ep[b] : BN;
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    // the backward's own columns contribute only on the rows [olo, ohi): a tile without such rows starts at w
+    const bool own = FWD || (r0 < ohi && r0 + BM > olo);
+    const int kbeg = own ? 0 : (w / BK) * BK, kend = (K + BK - 1) / BK * BK;
+    const bool vec = r0 + BM <= a.nrows && ld % VW == 0 && ((uintptr_t)X & 15) == 0;
+    auto colA = [&](int k) -> i64 {
+        if (FWD) return c0 + min(k, w - 1);
+        return k < w ? c0 + k : (k < K ? E[k - w] : c0);
+    };
+    T ra[AQ * VW], rb[BQ * VW];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int q = 0; q < AQ; q++) {
+            const int ev = (tid + 256 * q) * VW, r = ev % BM, kk = ev / BM, k = k0 + kk;
+            const T *src = X + (r0 + r) + colA(k) * ld;
+            if (vec) {
+                const V v = *reinterpret_cast<const V *>(src);
+#pragma unroll
+                for (int t = 0; t < VW; t++) ra[q * VW + t] = v[t];
+            } else {
+#pragma unroll
+                for (int t = 0; t < VW; t++) ra[q * VW + t] = r0 + r + t < a.nrows ? src[t] : S::zero();
+            }
+            if (!FWD && k < w) {
+#pragma unroll
+                for (int t = 0; t < VW; t++) {
+                    const i64 rr = r0 + r + t;
+                    if (rr < olo || rr >= ohi) ra[q * VW + t] = S::zero();
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < BQ; q++) {
+            const int ev = (tid + 256 * q) * VW, c = ev % BN, kk = ev / BN;
+            const V v = *reinterpret_cast<const V *>(B + (i64)(k0 + kk) * ldb + c);
+#pragma unroll
+            for (int t = 0; t < VW; t++) rb[q * VW + t] = v[t];
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < AQ; q++) {
+            const int ev = (tid + 256 * q) * VW;
+            V v;
+#pragma unroll
+            for (int t = 0; t < VW; t++) v[t] = ra[q * VW + t];
+            *reinterpret_cast<V *>(&As[buf][ev / BM][ev % BM]) = v;
+        }
+#pragma unroll
+        for (int q = 0; q < BQ; q++) {
+            const int ev = (tid + 256 * q) * VW;
+            V v;
+#pragma unroll
+            for (int t = 0; t < VW; t++) v[t] = rb[q * VW + t];
+            *reinterpret_cast<V *>(&Bs[buf][ev / BN][ev % BN]) = v;
+        }
+    };
+    auto rowof = [&](int i) { return 64 * (i >> 2) + 4 * tx + (i & 3); };
+    auto colof = [&](int j) { return 64 * (j >> 2) + 4 * ty + (j & 3); };
+    T acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            acc[i][j] = S::zero();
+            if (FWD) {
+                const i64 r = r0 + rowof(i);
+                const int t = ct * BN + colof(j);
+                if (r >= lo && r < hi && t < e) acc[i][j] = X[r + (i64)E[t] * ld];
+            }
+        }
+    if (kbeg < kend) {
+        gload(kbeg);
+        sstore(0);
+    }
+    __syncthreads();
+    int buf = 0;
+    for (int k0 = kbeg; k0 < kend; k0 += BK) {
+        const bool more = k0 + BK < kend;
+        if (more) gload(k0 + BK);
+#pragma unroll 1
+        for (int kk = 0; kk < BK; kk += 2) {
+            T a0[TM], a1[TM], b0[TN], b1[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                a0[i] = As[buf][kk][rowof(i)];
+                a1[i] = As[buf][kk + 1][rowof(i)];
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                b0[j] = Bs[buf][kk][colof(j)];
+                b1[j] = Bs[buf][kk + 1][colof(j)];
+            }
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) acc[i][j] = S::muladd2(a0[i], b0[j], a1[i], b1[j], acc[i][j]);
+        }
+        if (more) sstore(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const i64 r = r0 + rowof(i);
+            if (r < lo || r >= hi) continue;
+            if (FWD) {
+                const int t = ct * BN + colof(j);
+                if (t < e) X[r + (i64)E[t] * ld] = acc[i][j];
+            } else {
+                const int jj = colof(j);
+                if (jj < w) X[r + (i64)(c0 + jj) * ld] = acc[i][j];
+            }
+        }
+}
+
 // ===== relabel and permutations =====
 
 // C[i, j] = X[invp[i], invp[j]]  (C <- P^-1 X Q^-1, permuterowscols!, utils.jl:261-505): one workgroup per column
@@ -1137,6 +1487,22 @@ template <class S> struct PacksRun {
                                                             d.p_e, d.p_lo, d.p_poff, d.p_doff, (T *)fac->Dpack,
                                                             (T *)fac->Upack, (T *)fac->Lpack);
         LAUNCHCHK();
+        if (W.nb > 0) {
+            // star blocks: L_bb*, U_bb* into a scratch, then the GEMM packs (zero padding first)
+            T *stars = nullptr;
+            HIPCHK(hipMallocAsync((void **)&stars, (size_t)W.nb * 2 * BLK_W * BLK_W * sizeof(T), st));
+            k_fill<T><<<grid1(W.nbpack), NT, 0, st>>>((T *)fac->Bpack, W.nbpack, S::zero());
+            if (W.nhpack) k_fill<T><<<grid1(W.nhpack), NT, 0, st>>>((T *)fac->Hpack, W.nhpack, S::zero());
+            k_blk_stars<S><<<(unsigned)W.nb, NT, 0, st>>>((const T *)fac->LD, d.Dptr, d.nn, d.Rptr, d.p_front, d.p_c0,
+                                                          d.p_w, (int)W.np, stars);
+            if (W.prep.size())
+                k_blk_prep<S><<<(unsigned)(W.prep.size() / 4), NT, 0, st>>>(
+                    (const T *)fac->LD, (const T *)fac->LL, (const T *)fac->UL, d.Dptr, d.Lptr, d.nn, d.nj, d.Rptr,
+                    d.p_front, d.p_c0, d.p_w, d.p_e, d.p_lo, (int)W.np, d.prep, stars, d.b_boff, d.b_hoff, d.b_ep,
+                    d.b_bn, (T *)fac->Bpack, (T *)fac->Hpack);
+            LAUNCHCHK();
+            HIPCHK(hipFreeAsync(stars, st));
+        }
         timer_stop(ctx, 0);
         return "";
     }
@@ -1217,15 +1583,71 @@ static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type
 
 // Run the forward or backward lists of the sweep plan over X.  star_rows: each panel's own row range of the star;
 // otherwise rows [0, nrows) for every panel (solves), where forward scatters of one level may meet: atomic.
+// A list of star blocks: one launch of the block GEMM over all the list's tiles.  Rows per tile: 128 for 4-byte
+// elements when the list has at least two such tiles per compute unit, otherwise 64.
+template <class S, int TM, int TN>
+static void launch_blk(pp_ctx *ctx, bool fwd, typename S::value_type *X, i64 ld, const BlkArgs &a, const void *Hp,
+                       const void *Bp) {
+    typedef typename S::value_type T;
+    const unsigned grid = (unsigned)((a.ntask + 7) / 8 * 8);
+    if (fwd) k_blk<S, TM, 8, true><<<grid, 256, 0, ctx->stream>>>(X, ld, a, (const T *)Hp);
+    else k_blk<S, TM, TN, false><<<grid, 256, 0, ctx->stream>>>(X, ld, a, (const T *)Bp);
+}
+
+template <class S>
+static void launch_blocks(pp_ctx *ctx, const pp_fac *fac, bool fwd, typename S::value_type *X, i64 ld,
+                          const SweepPlan::List &li) {
+    typedef typename S::value_type T;
+    const SweepPlan &Wp = *fac->sym->splan;
+    const DevPlan &d = fac->plan;
+    int q = sizeof(T) == 4 && Wp.tiles[li.pT[1] + li.cnt] >= 2 * ctx->num_cu ? 1 : 0;
+    BlkArgs a;
+    a.ulist = d.plist + li.off;
+    a.pre = d.tiles + li.pT[q];
+    a.nu = (int32_t)li.cnt;
+    a.np = (int32_t)Wp.np;
+    a.ntask = Wp.tiles[li.pT[q] + li.cnt];
+    a.nrows = ld;
+    a.p_c0 = d.p_c0;
+    a.p_w = d.p_w;
+    a.p_e = d.p_e;
+    a.rlo = fwd ? d.p_rowA_lo : d.p_rowB_lo;
+    a.rhi = fwd ? d.p_rowA_hi : d.p_rowB_hi;
+    a.olo = d.p_rowA_lo;
+    a.ohi = d.p_rowA_hi;
+    a.p_eoff = d.p_eoff;
+    a.Eidx = d.Eidx;
+    a.b_boff = d.b_boff;
+    a.b_hoff = d.b_hoff;
+    a.b_ep = d.b_ep;
+    if (a.ntask == 0) return;
+    const bool wide = li.cls == BLK_CLS;
+    if constexpr (sizeof(T) == 4) {
+        if (q == 1) {
+            if (wide) launch_blk<S, 8, 8>(ctx, fwd, X, ld, a, fac->Hpack, fac->Bpack);
+            else launch_blk<S, 8, 4>(ctx, fwd, X, ld, a, fac->Hpack, fac->Bpack);
+            return;
+        }
+    }
+    if (wide) launch_blk<S, 4, 8>(ctx, fwd, X, ld, a, fac->Hpack, fac->Bpack);
+    else launch_blk<S, 4, 4>(ctx, fwd, X, ld, a, fac->Hpack, fac->Bpack);
+}
+
 template <class S>
 static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmode, typename S::value_type *X, i64 ld,
                               bool star_rows, i64 nrows, const void *pack) {
     const SweepPlan &Wp = *fac->sym->splan;
     const DevPlan &d = fac->plan;
     hipStream_t st = ctx->stream;
-    const auto &lists = fwd ? Wp.fwd : Wp.bwd;
+    // the star runs the blocks of the large fronts; the solves run panels only
+    const auto &lists = star_rows ? (fwd ? Wp.sfwd : Wp.sbwd) : (fwd ? Wp.fwd : Wp.bwd);
     if (nrows == 0) return "";
     for (const auto &li : lists) {
+        if (li.cls >= BLK_CLS) {
+            launch_blocks<S>(ctx, fac, fwd, X, ld, li);
+            LAUNCHCHK();
+            continue;
+        }
         SweepArgs a;
         a.plist = d.plist + li.off;
         a.pre = d.tiles;   // base of the prefix arrays; launch_list offsets it
@@ -1274,10 +1696,11 @@ template <class S> struct StarRun {
         HIPCHK(hipMallocAsync((void **)&X, std::max<i64>(1, n * n) * sizeof(T), st));
         timer_start(ctx, 1);
         const DevPlan &d = fac->plan;
-        const i64 np = fac->sym->splan->np;
-        if (np > 0)
-            k_identity_panels<S><<<dim3((unsigned)np, PANEL_W), NT, 0, st>>>(X, n, d.p_c0, d.p_w, d.p_rowA_lo,
-                                                                           d.p_rowA_hi, d.p_rowB_lo, d.p_rowB_hi);
+        const i64 nsu = (i64)fac->sym->splan->sunits.size();
+        if (nsu > 0)
+            k_identity_panels<S><<<dim3((unsigned)nsu, PANEL_W), NT, 0, st>>>(X, n, d.sunits, d.p_c0, d.p_w,
+                                                                            d.p_rowA_lo, d.p_rowA_hi, d.p_rowB_lo,
+                                                                            d.p_rowB_hi);
         LAUNCHCHK();
         std::string e = run_sweeps<S>(ctx, fac, true, 0, X, n, true, n, fac->Upack);
         if (!e.empty()) return e;

@@ -174,29 +174,120 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
         }
         last[f] = P.np - 1;
     }
-    P.Eidx.insert(P.Eidx.end(), EIDX_PAD, 0);
-    // forward levels (leaves to root) and backward levels (root to leaves)
-    std::vector<i64> lvA(P.np, 0), lvB(P.np, 0);
-    std::vector<i64> baseA(nf, 0);   // fronts are in postorder: a front's children come before it
+    P.np = (i64)P.front.size();
+    // star units: a front with at most PANEL_W columns keeps its panels; a wider front is cut into blocks of
+    // BLK_W columns while more than 3/4 BLK_W remain, then one block of the rest if it is wider than PANEL_W (a
+    // 64-column tile class when it fits), and the panels that cover a rest of at most PANEL_W columns
+    std::vector<std::vector<int32_t>> su(nf);
+    P.b_boff.clear();
+    P.b_hoff.clear();
+    P.b_kp.clear();
+    P.b_ep.clear();
+    P.b_bn.clear();
+    P.prep.clear();
+    P.nbpack = 0;
+    P.nhpack = 0;
+    auto up = [](i64 x, i64 m) { return (x + m - 1) / m * m; };
     for (i64 f = 0; f < nf; f++) {
-        for (i64 p = first[f]; p <= last[f]; p++) lvA[p] = baseA[f] + (p - first[f]);
-        if (S.parent[f] >= 0) baseA[S.parent[f]] = std::max(baseA[S.parent[f]], lvA[last[f]] + 1);
+        const i64 Rp = S.Rptr[f], nn = S.Rptr[f + 1] - Rp, nj = nn + (S.Sptr[f + 1] - S.Sptr[f]);
+        i64 done = 0;
+        while (nn > PANEL_W && nn - done > PANEL_W) {
+            const i64 rest = nn - done;
+            const i64 w = rest > BLK_W * 3 / 4 ? std::min<i64>(BLK_W, rest) : rest > BLK_W / 2 ? BLK_W / 2 : rest;
+            const i64 bn = w > BLK_W / 2 ? BLK_W : BLK_W / 2;
+            const i64 c0 = Rp + done, lo = done + w, e = nj - lo;
+            const i64 b = (i64)P.b_boff.size();
+            su[f].push_back((int32_t)P.front.size());
+            P.front.push_back((int32_t)f);
+            P.c0.push_back((int32_t)c0);
+            P.w.push_back((int32_t)w);
+            P.e.push_back((int32_t)e);
+            P.lo_ext.push_back((int32_t)lo);
+            P.chunks.push_back(1);
+            P.eoff.push_back((i64)P.Eidx.size());
+            for (i64 v = c0 + w; v < Rp + nn; v++) P.Eidx.push_back((int32_t)v);
+            for (i64 q = S.Sptr[f]; q < S.Sptr[f + 1]; q++) P.Eidx.push_back((int32_t)S.Stgt[q]);
+            P.poff.push_back(0);
+            P.doff.push_back(0);
+            P.rowA_lo.push_back((int32_t)S.Rptr[S.fdsc[f]]);
+            P.rowA_hi.push_back((int32_t)(c0 + w));
+            P.rowB_lo.push_back((int32_t)S.Rptr[S.fdsc[root[f]]]);
+            P.rowB_hi.push_back((int32_t)S.Rptr[root[f] + 1]);
+            P.max_e = std::max(P.max_e, e);
+            const i64 kp = up(w + e, BLK_K), wp = up(w, BLK_K), ep = up(e, BLK_W);
+            P.b_boff.push_back(P.nbpack);
+            P.b_kp.push_back((int32_t)kp);
+            P.b_bn.push_back((int32_t)bn);
+            P.nbpack += kp * bn;
+            P.b_hoff.push_back(P.nhpack);
+            P.b_ep.push_back((int32_t)ep);
+            P.nhpack += wp * ep;
+            // pack GEMM tiles: M (w x w), G (e x w), H (w x e)
+            const i64 tw = (w + PREP_T - 1) / PREP_T, te = (e + PREP_T - 1) / PREP_T;
+            auto task = [&](int part, i64 tr, i64 tc) {
+                P.prep.push_back((int32_t)b);
+                P.prep.push_back(part);
+                P.prep.push_back((int32_t)tr);
+                P.prep.push_back((int32_t)tc);
+            };
+            for (i64 tr = 0; tr < tw; tr++)
+                for (i64 tc = 0; tc < tw; tc++) task(0, tr, tc);
+            for (i64 tr = 0; tr < te; tr++)
+                for (i64 tc = 0; tc < tw; tc++) task(1, tr, tc);
+            for (i64 tr = 0; tr < tw; tr++)
+                for (i64 tc = 0; tc < te; tc++) task(2, tr, tc);
+            done += w;
+        }
+        // the rest, if any: panels (every block before a rest is 64 or 128 wide, so done is a multiple of PANEL_W)
+        if (done < nn)
+            for (i64 p = first[f] + done / PANEL_W; p <= last[f]; p++) su[f].push_back((int32_t)p);
     }
-    std::vector<i64> endB(nf, -1);   // level of the front's first panel (the last one visited)
-    for (i64 f = nf - 1; f >= 0; f--) {
-        i64 base = S.parent[f] >= 0 ? endB[S.parent[f]] + 1 : 0;
-        for (i64 p = last[f]; p >= first[f]; p--) lvB[p] = base + (last[f] - p);
-        endB[f] = lvB[first[f]];
+    P.nb = (i64)P.front.size() - P.np;
+    P.Eidx.insert(P.Eidx.end(), EIDX_PAD, 0);
+    // forward levels (leaves to root) and backward levels (root to leaves) of a sequence of units per front
+    const i64 nu = (i64)P.front.size();
+    auto levels = [&](const std::vector<std::vector<int32_t>> &units, std::vector<i64> &lvA, std::vector<i64> &lvB) {
+        lvA.assign(nu, -1);
+        lvB.assign(nu, -1);
+        std::vector<i64> baseA(nf, 0);   // fronts are in postorder: a front's children come before it
+        for (i64 f = 0; f < nf; f++) {
+            const auto &U = units[f];
+            for (size_t k = 0; k < U.size(); k++) lvA[U[k]] = baseA[f] + (i64)k;
+            if (S.parent[f] >= 0 && !U.empty()) baseA[S.parent[f]] = std::max(baseA[S.parent[f]], lvA[U.back()] + 1);
+        }
+        std::vector<i64> endB(nf, -1);   // level of the front's first unit (the last one visited)
+        for (i64 f = nf - 1; f >= 0; f--) {
+            const auto &U = units[f];
+            const i64 base = S.parent[f] >= 0 ? endB[S.parent[f]] + 1 : 0;
+            for (size_t k = 0; k < U.size(); k++) lvB[U[k]] = base + (i64)(U.size() - 1 - k);
+            endB[f] = U.empty() ? base - 1 : lvB[U[0]];
+        }
+    };
+    std::vector<i64> lvA, lvB, slvA, slvB;
+    {
+        std::vector<std::vector<int32_t>> pu(nf);
+        for (i64 f = 0; f < nf; f++)
+            for (i64 p = first[f]; p <= last[f]; p++) pu[f].push_back((int32_t)p);
+        levels(pu, lvA, lvB);
     }
-    auto make_lists = [&](const std::vector<i64> &lv, std::vector<SweepPlan::List> &out) {
+    levels(su, slvA, slvB);
+    P.sunits.clear();
+    for (i64 f = 0; f < nf; f++) P.sunits.insert(P.sunits.end(), su[f].begin(), su[f].end());
+    auto rowtiles = [](i64 lo, i64 hi, i64 bm) { return hi > lo ? (hi - lo / bm * bm + bm - 1) / bm : 0; };
+    auto make_lists = [&](const std::vector<i64> &lv, bool fwd, std::vector<SweepPlan::List> &out) {
         i64 L = 0;
-        for (i64 p = 0; p < P.np; p++) L = std::max(L, lv[p] + 1);
-        std::vector<std::vector<int32_t>> buckets(L * NCLASS);
-        for (i64 p = 0; p < P.np; p++) buckets[lv[p] * NCLASS + width_class(P.w[p])].push_back((int32_t)p);
+        for (i64 p = 0; p < nu; p++) L = std::max(L, lv[p] + 1);
+        constexpr int NC = BLK_CLS + 2;
+        std::vector<std::vector<int32_t>> buckets(L * NC);
+        for (i64 p = 0; p < nu; p++)
+            if (lv[p] >= 0) {
+                const int cls = p < P.np ? width_class(P.w[p]) : P.b_bn[p - P.np] == BLK_W ? BLK_CLS : BLK_CLS + 1;
+                buckets[lv[p] * NC + cls].push_back((int32_t)p);
+            }
         for (i64 b = 0; b < (i64)buckets.size(); b++) {
             if (buckets[b].empty()) continue;
             SweepPlan::List li;
-            li.cls = (int)(b % NCLASS);
+            li.cls = (int)(b % NC);
             li.off = (i64)P.plist.size();
             li.cnt = (i64)buckets[b].size();
             P.plist.insert(P.plist.end(), buckets[b].begin(), buckets[b].end());
@@ -214,6 +305,15 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
             li.pAu = prefix([&](int32_t p) { return tiles_of(P.rowA_lo[p], P.rowA_hi[p], TILE_ROWS) * P.chunks[p]; });
             li.pB64 = prefix([&](int32_t p) { return tiles_of(P.rowB_lo[p], P.rowB_hi[p], TILE_ROWS); });
             li.pC = prefix([&](int32_t p) { return (i64)P.chunks[p]; });
+            li.pT[0] = li.pT[1] = 0;
+            if (li.cls >= BLK_CLS)
+                for (int q = 0; q < 2; q++) {
+                    const i64 bm = 64 << q;
+                    li.pT[q] = prefix([&](int32_t p) {
+                        if (fwd) return P.e[p] > 0 ? rowtiles(P.rowA_lo[p], P.rowA_hi[p], bm) * ((P.e[p] + BLK_W - 1) / BLK_W) : 0;
+                        return rowtiles(P.rowB_lo[p], P.rowB_hi[p], bm);
+                    });
+                }
             li.esum = 0;
             for (int32_t p : buckets[b]) li.esum += P.e[p];
             li.uniB = true;
@@ -228,8 +328,12 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
     P.tiles.clear();
     P.fwd.clear();
     P.bwd.clear();
-    make_lists(lvA, P.fwd);
-    make_lists(lvB, P.bwd);
+    P.sfwd.clear();
+    P.sbwd.clear();
+    make_lists(lvA, true, P.fwd);
+    make_lists(lvB, false, P.bwd);
+    make_lists(slvA, true, P.sfwd);
+    make_lists(slvB, false, P.sbwd);
     return "";
 }
 

@@ -39,9 +39,12 @@ def dtype_for(s: int, float_dtype=np.float64):
 def assert_star_equal(s: int, C, D, rtol=1e-12):
     """Bit-exact for the idempotent semirings, relative tolerance for PlusProd."""
     if s == O.PLUSPROD:
+        # relative error in the normal range of the compared type; below its smallest normal number (gradual
+        # underflow, where the relative precision is gone) the error is measured against that number
+        floor = np.finfo(np.result_type(np.asarray(C).dtype, np.asarray(D).dtype)).tiny
         C = np.asarray(C, np.float64)
         D = np.asarray(D, np.float64)
-        scale = np.maximum(np.abs(D), np.finfo(np.float64).tiny)
+        scale = np.maximum(np.abs(D), floor)
         err = np.abs(C - D) / scale
         err[(C == 0) & (D == 0)] = 0
         assert err.max() <= rtol, f"max relative error {err.max()}"

@@ -73,6 +73,30 @@ def test_factor_and_star_match_oracle(name, s, fdtype):
     assert_star_equal(s, C, Co, rtol=rtol_for(s, dtype) * (10 if np.dtype(dtype) == np.float64 else 1))
 
 
+BLOCK_GRAPHS = {
+    # fronts of up to 272 columns (three star blocks), n a multiple of 4: the block GEMMs' 16-byte row loads
+    "grid16x17x15": lambda: W.grid((16, 17, 15)),
+    # odd n: the guarded row loads; a 161-column top front (two blocks, the second 33 wide)
+    "grid15x13x11": lambda: W.grid((15, 13, 11)),
+}
+
+
+@pytest.mark.parametrize("name", list(BLOCK_GRAPHS))
+@pytest.mark.parametrize("s,fdtype", [(O.MINPLUS, np.float32), (O.MAXMIN, np.float32), (O.ORAND, np.float32),
+                                      (O.MINPLUS, np.float64), (O.MAXPLUS, np.float64), (O.PLUSPROD, np.float64),
+                                      (O.PLUSPROD, np.float32)])
+def test_star_blocks_match_oracle(name, s, fdtype):
+    """Stars whose large fronts run as 128-column blocks (register-tiled GEMMs with the packs U_bb* L_bb*,
+    L[E, b] L_bb* and U_bb* U[b, E]) against the oracle's panel recurrence."""
+    dtype = dtype_for(s, fdtype)
+    g = weighted(BLOCK_GRAPHS[name](), s, dtype)
+    print(f"case blocks {name} s={s} dtype={np.dtype(dtype)}", flush=True)
+    sym, F, Fo = both(g, s, dtype)
+    assert max(np.diff(sym.export()["Rptr"])) > 128
+    C = P.Matrix(F)
+    assert_star_equal(s, C, O.star(Fo), rtol=rtol_for(s, dtype))
+
+
 @pytest.mark.parametrize("s", ALL)
 def test_solves_match_oracle(s):
     dtype = dtype_for(s, np.float64)
