@@ -52,7 +52,7 @@ constexpr int NCLASS = 6;      // sweep width classes 1, 2, 4, 8, 16, 32
 constexpr int TILE_ROWS = 64;    // rows per scatter / backward workgroup (one per lane, 4 waves)
 constexpr int SCATTER_T = 128;   // extension columns per scatter workgroup
 constexpr int BLK_W = 128;       // widest star block (the GEMM tile's column count)
-constexpr int BLK_K = 16;        // k step of the block GEMMs (pack rows are padded to a multiple)
+constexpr int BLK_K = 32;        // pack rows are padded to a multiple (of every k step of the block GEMMs)
 constexpr int BLK_CLS = 7;       // list class of star blocks with bn = BLK_W (BLK_CLS + 1: bn = BLK_W / 2)
 constexpr int PREP_T = 64;       // output tile of the block-pack GEMMs
 

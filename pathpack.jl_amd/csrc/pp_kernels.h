@@ -1100,7 +1100,7 @@ struct BlkArgs {
 };
 
 // Block step as a semiring GEMM over a BM x BN tile (BM = 16 TM, BN = 16 TN; 256 threads, 16 x 16, each a TM x TN
-// register block whose rows are groups of four, 64 apart, and likewise its columns; K in steps of BLK_K through two
+// register block whose rows are groups of four, 64 apart, and likewise its columns; K in steps of BK through two
 // LDS buffers with the next step's loads in registers, as k_gemm_tiled).  The backward's BN is the block's tile
 // width bn; the forward's tiles cover BLK_W extension entries.  Row tiles start at multiples of BM; rows outside the
 // sweep's range are computed from in-range memory and not stored.
@@ -1110,11 +1110,12 @@ struct BlkArgs {
 //         before it writes them, and no other workgroup touches them.
 // Workgroups are dealt to the 8 XCDs round-robin; XCD x takes the consecutive tiles [x per, (x + 1) per), so
 // neighbouring tiles (the same rows of a forward block, the same pack of a backward block) share its L2.
-template <class S, int TM, int TN, bool FWD>
+template <class S, int TM, int TN, int BK, bool FWD>
 __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict__ X, i64 ld, BlkArgs a,
                                              const typename S::value_type *__restrict__ Pk) {
     typedef typename S::value_type T;
-    constexpr int BM = 16 * TM, BN = 16 * TN, BK = BLK_K, PAD = 4;
+    static_assert(BLK_K % BK == 0, "pack rows are padded to BLK_K");
+    constexpr int BM = 16 * TM, BN = 16 * TN, PAD = 4;
     typedef typename Vec16<T>::type V;
     constexpr int VW = 16 / (int)sizeof(T);
     constexpr int AQ = BM * BK / (256 * VW), BQ = BN * BK / (256 * VW);   // vectors per thread per k step
@@ -1199,18 +1200,43 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
     };
     auto rowof = [&](int i) { return 64 * (i >> 2) + 4 * tx + (i & 3); };
     auto colof = [&](int j) { return 64 * (j >> 2) + 4 * ty + (j & 3); };
+    // a register block's rows come in groups of four consecutive rows: 16-byte accesses when all four are in range
+    auto rows_in = [&](int g) -> int {   // 2: all four rows of group g in [lo, hi), 1: some, 0: none
+        const i64 r = r0 + 64 * g + 4 * tx;
+        if (r >= lo && r + 4 <= hi) return 2;
+        return (r + 4 <= lo || r >= hi) ? 0 : 1;
+    };
     T acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
-            acc[i][j] = S::zero();
-            if (FWD) {
-                const i64 r = r0 + rowof(i);
+        for (int j = 0; j < TN; j++) acc[i][j] = S::zero();
+    if (FWD) {
+#pragma unroll
+        for (int g = 0; g < TM / 4; g++) {
+            const int st = rows_in(g);
+            if (st == 0) continue;
+            const i64 r = r0 + 64 * g + 4 * tx;
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
                 const int t = ct * BN + colof(j);
-                if (r >= lo && r < hi && t < e) acc[i][j] = X[r + (i64)E[t] * ld];
+                if (t >= e) continue;
+                const T *src = X + r + (i64)E[t] * ld;
+                if (st == 2 && vec) {
+#pragma unroll
+                    for (int h = 0; h < 4; h += VW) {
+                        const V v = *reinterpret_cast<const V *>(src + h);
+#pragma unroll
+                        for (int u = 0; u < VW; u++) acc[4 * g + h + u][j] = v[u];
+                    }
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; u++)
+                        if (r + u >= lo && r + u < hi) acc[4 * g + u][j] = src[u];
+                }
             }
         }
+    }
     if (kbeg < kend) {
         gload(kbeg);
         sstore(0);
@@ -1243,19 +1269,38 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
         buf ^= 1;
     }
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+    for (int g = 0; g < TM / 4; g++) {
+        const int st = rows_in(g);
+        if (st == 0) continue;
+        const i64 r = r0 + 64 * g + 4 * tx;
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-            const i64 r = r0 + rowof(i);
-            if (r < lo || r >= hi) continue;
+            i64 col;
             if (FWD) {
                 const int t = ct * BN + colof(j);
-                if (t < e) X[r + (i64)E[t] * ld] = acc[i][j];
+                if (t >= e) continue;
+                col = E[t];
             } else {
                 const int jj = colof(j);
-                if (jj < w) X[r + (i64)(c0 + jj) * ld] = acc[i][j];
+                if (jj >= w) continue;
+                col = c0 + jj;
+            }
+            T *dst = X + r + col * ld;
+            if (st == 2 && vec) {
+#pragma unroll
+                for (int h = 0; h < 4; h += VW) {
+                    V v;
+#pragma unroll
+                    for (int u = 0; u < VW; u++) v[u] = acc[4 * g + h + u][j];
+                    *reinterpret_cast<V *>(dst + h) = v;
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    if (r + u >= lo && r + u < hi) dst[u] = acc[4 * g + u][j];
             }
         }
+    }
 }
 
 // ===== relabel and permutations =====
@@ -1590,8 +1635,9 @@ static void launch_blk(pp_ctx *ctx, bool fwd, typename S::value_type *X, i64 ld,
                        const void *Bp) {
     typedef typename S::value_type T;
     const unsigned grid = (unsigned)((a.ntask + 7) / 8 * 8);
-    if (fwd) k_blk<S, TM, 8, true><<<grid, 256, 0, ctx->stream>>>(X, ld, a, (const T *)Hp);
-    else k_blk<S, TM, TN, false><<<grid, 256, 0, ctx->stream>>>(X, ld, a, (const T *)Bp);
+    constexpr int BK = TN == 4 ? 32 : 16;   // a 64-column tile takes twice the k per step (latency hiding)
+    if (fwd) k_blk<S, TM, 8, 16, true><<<grid, 256, 0, ctx->stream>>>(X, ld, a, (const T *)Hp);
+    else k_blk<S, TM, TN, BK, false><<<grid, 256, 0, ctx->stream>>>(X, ld, a, (const T *)Bp);
 }
 
 template <class S>

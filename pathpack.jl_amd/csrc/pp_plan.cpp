@@ -25,21 +25,35 @@ std::string build_factor_plan(const Symbolic &S, FactorPlan &P) {
     }
     P.arena = P.Foff[nf];
     P.Sptr32 = S.Sptr;
-    // positions of each separator in its parent's bag
+    // positions of each separator in its parent's bag: the parent's bag positions are scattered into a map over the
+    // vertices, which its children then read (linear in the bags and separators)
     P.relpos.assign(S.Stgt.size(), 0);
-    for (i64 f = 0; f < nf; f++) {
-        i64 p = S.parent[f];
-        if (p < 0) continue;
-        const i64 *b = S.Stgt.data() + S.Sptr[p], *e = S.Stgt.data() + S.Sptr[p + 1];
-        for (i64 q = S.Sptr[f]; q < S.Sptr[f + 1]; q++) {
-            i64 v = S.Stgt[q];
-            if (v >= S.Rptr[p] && v < S.Rptr[p + 1]) {
-                P.relpos[q] = (int32_t)(v - S.Rptr[p]);
-            } else {
-                const i64 *r = std::lower_bound(b, e, v);
-                if (r == e || *r != v) return "separator not contained in the parent's bag";
-                P.relpos[q] = (int32_t)((S.Rptr[p + 1] - S.Rptr[p]) + (r - b));
+    {
+        std::vector<int32_t> kids(nf + 1, 0), kid(nf);
+        for (i64 f = 0; f < nf; f++)
+            if (S.parent[f] >= 0) kids[S.parent[f] + 1]++;
+        for (i64 f = 0; f < nf; f++) kids[f + 1] += kids[f];
+        {
+            std::vector<int32_t> pos(kids.begin(), kids.end() - 1);
+            for (i64 f = 0; f < nf; f++)
+                if (S.parent[f] >= 0) kid[pos[S.parent[f]]++] = (int32_t)f;
+        }
+        std::vector<int32_t> where(S.n, -1);
+        for (i64 p = 0; p < nf; p++) {
+            if (kids[p + 1] == kids[p]) continue;
+            const i64 a = S.Rptr[p + 1] - S.Rptr[p];
+            for (i64 v = S.Rptr[p]; v < S.Rptr[p + 1]; v++) where[v] = (int32_t)(v - S.Rptr[p]);
+            for (i64 q = S.Sptr[p]; q < S.Sptr[p + 1]; q++) where[S.Stgt[q]] = (int32_t)(a + (q - S.Sptr[p]));
+            for (int32_t k = kids[p]; k < kids[p + 1]; k++) {
+                const int32_t f = kid[k];
+                for (i64 q = S.Sptr[f]; q < S.Sptr[f + 1]; q++) {
+                    const int32_t r = where[S.Stgt[q]];
+                    if (r < 0) return "separator not contained in the parent's bag";
+                    P.relpos[q] = r;
+                }
             }
+            for (i64 v = S.Rptr[p]; v < S.Rptr[p + 1]; v++) where[v] = -1;
+            for (i64 q = S.Sptr[p]; q < S.Sptr[p + 1]; q++) where[S.Stgt[q]] = -1;
         }
     }
     // children

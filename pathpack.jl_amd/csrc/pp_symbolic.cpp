@@ -13,9 +13,97 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <numeric>
+#include <unistd.h>
 
 namespace pp {
+
+namespace {
+int max_threads();
+}
+
+// A pool of worker threads kept for the life of the process (created at the first parallel call, again in a
+// forked child): starting and joining 15 threads costs about a millisecond, several times per analysis.
+namespace {
+class ThreadPool {
+  public:
+    explicit ThreadPool(int n) {
+        for (int i = 1; i < n; i++) th_.emplace_back([this, i] { loop(i); });
+    }
+    ~ThreadPool() {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (auto &t : th_) t.join();
+    }
+    int size() const { return (int)th_.size() + 1; }
+    void run(int n, const std::function<void(int)> &fn) {
+        std::lock_guard<std::mutex> one(run_mu_);   // one job at a time
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            job_ = &fn;
+            active_ = n;
+            pending_ = n - 1;
+            gen_++;
+        }
+        cv_.notify_all();
+        fn(0);
+        std::unique_lock<std::mutex> lk(mu_);
+        done_.wait(lk, [&] { return pending_ == 0; });
+        job_ = nullptr;
+    }
+
+  private:
+    void loop(int i) {
+        unsigned long seen = 0;
+        while (true) {
+            const std::function<void(int)> *job;
+            {
+                std::unique_lock<std::mutex> lk(mu_);
+                cv_.wait(lk, [&] { return stop_ || gen_ != seen; });
+                if (stop_) return;
+                seen = gen_;
+                if (i >= active_) continue;
+                job = job_;
+            }
+            (*job)(i);
+            std::lock_guard<std::mutex> lk(mu_);
+            if (--pending_ == 0) done_.notify_one();
+        }
+    }
+    std::vector<std::thread> th_;
+    std::mutex mu_, run_mu_;
+    std::condition_variable cv_, done_;
+    const std::function<void(int)> *job_ = nullptr;
+    int active_ = 0, pending_ = 0;
+    unsigned long gen_ = 0;
+    bool stop_ = false;
+};
+}  // namespace
+
+void pool_run(int n, const std::function<void(int)> &fn) {
+    static std::mutex mu;
+    static ThreadPool *pool = nullptr;
+    static pid_t owner = 0;
+    if (n <= 1) {
+        fn(0);
+        return;
+    }
+    ThreadPool *p;
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        if (!pool || owner != getpid()) {   // a forked child does not have its parent's threads
+            pool = new ThreadPool(std::max(2, max_threads()));   // kept to the end of the process
+            owner = getpid();
+        }
+        p = pool;
+    }
+    if (n > p->size()) n = p->size();
+    p->run(n, fn);
+}
 
 namespace {
 
@@ -26,23 +114,22 @@ struct Adj {
 };
 
 // Threads for the host analysis: up to 16 (PP_SYMBOLIC_THREADS overrides), one for small graphs.
-int analysis_threads(i64 n) {
+int max_threads() {
     int threads = (int)std::min<unsigned>(16, std::max(1u, std::thread::hardware_concurrency()));
     if (const char *e = std::getenv("PP_SYMBOLIC_THREADS")) threads = std::max(1, std::atoi(e));
-    return n < 20000 ? 1 : threads;
+    return threads;
 }
+int analysis_threads(i64 n) { return n < 20000 ? 1 : max_threads(); }
 
-// fn(lo, hi) over [0, count) in contiguous blocks on `threads` threads (the caller's thread takes the first block)
+// fn(lo, hi) over [0, count) in contiguous blocks on `threads` threads of the pool (the caller's thread takes the
+// first block)
 template <class Fn> void parallel_for(i64 count, int threads, Fn fn) {
     threads = (int)std::max<i64>(1, std::min<i64>(threads, count / 1024));
     if (threads <= 1) {
         fn((i64)0, count);
         return;
     }
-    std::vector<std::thread> pool;
-    for (int t = 1; t < threads; t++) pool.emplace_back([&, t] { fn(count * t / threads, count * (t + 1) / threads); });
-    fn((i64)0, count / threads);
-    for (auto &th : pool) th.join();
+    pool_run(threads, [&](int t) { fn(count * t / threads, count * (t + 1) / threads); });
 }
 
 // Symmetric pattern of A without the diagonal, neighbours sorted.
@@ -56,36 +143,36 @@ std::string symmetrize(i64 n, const i64 *colptr, const i64 *rowval, Adj &G) {
             if (p > colptr[j] && rowval[p] <= rowval[p - 1]) return "row indices must be sorted and unique in each column";
         }
     }
-    std::vector<i64> deg(n + 1, 0);
-    for (i64 j = 0; j < n; j++)
-        for (i64 p = colptr[j]; p < colptr[j + 1]; p++) {
-            i64 i = rowval[p];
-            if (i == j) continue;
-            deg[i]++;
-            deg[j]++;
-        }
+    // A^T by a counting sort over the columns of A: the entries of each of its columns come out in increasing order
+    const i64 nnz = colptr[n];
+    std::vector<i64> tptr(n + 1, 0);
+    std::vector<i32> tidx(nnz);
+    for (i64 p = 0; p < nnz; p++) tptr[rowval[p] + 1]++;
+    for (i64 v = 0; v < n; v++) tptr[v + 1] += tptr[v];
+    {
+        std::vector<i64> pos(tptr.begin(), tptr.end() - 1);
+        for (i64 j = 0; j < n; j++)
+            for (i64 p = colptr[j]; p < colptr[j + 1]; p++) tidx[pos[rowval[p]]++] = (i32)j;
+    }
+    // adj(v): the sorted union of column v of A and of A^T, without v
     G.n = n;
-    G.xadj.assign(n + 1, 0);
-    for (i64 v = 0; v < n; v++) G.xadj[v + 1] = G.xadj[v] + deg[v];
-    G.adj.assign(G.xadj[n], 0);
-    std::vector<i64> pos(G.xadj.begin(), G.xadj.end() - 1);
-    for (i64 j = 0; j < n; j++)
-        for (i64 p = colptr[j]; p < colptr[j + 1]; p++) {
-            i64 i = rowval[p];
-            if (i == j) continue;
-            G.adj[pos[i]++] = (i32)j;
-            G.adj[pos[j]++] = (i32)i;
-        }
-    // sort and deduplicate each list
     std::vector<i64> nx(n + 1, 0);
+    G.adj.resize(2 * nnz);
     i64 w = 0;
     for (i64 v = 0; v < n; v++) {
-        i32 *b = G.adj.data() + G.xadj[v], *e = G.adj.data() + G.xadj[v + 1];
-        std::sort(b, e);
-        i64 start = w;
-        for (i32 *q = b; q < e; q++)
-            if (q == b || *q != q[-1]) G.adj[w++] = *q;
-        nx[v] = start;
+        nx[v] = w;
+        i64 a = colptr[v], ae = colptr[v + 1], b = tptr[v], be = tptr[v + 1];
+        while (a < ae || b < be) {
+            i64 x;
+            if (b >= be || (a < ae && rowval[a] <= (i64)tidx[b])) {
+                x = rowval[a];
+                if (b < be && (i64)tidx[b] == x) b++;
+                a++;
+            } else {
+                x = tidx[b++];
+            }
+            if (x != v) G.adj[w++] = (i32)x;
+        }
     }
     nx[n] = w;
     G.xadj = nx;
@@ -354,10 +441,7 @@ struct ND {
                 cv.notify_all();
             }
         };
-        std::vector<std::thread> pool;
-        for (int t = 1; t < nthreads; t++) pool.emplace_back(work);
-        work();
-        for (auto &th : pool) th.join();
+        pool_run(nthreads, [&](int) { work(); });
     }
 };
 
@@ -610,10 +694,7 @@ std::string supernodal_tree(const Adj &G, const std::vector<i64> &perm, const st
         }
     };
     {
-        std::vector<std::thread> pool;
-        for (int t = 1; t < threads; t++) pool.emplace_back(worker, t);
-        worker(0);
-        for (auto &th : pool) th.join();
+        pool_run(threads, worker);
     }
     {
         std::vector<i32> mark(n, -1), buf;
@@ -703,38 +784,60 @@ std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, st
         out.Lptr[f + 1] = out.Lptr[f] + nn * na;
     }
     // where each stored entry (i, j) lands (new labels): the front f of min(i, j), at the local positions of i and j
-    // in bag(f) = res(f) then sep(f) (a separator position by binary search in the sorted sep(f)); in parallel over
-    // the columns of A
+    // in bag(f) = res(f) then sep(f).  Entries are grouped by front (counting sort), and each front's bag positions
+    // are scattered into a per-thread map over the vertices that its entries then read; in parallel over fronts.
+    stage("  structure copies", ts);
     out.nnz = colptr[n];
-    out.entry_front.resize(out.nnz);
-    out.entry_row.resize(out.nnz);
-    out.entry_col.resize(out.nnz);
+    const i64 nnz = out.nnz;
+    out.entry_front.resize(nnz);
+    out.entry_row.resize(nnz);
+    out.entry_col.resize(nnz);
     std::vector<i32> fof(n);
     for (i64 f = 0; f < nf; f++)
         for (i64 v = out.Rptr[f]; v < out.Rptr[f + 1]; v++) fof[v] = (i32)f;
+    std::vector<i64> eptr(nf + 1, 0);
+    std::vector<i32> eidx(nnz);
+    for (i64 c = 0; c < n; c++) {
+        const i64 j = out.invp[c];
+        for (i64 p = colptr[c]; p < colptr[c + 1]; p++) {
+            const i64 f = fof[std::min<i64>(out.invp[rowval[p]], j)];
+            out.entry_front[p] = f;
+            eptr[f + 1]++;
+        }
+    }
+    for (i64 f = 0; f < nf; f++) eptr[f + 1] += eptr[f];
+    {
+        std::vector<i64> pos(eptr.begin(), eptr.end() - 1);
+        for (i64 p = 0; p < nnz; p++) eidx[pos[out.entry_front[p]]++] = (i32)p;
+    }
+    std::vector<i64> colof(nnz);   // column of A of each entry
+    for (i64 c = 0; c < n; c++)
+        for (i64 p = colptr[c]; p < colptr[c + 1]; p++) colof[p] = c;
+    stage("  entry lists", ts);
     std::atomic<bool> outside(false);
-    parallel_for(n, analysis_threads(n), [&](i64 c0, i64 c1) {
-        for (i64 c = c0; c < c1; c++) {
-            const i64 j = out.invp[c];
-            for (i64 p = colptr[c]; p < colptr[c + 1]; p++) {
-                const i64 i = out.invp[rowval[p]];
-                const i64 lo = std::min(i, j), hi = std::max(i, j);
-                const i64 f = fof[lo], r0 = out.Rptr[f], r1 = out.Rptr[f + 1];
-                i64 lhi;
-                if (hi < r1) {
-                    lhi = hi - r0;
-                } else {
-                    const i64 *s0 = out.Stgt.data() + out.Sptr[f], *s1 = out.Stgt.data() + out.Sptr[f + 1];
-                    const i64 *q = std::lower_bound(s0, s1, hi);
-                    if (q == s1 || *q != hi) {
+    const int nth = analysis_threads(n);
+    std::atomic<i64> nextf(0);
+    pool_run(nth, [&](int) {
+        std::vector<i32> where(n, -1);
+        while (true) {
+            const i64 f0 = nextf.fetch_add(64);
+            if (f0 >= nf) break;
+            for (i64 f = f0; f < std::min<i64>(nf, f0 + 64); f++) {
+                const i64 r0 = out.Rptr[f], r1 = out.Rptr[f + 1];
+                for (i64 q = out.Sptr[f]; q < out.Sptr[f + 1]; q++) where[out.Stgt[q]] = (i32)((r1 - r0) + (q - out.Sptr[f]));
+                for (i64 k = eptr[f]; k < eptr[f + 1]; k++) {
+                    const i64 p = eidx[k];
+                    const i64 i = out.invp[rowval[p]], j = out.invp[colof[p]];
+                    const i64 hi = std::max(i, j);
+                    const i64 lhi = hi < r1 ? hi - r0 : where[hi];
+                    if (lhi < 0) {
                         outside = true;
                         continue;
                     }
-                    lhi = (r1 - r0) + (q - s0);
+                    out.entry_row[p] = (i32)(i < j ? i - r0 : lhi);
+                    out.entry_col[p] = (i32)(j <= i ? j - r0 : lhi);
                 }
-                out.entry_front[p] = f;
-                out.entry_row[p] = (i32)(i == lo ? lo - r0 : lhi);
-                out.entry_col[p] = (i32)(j == lo ? lo - r0 : lhi);
+                for (i64 q = out.Sptr[f]; q < out.Sptr[f + 1]; q++) where[out.Stgt[q]] = -1;
             }
         }
     });
@@ -860,12 +963,28 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
         }
         return s;
     };
-    std::vector<std::vector<i64>> kids(ns);
-    for (i64 s = 0; s < ns; s++)
-        if (par1[s] >= 0) kids[par1[s]].push_back(s);
+    // children of every supernode and, after the merges, members and children of every merged front: lists in
+    // increasing order, stored as (pointer, index) arrays
+    auto csr = [&](i64 m, auto key, std::vector<i64> &ptr, std::vector<i64> &idx) {   // idx lists s with key(s) = k
+        ptr.assign(ns + 1, 0);
+        for (i64 s = 0; s < m; s++) {
+            const i64 k = key(s);
+            if (k >= 0) ptr[k + 1]++;
+        }
+        for (i64 k = 0; k < ns; k++) ptr[k + 1] += ptr[k];
+        idx.assign(ptr[ns], 0);
+        std::vector<i64> pos(ptr.begin(), ptr.end() - 1);
+        for (i64 s = 0; s < m; s++) {
+            const i64 k = key(s);
+            if (k >= 0) idx[pos[k]++] = s;
+        }
+    };
+    std::vector<i64> kptr, kidx;
+    csr(ns, [&](i64 s) { return par1[s]; }, kptr, kidx);
+    std::vector<i64> cs;
     for (i64 p = 0; p < ns; p++) {
         // children with few columns first: they gain the most
-        std::vector<i64> cs = kids[p];
+        cs.assign(kidx.begin() + kptr[p], kidx.begin() + kptr[p + 1]);
         std::stable_sort(cs.begin(), cs.end(), [&](i64 a, i64 b) { return mnn[find(a)] < mnn[find(b)]; });
         for (i64 c : cs) {
             i64 rc = find(c), rp = find(p);
@@ -888,34 +1007,27 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
     //    (post)order, so the new order is still a topological order of the elimination tree
     std::vector<i64> root(ns);
     for (i64 s = 0; s < ns; s++) root[s] = find(s);
-    std::vector<std::vector<i64>> members(ns), mkids(ns);
-    for (i64 s = 0; s < ns; s++) members[root[s]].push_back(s);
-    std::vector<char> is_root(ns, 0);
-    for (i64 s = 0; s < ns; s++)
-        if (root[s] == s) {
-            is_root[s] = 1;
-            // parent of a merged front: the merged front of its top member's parent
-            i64 top = members[s].back();
-            if (par1[top] >= 0) mkids[root[par1[top]]].push_back(s);
-        }
+    std::vector<i64> mptr, midx, cptr, cidx;
+    csr(ns, [&](i64 s) { return root[s]; }, mptr, midx);
+    auto top_of = [&](i64 s) { return midx[mptr[s + 1] - 1]; };   // the last member of merged front s
+    // parent of a merged front: the merged front of its top member's parent
+    csr(ns, [&](i64 s) { return root[s] == s && par1[top_of(s)] >= 0 ? root[par1[top_of(s)]] : (i64)-1; }, cptr, cidx);
     std::vector<i64> perm2, R2, fid(ns, -1);
     perm2.reserve(n);
     R2.push_back(0);
-    std::vector<std::pair<i64, size_t>> stack;
+    std::vector<std::pair<i64, i64>> stack;
     for (i64 s = 0; s < ns; s++) {
-        if (!is_root[s]) continue;
-        i64 top = members[s].back();
-        if (par1[top] >= 0) continue;
-        stack.push_back({s, 0});
+        if (root[s] != s || par1[top_of(s)] >= 0) continue;
+        stack.push_back({s, cptr[s]});
         while (!stack.empty()) {
             auto &tp = stack.back();
-            i64 m = tp.first;
-            if (tp.second < mkids[m].size()) {
-                i64 c = mkids[m][tp.second++];
-                stack.push_back({c, 0});
+            const i64 m = tp.first;
+            if (tp.second < cptr[m + 1]) {
+                const i64 c = cidx[tp.second++];
+                stack.push_back({c, cptr[c]});
             } else {
-                for (i64 mem : members[m])
-                    for (i64 v = R1[mem]; v < R1[mem + 1]; v++) perm2.push_back(perm1[v]);
+                for (i64 q = mptr[m]; q < mptr[m + 1]; q++)
+                    for (i64 v = R1[midx[q]]; v < R1[midx[q] + 1]; v++) perm2.push_back(perm1[v]);
                 fid[m] = (i64)R2.size() - 1;
                 R2.push_back((i64)perm2.size());
                 stack.pop_back();
@@ -926,8 +1038,8 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
     // the merged tree in the final numbering: a merged front's parent holds its top member's parent
     std::vector<i64> tree2((i64)R2.size() - 1, -1);
     for (i64 s = 0; s < ns; s++)
-        if (is_root[s]) {
-            const i64 top = members[s].back();
+        if (root[s] == s) {
+            const i64 top = top_of(s);
             if (par1[top] >= 0) tree2[fid[s]] = fid[root[par1[top]]];
         }
     stage("amalgamation", ts);

@@ -15,6 +15,7 @@
 // inputs).
 #pragma once
 #include <cstdint>
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -55,6 +56,9 @@ struct Symbolic {
 // otherwise an error message.  `given_perm` is used when opts.ordering == 2.
 std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOptions &opts, const i64 *given_perm,
                     Symbolic &out);
+
+// fn(0), ..., fn(n - 1) concurrently on the library's worker threads (fn(0) on the caller's); one job at a time.
+void pool_run(int n, const std::function<void(int)> &fn);
 
 // The symbolic structure for a given permutation and partition into fronts (Rptr, fronts in postorder).
 std::string analyze_given(i64 n, const i64 *colptr, const i64 *rowval, const i64 *perm, i64 nf, const i64 *Rptr,
