@@ -370,6 +370,11 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     u2.add(W.b_bn, &d.b_bn);
     u2.add(W.prep, &d.prep);
     u2.add(W.sunits, &d.sunits);
+    u2.add(W.sub_ptr, &d.sub_ptr);
+    u2.add(W.sub_pan, &d.sub_pan);
+    u2.add(W.sub_rows, &d.sub_rows);
+    u2.add(W.sub_preF, &d.sub_preF);
+    u2.add(W.sub_preB, &d.sub_preB);
     u2.add(S.perm, &d.perm);
     u2.add(S.invp, &d.invp);
     u2.add(invp32, &d.invp32);

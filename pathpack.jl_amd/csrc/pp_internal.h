@@ -26,6 +26,11 @@
 //   Bpack[b]  (kp x bn, k-major, kp = w + e rounded up to BLK_K): rows 0..w-1 hold M_b = U_bb* (x) L_bb*, rows
 //             w + t hold G_b[t, :] = L[E_t, blk] (x) L_bb*;
 //   Hpack[b]  (wp x ep, k-major, wp = w rounded up to BLK_K, ep = e rounded up to BLK_W): H_b = U_bb* (x) U[blk, E].
+//
+// Star subtrees.  A maximal subtree of fronts with at most PANEL_W columns (one panel each) whose columns plus its
+// root's separator number at most SUB_L runs in one launch per sweep: a wave takes a 64-row tile and steps through
+// the subtree's panels in postorder (forward) or reverse postorder (backward), so what a panel reads was written just
+// before by the same lane (no synchronization) and is still in the cache.
 // Forward step:  X[R, E] <- X[R, E] (+) X[R, blk] (x) H_b over the rows R of the block's subtree (X[R, blk] as
 // accumulated, unsolved).  Backward step: X[:, blk] <- X[:, blk] (x) M_b (+) X[:, E] (x) G_b over the component's
 // rows, X[:, blk] taken as zero outside R.  In exact arithmetic this is the panel recurrence (U_bb* solves the
@@ -55,6 +60,7 @@ constexpr int BLK_W = 128;       // widest star block (the GEMM tile's column co
 constexpr int BLK_K = 32;        // pack rows are padded to a multiple (of every k step of the block GEMMs)
 constexpr int BLK_CLS = 7;       // list class of star blocks with bn = BLK_W (BLK_CLS + 1: bn = BLK_W / 2)
 constexpr int PREP_T = 64;       // output tile of the block-pack GEMMs
+constexpr int SUB_L = 512;       // largest star subtree: columns plus the root's separator
 
 inline int width_class(int w) {
     int c = 0;
@@ -104,6 +110,9 @@ struct SweepPlan {
     i64 nbpack = 0, nhpack = 0;
     std::vector<int32_t> prep;           // block-pack GEMM tiles: (block, part, tile row, tile column)
     std::vector<int32_t> sunits;         // the star's units: panels of fronts with at most PANEL_W columns, blocks
+    // star subtrees: panels of subtree s at sub_pan[sub_ptr[s] .. sub_ptr[s + 1]) in postorder; rows (forward lo, hi,
+    // backward lo, hi) and per-subtree prefixes of 64-row tiles (forward, backward); their panels are in no list
+    std::vector<int32_t> sub_ptr, sub_pan, sub_rows, sub_preF, sub_preB;
     struct List {
         int cls;                     // width class (BLK_CLS, BLK_CLS + 1: star blocks)
         i64 off, cnt;                // panel ids in plist
@@ -139,6 +148,7 @@ struct DevPlan {
     int32_t *Eidx = nullptr, *plist = nullptr, *tiles = nullptr;
     i64 *b_boff = nullptr, *b_hoff = nullptr;
     int32_t *b_kp = nullptr, *b_ep = nullptr, *b_bn = nullptr, *prep = nullptr, *sunits = nullptr;
+    int32_t *sub_ptr = nullptr, *sub_pan = nullptr, *sub_rows = nullptr, *sub_preF = nullptr, *sub_preB = nullptr;
     // permutation
     i64 *perm = nullptr, *invp = nullptr;
     int32_t *invp32 = nullptr;

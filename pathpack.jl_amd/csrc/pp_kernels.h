@@ -910,6 +910,207 @@ __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(siz
     }
 }
 
+// ===== star subtrees: a wave steps through a small subtree's panels for its 64 rows =====
+
+struct SubArgs {
+    const int32_t *ptr, *pan, *rows, *pre;   // subtree panel lists, rows, prefix of 64-row tiles
+    int32_t nsub;
+    const int32_t *p_c0, *p_w, *p_e, *rowA_lo, *rowA_hi;
+    const i64 *p_eoff, *p_poff, *p_doff;
+    const int32_t *Eidx;
+};
+
+// Forward step of panel p (width class W) on row r (the lane stores only when `store`): x <- x D* over the panel's
+// columns, then X[r, E_t] <- X[r, E_t] (+) sum_j x_j (x) P(j, t) for every t, four targets at a time with the next
+// four loads in flight (the targets are distinct columns, so no load meets a pending store).
+template <class S, int W>
+__device__ inline void sub_fwd_panel(typename S::value_type *__restrict__ X, i64 ld, const SubArgs &a, int p, i64 r,
+                                     bool store, const typename S::value_type *__restrict__ Dpack,
+                                     const typename S::value_type *__restrict__ Pk) {
+    typedef typename S::value_type T;
+    const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
+    const T *D = Dpack + a.p_doff[p];
+    const T *Pp = Pk + a.p_poff[p];
+    const int32_t *E = a.Eidx + a.p_eoff[p];
+    T *xr = X + r;
+    T x[W];
+#pragma unroll
+    for (int j = 0; j < W; j++) {
+        const T v = xr[(i64)(c0 + min(j, w - 1)) * ld];
+        x[j] = j < w ? v : S::zero();
+    }
+#pragma unroll
+    for (int j = 0; j < W; j++) {
+        T acc = x[j];
+#pragma unroll
+        for (int i = 0; i < j; i++) acc = S::muladd(x[i], D[i + j * W], acc);
+        if (!S::integral) acc = S::prod(acc, S::star(D[j + j * W]));
+        x[j] = acc;
+    }
+    if (e == 0) return;
+    T A[4], B[4];
+    auto ld4 = [&](int t0, T(&v)[4]) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = xr[(i64)E[min(t0 + u, e - 1)] * ld];
+    };
+    auto upd4 = [&](int t0, const T(&v)[4]) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int t = t0 + u;
+            if (t < e) {
+                const T *pc = Pp + (i64)t * W;
+                T acc = v[u];
+                if (W == 1) {
+                    acc = S::muladd(x[0], pc[0], acc);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < W; j += 2) acc = S::muladd2(x[j], pc[j], x[j + 1], pc[j + 1], acc);
+                }
+                if (store) xr[(i64)E[t] * ld] = acc;
+            }
+        }
+    };
+    ld4(0, A);
+    for (int t0 = 0; t0 < e; t0 += 8) {   // A holds targets t0.., B then t0 + 4..
+        if (t0 + 4 < e) ld4(t0 + 4, B);
+        upd4(t0, A);
+        if (t0 + 4 >= e) break;
+        if (t0 + 8 < e) ld4(t0 + 8, A);
+        upd4(t0 + 4, B);
+    }
+}
+
+// Backward step of panel p on row r: x <- (the panel's unsolved forward values, solved, on its own rows [alo, ahi);
+// zero elsewhere) (+) sum_t X[r, E_t] (x) Q(t, :), then the unit lower triangle of D; stored when `store`.
+template <class S, int W>
+__device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64 ld, const SubArgs &a, int p, i64 r,
+                                     bool store, const typename S::value_type *__restrict__ Dpack,
+                                     const typename S::value_type *__restrict__ Qk) {
+    typedef typename S::value_type T;
+    const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
+    const T *D = Dpack + a.p_doff[p];
+    const T *Qp = Qk + a.p_poff[p];
+    const int32_t *E = a.Eidx + a.p_eoff[p];
+    const T *xr = X + r;
+    T acc[W];
+#pragma unroll
+    for (int j = 0; j < W; j++) acc[j] = S::zero();
+    if (r >= a.rowA_lo[p] && r < a.rowA_hi[p]) {
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            const T v = xr[(i64)(c0 + min(j, w - 1)) * ld];
+            acc[j] = j < w ? v : S::zero();
+        }
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            T s = acc[j];
+#pragma unroll
+            for (int i = 0; i < j; i++) s = S::muladd(acc[i], D[i + j * W], s);
+            if (!S::integral) s = S::prod(s, S::star(D[j + j * W]));
+            acc[j] = s;
+        }
+    }
+    // gathers in groups of four, three register sets in rotation (eight loads in flight)
+    auto ld4 = [&](int t0, T(&v)[4]) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = xr[(i64)E[min(t0 + u, e - 1)] * ld];
+    };
+    auto mad4 = [&](int t0, const T(&v)[4]) {
+        const T *qq = Qp + (i64)t0 * W;
+        if (t0 + 4 <= e) {
+#pragma unroll
+            for (int j = 0; j < W; j++) {
+                acc[j] = S::muladd2(v[0], qq[j], v[1], qq[W + j], acc[j]);
+                acc[j] = S::muladd2(v[2], qq[2 * W + j], v[3], qq[3 * W + j], acc[j]);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (t0 + u < e) {
+#pragma unroll
+                    for (int j = 0; j < W; j++) acc[j] = S::muladd(v[u], qq[u * W + j], acc[j]);
+                }
+        }
+    };
+    if (e > 0) {
+        T A[4], B[4], C[4];
+        ld4(0, A);
+        if (4 < e) ld4(4, B);
+        int t0 = 0;
+        for (; t0 + 12 <= e; t0 += 12) {
+            if (t0 + 8 < e) ld4(t0 + 8, C);
+            mad4(t0, A);
+            if (t0 + 12 < e) ld4(t0 + 12, A);
+            mad4(t0 + 4, B);
+            if (t0 + 16 < e) ld4(t0 + 16, B);
+            mad4(t0 + 8, C);
+        }
+        if (t0 < e) {
+            if (t0 + 8 < e) ld4(t0 + 8, C);
+            mad4(t0, A);
+            if (t0 + 4 < e) mad4(t0 + 4, B);
+            if (t0 + 8 < e) mad4(t0 + 8, C);
+        }
+    }
+#pragma unroll
+    for (int j = W - 1; j >= 0; j--) {
+        T s = acc[j];
+#pragma unroll
+        for (int i = j + 1; i < W; i++) s = S::muladd(acc[i], D[i + j * W], s);
+        acc[j] = s;
+    }
+    if (store) {
+#pragma unroll
+        for (int j = 0; j < W; j++)
+            if (j < w) X[(i64)(c0 + j) * ld + r] = acc[j];
+    }
+}
+
+// One wave per (subtree, 64-row tile): forward over the subtree's rows in postorder, or backward over the
+// component's rows in reverse postorder.  Every value a panel reads on row r was last written by this lane.
+template <class S, bool FWD>
+__global__ __launch_bounds__(64) void k_sub(typename S::value_type *__restrict__ X, i64 ld, SubArgs a,
+                                            const typename S::value_type *__restrict__ Dpack,
+                                            const typename S::value_type *__restrict__ Pk) {
+    const int task = blockIdx.x;
+    const int s = search(a.pre, a.nsub, task);
+    const int tile = task - a.pre[s];
+    const int lo = a.rows[4 * s + (FWD ? 0 : 2)], hi = a.rows[4 * s + (FWD ? 1 : 3)];
+    const i64 r = (i64)lo + (i64)tile * TILE_ROWS + threadIdx.x;
+    const int k0 = a.ptr[s], k1 = a.ptr[s + 1];
+    for (int kk = 0; kk < k1 - k0; kk++) {
+        const int p = __builtin_amdgcn_readfirstlane(a.pan[FWD ? k0 + kk : k1 - 1 - kk]);
+        const int w = a.p_w[p];
+        // rows of this step: the panel's own rows [alo, ahi) forward, all the tile's rows backward; lanes outside
+        // compute on a row inside and store nothing
+        const int plo = FWD ? a.rowA_lo[p] : lo, phi = FWD ? a.rowA_hi[p] : hi;
+        const i64 t0 = (i64)lo + (i64)tile * TILE_ROWS;
+        if (t0 >= phi || t0 + TILE_ROWS <= plo) continue;
+        const bool store = r >= plo && r < phi;
+        const i64 rr = r < plo ? plo : (r >= phi ? phi - 1 : r);
+        const int cls = w <= 1 ? 0 : 32 - __builtin_clz(w - 1);
+        if (FWD) {
+            switch (cls) {
+            case 0: sub_fwd_panel<S, 1>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            case 1: sub_fwd_panel<S, 2>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            case 2: sub_fwd_panel<S, 4>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            case 3: sub_fwd_panel<S, 8>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            case 4: sub_fwd_panel<S, 16>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            default: sub_fwd_panel<S, 32>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            }
+        } else {
+            switch (cls) {
+            case 0: sub_bwd_panel<S, 1>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            case 1: sub_bwd_panel<S, 2>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            case 2: sub_bwd_panel<S, 4>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            case 3: sub_bwd_panel<S, 8>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            case 4: sub_bwd_panel<S, 16>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            default: sub_bwd_panel<S, 32>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            }
+        }
+    }
+}
+
 // ===== star blocks: fronts with more than PANEL_W columns, in blocks of at most BLK_W columns =====
 //
 // Per block b (columns c_0 .. c_{w-1} of front f, local start cb; extension E_b as for a panel):
@@ -1641,7 +1842,7 @@ static void launch_blk(pp_ctx *ctx, bool fwd, typename S::value_type *X, i64 ld,
 }
 
 template <class S>
-static void launch_blocks(pp_ctx *ctx, const pp_fac *fac, bool fwd, typename S::value_type *X, i64 ld,
+static void launch_blocks(pp_ctx *ctx, const pp_fac *fac, bool fwd, typename S::value_type *X, i64 ld, i64 nrows,
                           const SweepPlan::List &li) {
     typedef typename S::value_type T;
     const SweepPlan &Wp = *fac->sym->splan;
@@ -1653,7 +1854,7 @@ static void launch_blocks(pp_ctx *ctx, const pp_fac *fac, bool fwd, typename S::
     a.nu = (int32_t)li.cnt;
     a.np = (int32_t)Wp.np;
     a.ntask = Wp.tiles[li.pT[q] + li.cnt];
-    a.nrows = ld;
+    a.nrows = nrows;
     a.p_c0 = d.p_c0;
     a.p_w = d.p_w;
     a.p_e = d.p_e;
@@ -1685,12 +1886,40 @@ static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmod
     const SweepPlan &Wp = *fac->sym->splan;
     const DevPlan &d = fac->plan;
     hipStream_t st = ctx->stream;
-    // the star runs the blocks of the large fronts; the solves run panels only
+    // the star runs the blocks of the large fronts and the small subtrees (first forward, last backward); the solves
+    // run panels only
     const auto &lists = star_rows ? (fwd ? Wp.sfwd : Wp.sbwd) : (fwd ? Wp.fwd : Wp.bwd);
     if (nrows == 0) return "";
+    auto subtrees = [&]() {
+        typedef typename S::value_type T;
+        const i64 nsub = (i64)Wp.sub_ptr.size() - 1;
+        const int32_t ntask = fwd ? Wp.sub_preF.back() : Wp.sub_preB.back();
+        if (nsub <= 0 || ntask == 0) return;
+        SubArgs b;
+        b.ptr = d.sub_ptr;
+        b.pan = d.sub_pan;
+        b.rows = d.sub_rows;
+        b.pre = fwd ? d.sub_preF : d.sub_preB;
+        b.nsub = (int32_t)nsub;
+        b.p_c0 = d.p_c0;
+        b.p_w = d.p_w;
+        b.p_e = d.p_e;
+        b.rowA_lo = d.p_rowA_lo;
+        b.rowA_hi = d.p_rowA_hi;
+        b.p_eoff = d.p_eoff;
+        b.p_poff = d.p_poff;
+        b.p_doff = d.p_doff;
+        b.Eidx = d.Eidx;
+        if (fwd) k_sub<S, true><<<(unsigned)ntask, 64, 0, st>>>(X, ld, b, (const T *)fac->Dpack, (const T *)pack);
+        else k_sub<S, false><<<(unsigned)ntask, 64, 0, st>>>(X, ld, b, (const T *)fac->Dpack, (const T *)pack);
+    };
+    if (star_rows && fwd) {
+        subtrees();
+        LAUNCHCHK();
+    }
     for (const auto &li : lists) {
         if (li.cls >= BLK_CLS) {
-            launch_blocks<S>(ctx, fac, fwd, X, ld, li);
+            launch_blocks<S>(ctx, fac, fwd, X, ld, nrows, li);
             LAUNCHCHK();
             continue;
         }
@@ -1722,6 +1951,10 @@ static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmod
         case 4: launch_list<S, 16>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
         default: launch_list<S, 32>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
         }
+        LAUNCHCHK();
+    }
+    if (star_rows && !fwd) {
+        subtrees();
         LAUNCHCHK();
     }
     return "";

@@ -277,6 +277,33 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
             endB[f] = U.empty() ? base - 1 : lvB[U[0]];
         }
     };
+    // star subtrees (fronts with at most PANEL_W columns have exactly one panel); their panels leave the star lists
+    P.sub_ptr.assign(1, 0);
+    P.sub_pan.clear();
+    P.sub_rows.clear();
+    P.sub_preF.assign(1, 0);
+    P.sub_preB.assign(1, 0);
+    {
+        std::vector<char> small(nf), ok(nf);
+        for (i64 f = 0; f < nf; f++) small[f] = S.Rptr[f + 1] - S.Rptr[f] <= PANEL_W;
+        for (i64 f = 0; f < nf; f++)   // postorder: a front's children come before it
+            if (!small[f] && S.parent[f] >= 0) small[S.parent[f]] = 0;
+        for (i64 f = 0; f < nf; f++)
+            ok[f] = small[f] && (S.Rptr[f + 1] - S.Rptr[S.fdsc[f]]) + (S.Sptr[f + 1] - S.Sptr[f]) <= SUB_L;
+        for (i64 r = 0; r < nf; r++) {
+            if (!ok[r] || (S.parent[r] >= 0 && ok[S.parent[r]])) continue;
+            for (i64 f = S.fdsc[r]; f <= r; f++) {
+                P.sub_pan.push_back((int32_t)first[f]);
+                su[f].clear();
+            }
+            P.sub_ptr.push_back((int32_t)P.sub_pan.size());
+            const int32_t p = (int32_t)first[r];
+            const int32_t flo = (int32_t)S.Rptr[S.fdsc[r]], fhi = (int32_t)S.Rptr[r + 1];
+            P.sub_rows.insert(P.sub_rows.end(), {flo, fhi, P.rowB_lo[p], P.rowB_hi[p]});
+            P.sub_preF.push_back(P.sub_preF.back() + (fhi - flo + TILE_ROWS - 1) / TILE_ROWS);
+            P.sub_preB.push_back(P.sub_preB.back() + (P.rowB_hi[p] - P.rowB_lo[p] + TILE_ROWS - 1) / TILE_ROWS);
+        }
+    }
     std::vector<i64> lvA, lvB, slvA, slvB;
     {
         std::vector<std::vector<int32_t>> pu(nf);
@@ -287,6 +314,7 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
     levels(su, slvA, slvB);
     P.sunits.clear();
     for (i64 f = 0; f < nf; f++) P.sunits.insert(P.sunits.end(), su[f].begin(), su[f].end());
+    P.sunits.insert(P.sunits.end(), P.sub_pan.begin(), P.sub_pan.end());
     auto rowtiles = [](i64 lo, i64 hi, i64 bm) { return hi > lo ? (hi - lo / bm * bm + bm - 1) / bm : 0; };
     auto make_lists = [&](const std::vector<i64> &lv, bool fwd, std::vector<SweepPlan::List> &out) {
         i64 L = 0;

@@ -880,6 +880,10 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
     Adj G;
     std::string err = symmetrize(n, colptr, rowval, G);
     if (!err.empty()) return err;
+    {
+        double tt = t0;
+        stage("  symmetrize", tt);
+    }
     // 1. fill-reducing order
     std::vector<i64> perm0(n);
     if (opts.ordering == 0) {
