@@ -180,15 +180,18 @@ def bench_mstar(args):
         "phases_ms": {k: round(v * 1e3, 3) for k, v in ph.items()},
     }
     if args.timing and cfg == 3:
-        # dominant kernel family: the X <- X L* sweep (k_sweep_bwd); algorithmic work n * nnz(L) madds
+        # dominant kernel family: the X <- X L* sweep (k_blk backward, k_sweep_bwd, k_sub backward), timed with HIP
+        # events around all its launches on the context's stream; algorithmic work n * nnz(L) madds
         n = g.n
         lstar_madds = n * st["nnzL_alg"]
         t_l = ph["star_Lstar_s"]
         ach = lstar_madds / t_l
-        result["roofline"] = {"bound": "valu", "kernel": "k_sweep_bwd (X <- X L*, all launches of one star)",
+        result["roofline"] = {"bound": "valu",
+                              "kernel": "X <- X L* sweep: k_blk<..., false> + k_sweep_bwd + k_sub<..., false>, all launches "
+                                        "of one star",
                               "achieved": round(ach / 1e12, 4), "peak": round(VALU_PEAK_MADD / 1e12, 2),
                               "unit": "Tmadd/s", "frac": round(ach / VALU_PEAK_MADD, 4),
-                              "traffic": measured_traffic("k_sweep_bwd"),
+                              "traffic": measured_traffic("lstar_sweep"),
                               "algorithmic_madds": lstar_madds, "seconds": round(t_l, 6),
                               "output_floor_GBps": round(4.0 * n * n / T / 1e9, 1)}
     if not args.no_cpu and cfg == 3:

@@ -1,0 +1,76 @@
+"""CPU replay of the star's device schedule (tests/emu/star_plan_emu.cpp): the real plan and block packs, the device
+kernels' index arithmetic launch by launch, bounds / race / initialisation checks, and the result against the oracle.
+
+The replay is built with hipcc as host code (it includes the plan headers) and linked with the oracle library; it is
+skipped where hipcc is absent.  Graphs are chosen so that large fronts cut into 128- and 64-column blocks, blocks are
+followed by panels, small subtrees form, n is odd (guarded row loads) and the graph has several components.
+"""
+
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import dtype_for, weighted
+from pathpack_hip import workloads as W
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+CSRC = os.path.join(REPO, "pathpack.jl_amd", "csrc")
+
+
+def _hipcc():
+    for c in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if c and os.path.exists(c):
+            return c
+    return None
+
+
+@pytest.fixture(scope="module")
+def emu(tmp_path_factory):
+    hipcc = _hipcc()
+    if hipcc is None:
+        pytest.skip("hipcc not available")
+    O.build()
+    exe = str(tmp_path_factory.mktemp("emu") / "star_plan_emu")
+    cmd = [hipcc, "-O2", "-std=c++20", "-I", CSRC, "-I", os.path.join(REPO, "include"),
+           os.path.join(HERE, "emu", "star_plan_emu.cpp"), os.path.join(CSRC, "pp_symbolic.cpp"),
+           os.path.join(CSRC, "pp_plan.cpp"), "-L", os.path.join(REPO, "oracle"), "-lpporacle",
+           "-Wl,-rpath," + os.path.join(REPO, "oracle"), "-lpthread", "-o", exe]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-3000:]
+    return exe
+
+
+GRAPHS = {
+    "grid12x12x12": lambda: W.grid((12, 12, 12)),          # 144-column top front: a 128 block and a 16 panel
+    "grid15x13x11": lambda: W.grid((15, 13, 11)),          # odd n; a 161-column front: 128 + 33 (a 64-wide tile)
+    "grid9x9x9": lambda: W.grid((9, 9, 9)),                # an 82-column front: a 64 block and an 18 panel
+    "components": lambda: W.disjoint_union([W.grid((10, 10, 9)), W.grid((30, 29)), W.rgg(300, seed=5)],
+                                           isolated=3, name="components"),
+}
+
+ALL = [(O.MINPLUS, np.float32), (O.MINPLUS, np.float64), (O.MAXMIN, np.float32), (O.MAXPLUS, np.float64),
+       (O.PLUSPROD, np.float64), (O.ORAND, np.float32)]
+FEW = [(O.MINPLUS, np.float32), (O.MINPLUS, np.float64), (O.PLUSPROD, np.float64)]
+CASES = [(name, s, d) for name in GRAPHS for (s, d) in (ALL if name in ("grid9x9x9", "components") else FEW)]
+
+
+@pytest.mark.parametrize("name,s,fdtype", CASES)
+def test_star_schedule_replay(emu, tmp_path, name, s, fdtype):
+    dtype = dtype_for(s, fdtype)
+    g = weighted(GRAPHS[name](), s, dtype)
+    path = tmp_path / "graph.bin"
+    with open(path, "wb") as f:
+        np.array([g.n, len(g.rowval)], np.int64).tofile(f)
+        np.asarray(g.colptr, np.int64).tofile(f)
+        np.asarray(g.rowval, np.int64).tofile(f)
+        np.asarray(g.nzval, dtype).tofile(f)
+    dcode = {np.dtype(np.float32): 0, np.dtype(np.float64): 1, np.dtype(np.int32): 2}[np.dtype(dtype)]
+    # a compute-unit count of 1 makes every launch with a 128-row tile take it; a huge one forces 64-row tiles
+    for ncu in ([1, 1 << 20] if s == O.MINPLUS and np.dtype(dtype).itemsize == 4 else [1]):
+        r = subprocess.run([emu, str(path), str(s), str(dcode), str(ncu)], capture_output=True, text=True, timeout=300)
+        assert r.returncode == 0, f"ncu={ncu}: {r.stdout[-500:]} {r.stderr[-2000:]}"
