@@ -89,6 +89,14 @@ pp_status pp_destroy(pp_ctx *ctx) {
         if (e) hipEventDestroy(e);
     if (ctx->staging) hipHostFree(ctx->staging);
     if (ctx->staging2) hipHostFree(ctx->staging2);
+    if (ctx->copy_stream) {
+        hipStreamSynchronize(ctx->copy_stream);
+        hipStreamDestroy(ctx->copy_stream);
+    }
+    for (auto &e : ctx->pev)
+        if (e) hipEventDestroy(e);
+    for (auto &p : ctx->outpin)
+        if (p) hipHostFree(p);
     delete ctx;
     return PP_OK;
 }
@@ -443,19 +451,13 @@ pp_status pp_star(pp_ctx *ctx, const pp_fac *fac, void *out, int64_t ldc, int ou
     const size_t es = (size_t)pp::dtype_size(fac->dtype);
     size_t freeb = 0, totalb = 0;
     CHECK_HIP(ctx, hipMemGetInfo(&freeb, &totalb));
-    const size_t need = (size_t)n * n * es * (out_on_device ? 1 : 2);
+    // the star buffer X, plus two column chunks of at most STAR_CHUNK_BYTES each when the output is in host memory
+    const size_t need = (size_t)n * n * es + (out_on_device ? 0 : 2 * (size_t)pp::STAR_CHUNK_BYTES + 2 * (size_t)n * es);
     if (need > freeb)
         return fail(ctx, PP_ENOMEM, "pp_star: needs " + std::to_string(need) + " bytes of device memory, " +
                                         std::to_string(freeb) + " free");
-    void *dout = out;
-    if (!out_on_device) CHECK_HIP(ctx, hipMalloc(&dout, std::max<size_t>(1, (size_t)n * n * es)));
-    std::string e = pp::device_star(ctx, fac, dout, out_on_device ? ldc : n);
+    std::string e = pp::device_star(ctx, fac, out, ldc, out_on_device ? 0 : 1);
     hipError_t se = hipStreamSynchronize(ctx->stream);
-    if (e.empty() && se == hipSuccess && !out_on_device) {
-        if (ldc == n) se = hipMemcpy(out, dout, (size_t)n * n * es, hipMemcpyDeviceToHost);
-        else se = hipMemcpy2D(out, ldc * es, dout, n * es, n * es, n, hipMemcpyDeviceToHost);
-    }
-    if (!out_on_device) hipFree(dout);
     if (!e.empty() || se != hipSuccess)
         return fail(ctx, PP_EHIP, "pp_star: " + (e.empty() ? std::string(hipGetErrorString(se)) : e));
     return PP_OK;

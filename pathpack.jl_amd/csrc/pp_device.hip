@@ -12,7 +12,7 @@ namespace pp {
 
 template <class S> std::string factor_impl(pp_ctx *ctx, pp_fac *fac, const void *nz);
 template <class S> std::string packs_impl(pp_ctx *ctx, pp_fac *fac);
-template <class S> std::string star_impl(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc);
+template <class S> std::string star_impl(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc, int host);
 template <class S> std::string solve_impl(pp_ctx *ctx, const pp_fac *fac, void *B, i64 ldb, i64 nrhs, bool left);
 template <class S>
 std::string gemm_impl(pp_ctx *ctx, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B, i64 ldb, void *C, i64 ldc);
@@ -109,8 +109,8 @@ std::string device_factor(pp_ctx *ctx, pp_fac *fac, const void *d_nzval) {
 
 std::string device_factor_packs(pp_ctx *ctx, pp_fac *fac) { PP_DISPATCH(fac->semiring, fac->dtype, packs_impl<S>(ctx, fac)); }
 
-std::string device_star(pp_ctx *ctx, const pp_fac *fac, void *d_out, i64 ldc) {
-    PP_DISPATCH(fac->semiring, fac->dtype, star_impl<S>(ctx, fac, d_out, ldc));
+std::string device_star(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc, int host) {
+    PP_DISPATCH(fac->semiring, fac->dtype, star_impl<S>(ctx, fac, out, ldc, host));
 }
 
 std::string device_rmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs) {

@@ -61,6 +61,7 @@ constexpr int BLK_K = 32;        // pack rows are padded to a multiple (of every
 constexpr int BLK_CLS = 7;       // list class of star blocks with bn = BLK_W (BLK_CLS + 1: bn = BLK_W / 2)
 constexpr int PREP_T = 64;       // output tile of the block-pack GEMMs
 constexpr int SUB_L = 512;       // largest star subtree: columns plus the root's separator
+constexpr long STAR_CHUNK_BYTES = 128L << 20;   // column chunk of a star written to host memory
 
 inline int width_class(int w) {
     int c = 0;
@@ -178,6 +179,12 @@ struct pp_ctx {
     size_t staging_bytes = 0;
     void *staging2 = nullptr;       // pinned host staging of the sweep plan
     size_t staging2_bytes = 0;
+    // star to host memory: a second stream for the device-to-host copies, the pipeline's events, and two pinned
+    // chunk buffers (kept between calls)
+    hipStream_t copy_stream = nullptr;
+    hipEvent_t pev[4] = {};
+    void *outpin[2] = {nullptr, nullptr};
+    size_t outpin_bytes = 0;
 };
 
 struct pp_fac {
@@ -195,7 +202,9 @@ namespace pp {
 // Numeric drivers (pp_device.hip).  Return "" or an error message.
 std::string device_factor(pp_ctx *ctx, pp_fac *fac, const void *d_nzval);   // up to the reference layout
 std::string device_factor_packs(pp_ctx *ctx, pp_fac *fac);                 // the sweep packs; frees the fronts
-std::string device_star(pp_ctx *ctx, const pp_fac *fac, void *d_out, i64 ldc);
+// The star into out (ldc): device memory, or host memory (host != 0) through pinned chunks overlapped with the
+// device-to-host copies.
+std::string device_star(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc, int host);
 std::string device_rmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs);
 std::string device_lmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs);
 std::string device_sgemx(pp_ctx *ctx, int sr, int dt, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B,

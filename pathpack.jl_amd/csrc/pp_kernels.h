@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstring>
 #include <type_traits>
 
 #include "pp_internal.h"
@@ -1506,17 +1507,19 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
 
 // ===== relabel and permutations =====
 
-// C[i, j] = X[invp[i], invp[j]]  (C <- P^-1 X Q^-1, permuterowscols!, utils.jl:261-505): one workgroup per column
+// C[i, j - j0] = X[invp[i], invp[j]] for the columns j0 <= j < j0 + gridDim (C <- P^-1 X Q^-1, permuterowscols!,
+// utils.jl:261-505): one workgroup per column
 template <class T>
 __global__ __launch_bounds__(NT) void k_relabel(const T *__restrict__ X, i64 n, T *__restrict__ C, i64 ldc,
-                                               const i64 *__restrict__ invp) {
-    const i64 j = blockIdx.x;
+                                               const i64 *__restrict__ invp, i64 j0) {
+    const i64 j = j0 + blockIdx.x;
     const T *src = X + invp[j] * n;
-    T *dst = C + j * ldc;
+    T *dst = C + (j - j0) * ldc;
     for (i64 i = threadIdx.x; i < n; i += NT) dst[i] = src[invp[i]];
 }
 
-// The same with the source column staged in LDS (coalesced read, gather from LDS, coalesced write), for columns of
+// The same for the columns [j0, j1), with the source column staged in LDS (coalesced read, gather from LDS, coalesced
+// write), for columns of
 // at most RELABEL_LDS bytes; persistent workgroups, one per CU.  Rows move in 16-byte vectors (n and ldc multiples
 // of the vector width, 16-byte aligned output), and the next column's loads are in flight while the current one is
 // gathered and written.
@@ -1526,7 +1529,7 @@ constexpr int RELABEL_NT = 1024;
 
 template <class T>
 __global__ __launch_bounds__(RELABEL_NT) void k_relabel_lds(const T *__restrict__ X, i64 n, T *__restrict__ C, i64 ldc,
-                                                           const int32_t *__restrict__ invp) {
+                                                           const int32_t *__restrict__ invp, i64 j0, i64 j1) {
     typedef typename Vec16<T>::type V;
     typedef typename Vec16<T>::idx I;
     constexpr int VW = 16 / sizeof(T);
@@ -1543,17 +1546,17 @@ __global__ __launch_bounds__(RELABEL_NT) void k_relabel_lds(const T *__restrict_
             if (v < nv) buf[u] = __builtin_nontemporal_load(src + v);
         }
     };
-    i64 j = blockIdx.x;
-    if (j < n) load(j);
-    for (; j < n; j += gridDim.x) {
+    i64 j = j0 + blockIdx.x;
+    if (j < j1) load(j);
+    for (; j < j1; j += gridDim.x) {
 #pragma unroll
         for (int u = 0; u < RV; u++) {
             const int v = threadIdx.x + u * RELABEL_NT;
             if (v < nv) col[v] = buf[u];
         }
         __syncthreads();
-        if (j + gridDim.x < n) load(j + gridDim.x);
-        V *dst = reinterpret_cast<V *>(C + j * ldc);
+        if (j + gridDim.x < j1) load(j + gridDim.x);
+        V *dst = reinterpret_cast<V *>(C + (j - j0) * ldc);
         const I *ip = reinterpret_cast<const I *>(invp);
         for (int v = threadIdx.x; v < nv; v += RELABEL_NT) {
             const I p = ip[v];
@@ -1965,8 +1968,21 @@ template <class S> struct StarRun {
     const pp_fac *fac;
     void *out;
     i64 ldc;
+    int host;
     std::string err;
     void operator()() { err = run(); }
+    // C[:, j0:j1] <- X relabelled, into device memory at C (leading dimension ldc)
+    void relabel(const typename S::value_type *X, i64 n, typename S::value_type *C, i64 ld, i64 j0, i64 j1) {
+        typedef typename S::value_type T;
+        hipStream_t st = ctx->stream;
+        if (j1 <= j0) return;
+        constexpr i64 VW = 16 / sizeof(T);
+        if (n * (i64)sizeof(T) <= RELABEL_LDS && n % VW == 0 && ld % VW == 0 && ((uintptr_t)C & 15) == 0)
+            k_relabel_lds<T><<<(unsigned)std::min<i64>(j1 - j0, ctx->num_cu), RELABEL_NT, 0, st>>>(
+                X, n, C, ld, fac->plan.invp32, j0, j1);
+        else
+            k_relabel<T><<<(unsigned)(j1 - j0), NT, 0, st>>>(X, n, C, ld, fac->plan.invp, j0);
+    }
     std::string run() {
         typedef typename S::value_type T;
         const i64 n = fac->sym->S.n;
@@ -1989,18 +2005,94 @@ template <class S> struct StarRun {
         if (!e.empty()) return e;
         timer_stop(ctx, 2);
         timer_start(ctx, 3);
-        if (n > 0) {
-            constexpr i64 VW = 16 / sizeof(T);
-            if (n * (i64)sizeof(T) <= RELABEL_LDS && n % VW == 0 && ldc % VW == 0 && ((uintptr_t)out & 15) == 0)
-                k_relabel_lds<T><<<(unsigned)std::min<i64>(n, ctx->num_cu), RELABEL_NT, 0, st>>>(X, n, (T *)out, ldc,
-                                                                                                fac->plan.invp32);
-            else
-                k_relabel<T><<<(unsigned)n, NT, 0, st>>>(X, n, (T *)out, ldc, fac->plan.invp);
+        if (!host) {
+            relabel(X, n, (T *)out, ldc, 0, n);
+            LAUNCHCHK();
+        } else if (n > 0) {
+            e = to_host(X, n);
+            if (!e.empty()) {
+                hipStreamSynchronize(st);
+                hipFreeAsync(X, st);
+                return e;
+            }
         }
-        LAUNCHCHK();
         timer_stop(ctx, 3);
         HIPCHK(hipFreeAsync(X, st));
         return "";
+    }
+    // Relabel into host memory in K >= 4 column chunks: chunk k is relabelled into device buffer k % 2 (the
+    // context's stream), copied into pinned buffer k % 2 (the copy stream, after the relabel's event), then copied
+    // by the host's worker threads into `out`; the relabel of chunk k + 2 starts once chunk k's device-to-host copy
+    // is done, and its copy once the host has read the pinned buffer.  The device computes, the copy engine moves
+    // and the host copies three different chunks at a time.
+    std::string to_host(const typename S::value_type *X, i64 n) {
+        typedef typename S::value_type T;
+        hipStream_t st = ctx->stream;
+        const i64 total = n * n * (i64)sizeof(T);
+        const i64 K = std::min<i64>(n, std::max<i64>(4, (total + STAR_CHUNK_BYTES - 1) / STAR_CHUNK_BYTES));
+        const i64 CB = (n + K - 1) / K;   // columns per chunk
+        const i64 nchunk = (n + CB - 1) / CB;
+        const size_t cbytes = (size_t)(CB * n) * sizeof(T);
+        if (!ctx->copy_stream) HIPCHK(hipStreamCreateWithFlags(&ctx->copy_stream, hipStreamNonBlocking));
+        for (auto &ev : ctx->pev)
+            if (!ev) HIPCHK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+        if (ctx->outpin_bytes < cbytes) {
+            for (auto &p : ctx->outpin)
+                if (p) hipHostFree(p);
+            ctx->outpin[0] = ctx->outpin[1] = nullptr;
+            ctx->outpin_bytes = 0;
+            for (auto &p : ctx->outpin) HIPCHK(hipHostMalloc(&p, cbytes, hipHostMallocDefault));
+            ctx->outpin_bytes = cbytes;
+        }
+        T *dc[2] = {nullptr, nullptr};
+        HIPCHK(hipMallocAsync((void **)&dc[0], 2 * cbytes, st));
+        dc[1] = dc[0] + CB * n;
+        hipStream_t cs = ctx->copy_stream;
+        auto cols = [&](i64 k, i64 &j0, i64 &j1) {
+            j0 = k * CB;
+            j1 = std::min(n, j0 + CB);
+        };
+        auto produce = [&](i64 k) -> std::string {   // relabel chunk k on the device, then its copy to pinned memory
+            i64 j0, j1;
+            cols(k, j0, j1);
+            const int b = (int)(k & 1);
+            relabel(X, n, dc[b], n, j0, j1);
+            LAUNCHCHK();
+            HIPCHK(hipEventRecord(ctx->pev[b], st));
+            HIPCHK(hipStreamWaitEvent(cs, ctx->pev[b], 0));
+            HIPCHK(hipMemcpyAsync(ctx->outpin[b], dc[b], (size_t)((j1 - j0) * n) * sizeof(T), hipMemcpyDeviceToHost, cs));
+            HIPCHK(hipEventRecord(ctx->pev[2 + b], cs));
+            return "";
+        };
+        std::string e;
+        for (i64 k = 0; k < std::min<i64>(2, nchunk) && e.empty(); k++) e = produce(k);
+        for (i64 k = 0; k < nchunk && e.empty(); k++) {
+            const int b = (int)(k & 1);
+            hipError_t he = hipEventSynchronize(ctx->pev[2 + b]);
+            if (he != hipSuccess) {
+                e = std::string("hipEventSynchronize: ") + hipGetErrorString(he);
+                break;
+            }
+            i64 j0, j1;
+            cols(k, j0, j1);
+            const T *src = (const T *)ctx->outpin[b];
+            T *dst = (T *)out + j0 * ldc;
+            const i64 m = j1 - j0;
+            const int nt = (int)std::max<i64>(1, std::min<i64>(16, (m * n * (i64)sizeof(T)) >> 22));   // 4 MiB a thread
+            pool_run(nt, [&](int t) {
+                if (ldc == n) {
+                    const i64 a = m * n * t / nt, z = m * n * (t + 1) / nt;
+                    std::memcpy(dst + a, src + a, (size_t)(z - a) * sizeof(T));
+                } else {
+                    for (i64 j = m * t / nt; j < m * (t + 1) / nt; j++)
+                        std::memcpy(dst + j * ldc, src + j * n, (size_t)n * sizeof(T));
+                }
+            });
+            if (k + 2 < nchunk) e = produce(k + 2);
+        }
+        hipStreamSynchronize(cs);
+        hipFreeAsync(dc[0], st);
+        return e;
     }
 };
 
@@ -2093,8 +2185,8 @@ template <class S> std::string packs_impl(pp_ctx *ctx, pp_fac *fac) {
     r();
     return r.err;
 }
-template <class S> std::string star_impl(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc) {
-    StarRun<S> r{ctx, fac, out, ldc};
+template <class S> std::string star_impl(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc, int host) {
+    StarRun<S> r{ctx, fac, out, ldc, host};
     r();
     return r.err;
 }

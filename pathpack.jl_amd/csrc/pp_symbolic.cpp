@@ -277,15 +277,10 @@ struct ND {
             return;
         }
         // connected components of the item
+        // the first breadth-first search starts at the item's first vertex; the pseudo-peripheral search below moves
+        // the root to the far end
         i64 cnt;
         i32 root = it.V[0];
-        {
-            i64 bd = 1LL << 60;
-            for (i32 v : it.V) {
-                i64 d = degree_in(v, id);
-                if (d < bd) { bd = d; root = v; }
-            }
-        }
         int nlev = bfs(queue, id, root, cnt, lptr);
         if (cnt < sz) {
             // disconnected: every component becomes an item of its own

@@ -252,3 +252,21 @@ def test_device_resident_star_and_solves():
     dR = P.DeviceArray.from_numpy(R)
     P.rmul_(dR, F)
     assert np.array_equal(bits(dR.numpy()), bits(C[[0, 10, 20, 30, 89], :]))
+
+
+@pytest.mark.parametrize("ld_pad", [0, 3])
+def test_star_to_host_in_chunks(ld_pad):
+    """pp_star into host memory goes through pinned column chunks (at least four) and the host's copy threads; with
+    a leading dimension larger than n the chunks land column by column.  Same bits as the star left in HBM."""
+    import ctypes
+
+    g = weighted(W.grid((15, 13, 11)), O.MINPLUS, np.float32)
+    F = P.mlu(P.MinPlus(), g)
+    D = P.Matrix(F, device=True).numpy()
+    n = g.n
+    ldc = n + ld_pad
+    C = np.full((ldc, n), -1.0, np.float32, order="F")
+    F.ctx.check(P.lib().pp_star(F.ctx.handle, F.handle, ctypes.c_void_p(C.ctypes.data), ldc, 0))
+    assert np.array_equal(bits(C[:n, :]), bits(D))
+    assert np.all(C[n:, :] == -1.0)
+    assert np.array_equal(bits(D), bits(O.star(O.factor(O.MINPLUS, oracle_sym(F.sym), g.colptr, g.rowval, g.nzval))))
