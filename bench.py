@@ -354,6 +354,24 @@ def bench_solve(args, cfg):
     st = sym.stats()
     madds = st["madds_rhs_alg"] * nrhs
     name = "lmul!" if left else "rmul!"
+    # the same unit-vector right-hand sides as one batch of sources (columns / rows of A*, pp_star_sources): the
+    # sweeps visit only the sources under each front; the result must equal the solve's
+    which = 1 if left else 0
+    dO = P.DeviceArray(B.shape, B.dtype)
+    csrc = np.ascontiguousarray(src, dtype=np.int64)
+
+    def run_src():
+        ctx.check(P.lib().pp_star_sources(ctx.handle, F.handle, which, nrhs, csrc.ctypes.data_as(ctypes.c_void_p),
+                                          ctypes.c_void_p(dO.ptr), ld, 1))
+
+    T2 = timed(run_src, ctx, args.steps, args.warmup)
+    got, ref = dO.numpy(), dB.numpy()
+    if left:
+        same = bool(np.array_equal(got.view(np.uint32), ref.view(np.uint32)))
+        maxrel = 0.0
+    else:
+        maxrel = float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), np.finfo(np.float64).tiny)))
+        same = maxrel <= 1e-12
     r = base_result(args, f"{name} sec + semiring Gop/s, {s.name} {nrhs} RHS, n={n}", madds / T / 1e9,
                     "semiring Gop/s", T, "f32" if left else "f64",
                     (f"MaxMin lmul! of 1024 unit columns (+Inf at a seeded source, -Inf elsewhere) on a random "
@@ -364,6 +382,8 @@ def bench_solve(args, cfg):
                     {"n": n, "nrhs": nrhs, "madds_alg": madds, "fronts": sym.nf})
     r["phases_ms"] = {"symbolic_s": round(t_sym * 1e3, 3), "factor_s": round(t_fac * 1e3, 3),
                       "solve_device_s": round(t_dev * 1e3, 3)}
+    r["unit_sources"] = {"entry": "pp_star_sources", "ms_per_step": round(T2 * 1e3, 3),
+                         "speedup_vs_solve": round(T / T2, 2), "matches_solve": same, "max_rel": maxrel}
     if not args.no_cpu:
         k = 32
         e = sym.export()

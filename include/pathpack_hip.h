@@ -127,6 +127,14 @@ pp_status pp_fac_destroy(pp_fac *fac);
  * out_on_device != 0, else a host pointer (the star is assembled in HBM, then copied back).  Replaces sgetri!(F, C)
  * (src/CPU/chordal_slu.jl:501-513 -> chordal/sgetri.jl:13-31, utils.jl:261-505). */
 pp_status pp_star(pp_ctx *ctx, const pp_fac *fac, void *out, int64_t ldc, int out_on_device);
+/* Rows (which = 0) or columns (which = 1) of A* for the sources src[0..nsrc) (0-based original labels, in any
+ * order, repeats allowed): rows: out (nsrc x n, ldo >= nsrc) row k <- row src[k] of A*; columns: out (n x nsrc,
+ * ldo >= n) column k <- column src[k] of A*.  The sweeps visit, for each front, only the sources of its subtree
+ * (forward) and of its component (backward).  Replaces sgetre!(F, Val(:L), Val(:T), b, k) (rows) and
+ * sgetre!(F, Val(:L), Val(:N), b, k) (columns), one source at a time in the reference
+ * (src/CPU/chordal_slu.jl:445-493, chordal/sgetre.jl).  `out` is a device pointer when out_on_device != 0. */
+pp_status pp_star_sources(pp_ctx *ctx, const pp_fac *fac, int which, int64_t nsrc, const int64_t *src, void *out,
+                          int64_t ldo, int out_on_device);
 /* lmul!(F, B): B (n x nrhs, column-major, ldb >= n) <- A* B, the least solution of X = A X (+) B.
  * B is a device pointer when on_device != 0, else a host pointer.  (abstract_slu.jl:131-134) */
 pp_status pp_lmul(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int64_t nrhs, int on_device);

@@ -463,6 +463,77 @@ pp_status pp_star(pp_ctx *ctx, const pp_fac *fac, void *out, int64_t ldc, int ou
     return PP_OK;
 }
 
+pp_status pp_star_sources(pp_ctx *ctx, const pp_fac *fac, int which, int64_t nsrc, const int64_t *src, void *out,
+                          int64_t ldo, int out_on_device) {
+    if (!ctx || !fac || (nsrc > 0 && (!src || !out))) return fail(ctx, PP_EINVAL, "pp_star_sources: null argument");
+    if (which != 0 && which != 1) return fail(ctx, PP_EINVAL, "pp_star_sources: which must be 0 (rows) or 1 (columns)");
+    const pp::Symbolic &S = fac->sym->S;
+    const i64 n = S.n;
+    if (nsrc < 0) return fail(ctx, PP_EINVAL, "pp_star_sources: nsrc < 0");
+    if (which == 0 ? ldo < std::max<i64>(1, nsrc) : ldo < std::max<i64>(1, n))
+        return fail(ctx, PP_EINVAL, "pp_star_sources: leading dimension too small");
+    if (nsrc > (i64)1 << 30) return fail(ctx, PP_EINVAL, "pp_star_sources: too many sources");
+    for (i64 k = 0; k < nsrc; k++)
+        if (src[k] < 0 || src[k] >= n) return fail(ctx, PP_EINVAL, "pp_star_sources: source index out of range");
+    if (nsrc == 0 || n == 0) return PP_OK;
+    CHECK_HIP(ctx, hipSetDevice(ctx->device));
+    const pp::SweepPlan &P = *fac->sym->splan;
+    // the sweep rows: the distinct sources in elimination order
+    pp::RowSub R;
+    R.js.resize(nsrc);
+    for (i64 k = 0; k < nsrc; k++) R.js[k] = (int32_t)S.invp[src[k]];
+    std::sort(R.js.begin(), R.js.end());
+    R.js.erase(std::unique(R.js.begin(), R.js.end()), R.js.end());
+    std::vector<int32_t> pos(nsrc);
+    for (i64 k = 0; k < nsrc; k++) pos[k] = R.map((int32_t)S.invp[src[k]]);
+    pp::build_row_subset(P, S, R);
+    const i64 m = (i64)R.js.size();
+    const size_t es = (size_t)pp::dtype_size(fac->dtype);
+    const size_t bytesO = (size_t)ldo * (size_t)(which == 0 ? n : nsrc) * es;
+    // one device block for the row-subset arrays
+    std::vector<int32_t> blk;
+    std::vector<std::pair<int32_t **, size_t>> where;
+    auto add = [&](const std::vector<int32_t> &v, int32_t **dst) {
+        where.push_back({dst, blk.size()});
+        blk.insert(blk.end(), v.begin(), v.end());
+        blk.resize((blk.size() + 63) / 64 * 64);   // 256-byte aligned pieces
+    };
+    add(R.js, &R.d_js);
+    add(R.rowA_lo, &R.d_rowA_lo);
+    add(R.rowA_hi, &R.d_rowA_hi);
+    add(R.rowB_lo, &R.d_rowB_lo);
+    add(R.rowB_hi, &R.d_rowB_hi);
+    add(R.tiles, &R.d_tiles);
+    add(R.sub_rows, &R.d_sub_rows);
+    add(R.sub_preF, &R.d_sub_preF);
+    add(R.sub_preB, &R.d_sub_preB);
+    add(pos, &R.d_pos);
+    size_t freeb = 0, totalb = 0;
+    CHECK_HIP(ctx, hipMemGetInfo(&freeb, &totalb));
+    const size_t need = (size_t)m * n * es + blk.size() * sizeof(int32_t) + (out_on_device ? 0 : bytesO);
+    if (need > freeb)
+        return fail(ctx, PP_ENOMEM, "pp_star_sources: needs " + std::to_string(need) + " bytes of device memory, " +
+                                        std::to_string(freeb) + " free");
+    void *dblk = nullptr;
+    CHECK_HIP(ctx, hipMalloc(&dblk, blk.size() * sizeof(int32_t)));
+    for (auto &w : where) *w.first = (int32_t *)dblk + w.second;
+    void *dO = out;
+    hipError_t ue = hipMemcpy(dblk, blk.data(), blk.size() * sizeof(int32_t), hipMemcpyHostToDevice);
+    if (ue == hipSuccess && !out_on_device) ue = hipMalloc(&dO, bytesO);
+    if (ue != hipSuccess) {
+        hipFree(dblk);
+        return fail(ctx, PP_EHIP, std::string("pp_star_sources: ") + hipGetErrorString(ue));
+    }
+    std::string e = pp::device_star_sources(ctx, fac, R, nsrc, which, dO, ldo);
+    hipError_t se = hipStreamSynchronize(ctx->stream);
+    if (e.empty() && se == hipSuccess && !out_on_device) se = hipMemcpy(out, dO, bytesO, hipMemcpyDeviceToHost);
+    if (!out_on_device) hipFree(dO);
+    hipFree(dblk);
+    if (!e.empty() || se != hipSuccess)
+        return fail(ctx, PP_EHIP, "pp_star_sources: " + (e.empty() ? std::string(hipGetErrorString(se)) : e));
+    return PP_OK;
+}
+
 static pp_status solve(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int64_t nrhs, int on_device, bool left) {
     const char *name = left ? "pp_lmul" : "pp_rmul";
     if (!ctx || !fac || (!B && nrhs > 0)) return fail(ctx, PP_EINVAL, std::string(name) + ": null argument");

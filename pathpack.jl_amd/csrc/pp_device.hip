@@ -13,6 +13,8 @@ namespace pp {
 template <class S> std::string factor_impl(pp_ctx *ctx, pp_fac *fac, const void *nz);
 template <class S> std::string packs_impl(pp_ctx *ctx, pp_fac *fac);
 template <class S> std::string star_impl(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc, int host);
+template <class S>
+std::string star_src_impl(pp_ctx *ctx, const pp_fac *fac, const RowSub &R, i64 nsrc, int cols, void *out, i64 ldo);
 template <class S> std::string solve_impl(pp_ctx *ctx, const pp_fac *fac, void *B, i64 ldb, i64 nrhs, bool left);
 template <class S>
 std::string gemm_impl(pp_ctx *ctx, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B, i64 ldb, void *C, i64 ldc);
@@ -111,6 +113,10 @@ std::string device_factor_packs(pp_ctx *ctx, pp_fac *fac) { PP_DISPATCH(fac->sem
 
 std::string device_star(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc, int host) {
     PP_DISPATCH(fac->semiring, fac->dtype, star_impl<S>(ctx, fac, out, ldc, host));
+}
+
+std::string device_star_sources(pp_ctx *ctx, const pp_fac *fac, const RowSub &R, i64 nsrc, int cols, void *out, i64 ldo) {
+    PP_DISPATCH(fac->semiring, fac->dtype, star_src_impl<S>(ctx, fac, R, nsrc, cols, out, ldo));
 }
 
 std::string device_rmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs) {

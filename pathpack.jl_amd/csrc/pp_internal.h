@@ -135,6 +135,24 @@ struct SweepPlan {
 std::string build_factor_plan(const Symbolic &S, FactorPlan &P);
 std::string build_sweep_plan(const Symbolic &S, SweepPlan &P);
 
+// The sweeps over the rows of a set of sources instead of all n (rows or columns of the star for chosen vertices).
+// Row k of the sweep buffer starts as the unit vector of source js[k] (elimination labels, ascending).  A unit's
+// forward rows are then the sources in its subtree, a contiguous range of js, and its backward rows the sources of
+// its component: the plan's row ranges mapped through js, with the tile prefixes of every list recomputed in the
+// plan's layout.
+struct RowSub {
+    std::vector<int32_t> js;                        // sorted sources (elimination labels)
+    std::vector<int32_t> rowA_lo, rowA_hi, rowB_lo, rowB_hi;   // per unit
+    std::vector<int32_t> tiles;                     // the plan's prefix arrays for these rows
+    std::vector<int32_t> sub_rows, sub_preF, sub_preB;
+    // device copies
+    int32_t *d_js = nullptr, *d_rowA_lo = nullptr, *d_rowA_hi = nullptr, *d_rowB_lo = nullptr, *d_rowB_hi = nullptr;
+    int32_t *d_tiles = nullptr, *d_sub_rows = nullptr, *d_sub_preF = nullptr, *d_sub_preB = nullptr;
+    int32_t *d_pos = nullptr;                       // row of the sweep buffer of each requested source (input order)
+    int32_t map(int32_t r) const;                   // plan row r (a source label) -> first sweep row with js >= r
+};
+void build_row_subset(const SweepPlan &P, const Symbolic &S, RowSub &R);
+
 // Device copies of the plans.
 struct DevPlan {
     // factor
@@ -205,6 +223,9 @@ std::string device_factor_packs(pp_ctx *ctx, pp_fac *fac);                 // th
 // The star into out (ldc): device memory, or host memory (host != 0) through pinned chunks overlapped with the
 // device-to-host copies.
 std::string device_star(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc, int host);
+// Rows (cols = 0: out[k, j] = A*[src_k, j], nsrc x n, leading dimension ldo) or columns (cols = 1: out[i, k] =
+// A*[i, src_k], n x nsrc) of the star for the sources of R (device copies uploaded), into device memory.
+std::string device_star_sources(pp_ctx *ctx, const pp_fac *fac, const RowSub &R, i64 nsrc, int cols, void *out, i64 ldo);
 std::string device_rmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs);
 std::string device_lmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs);
 std::string device_sgemx(pp_ctx *ctx, int sr, int dt, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B,

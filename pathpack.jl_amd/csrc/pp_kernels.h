@@ -53,26 +53,30 @@ __global__ void k_scatter_entries(T *__restrict__ F, const i64 *__restrict__ pos
     for (i64 i = blockIdx.x * (i64)NT + threadIdx.x; i < nnz; i += (i64)gridDim.x * NT) F[pos[i]] = val[i];
 }
 
-// X <- I in the semiring (the start of X <- U*), on the entries the sweeps read before writing them, for the star's
-// units (panels and blocks) p: column c of p over the rows [alo[p], ahi[p]) of its subtree (every forward write into column c comes from a panel of
+// X <- I in the semiring (the start of X <- U*; row i is the unit vector of source rsrc[i], or of i), on the entries
+// the sweeps read before writing them, for the units p (units[], or all panels): column c of p over the rows
+// [alo[p], ahi[p]) of its subtree (every forward write into column c comes from a panel of
 // that subtree; the backward sweep takes the other rows of its component as zero), and over the rows outside the
 // component [blo[p], bhi[p]), which no sweep visits.
 template <class S>
 __global__ __launch_bounds__(NT) void k_identity_panels(typename S::value_type *__restrict__ X, i64 n,
-                                                        const int32_t *__restrict__ units,
+                                                        const int32_t *__restrict__ units, const int32_t *__restrict__ rsrc,
+                                                        i64 ncols,
                                                         const int32_t *__restrict__ c0, const int32_t *__restrict__ w,
                                                         const int32_t *__restrict__ alo, const int32_t *__restrict__ ahi,
                                                         const int32_t *__restrict__ blo,
                                                         const int32_t *__restrict__ bhi) {
     typedef typename S::value_type T;
-    const int p = units[blockIdx.x];
+    const int p = units ? units[blockIdx.x] : (int)blockIdx.x;
     for (int j = blockIdx.y; j < w[p]; j += gridDim.y) {
         const i64 col = c0[p] + j;
         T *x = X + col * n;
-        for (i64 i = alo[p] + threadIdx.x; i < ahi[p]; i += NT) x[i] = i == col ? S::one() : S::zero();
+        for (i64 i = alo[p] + threadIdx.x; i < ahi[p]; i += NT)
+            x[i] = (rsrc ? (i64)rsrc[i] : i) == col ? S::one() : S::zero();
         for (i64 i = threadIdx.x; i < blo[p]; i += NT) x[i] = S::zero();
         for (i64 i = bhi[p] + threadIdx.x; i < n; i += NT) x[i] = S::zero();
     }
+    (void)ncols;
 }
 
 // ===== extend-add: F_f <- F_f (+) inj M_c inj^T for every child c (sgetrf_send!, chordal/sgetrf.jl:257-290) =====
@@ -1086,7 +1090,7 @@ __global__ __launch_bounds__(64) void k_sub(typename S::value_type *__restrict__
         // compute on a row inside and store nothing
         const int plo = FWD ? a.rowA_lo[p] : lo, phi = FWD ? a.rowA_hi[p] : hi;
         const i64 t0 = (i64)lo + (i64)tile * TILE_ROWS;
-        if (t0 >= phi || t0 + TILE_ROWS <= plo) continue;
+        if (plo >= phi || t0 >= phi || t0 + TILE_ROWS <= plo) continue;   // (a source subset can leave none)
         const bool store = r >= plo && r < phi;
         const i64 rr = r < plo ? plo : (r >= phi ? phi - 1 : r);
         const int cls = w <= 1 ? 0 : 32 - __builtin_clz(w - 1);
@@ -1773,10 +1777,11 @@ static void launch_bwd(unsigned grid, int dmode, typename S::value_type *X, i64 
 template <class S, int W>
 static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type *X, i64 ld, const SweepArgs &base,
                         const SweepPlan &Wp, const SweepPlan::List &li, bool star_rows, i64 nrows, const void *Dpack,
-                        const void *pack, hipStream_t st) {
+                        const void *pack, hipStream_t st, const RowSub *rs) {
     typedef typename S::value_type T;
     const T *D = (const T *)Dpack, *Pk = (const T *)pack;
-    const int32_t *tiles = base.pre;   // device copy of Wp.tiles
+    const int32_t *tiles = base.pre;   // device copy of the prefix arrays
+    const std::vector<int32_t> &HT = rs ? rs->tiles : Wp.tiles;
     SweepArgs a = base;
     if (fwd) {
         // one launch per list: the panels' own columns solved and scattered, per (64-row tile, target chunk)
@@ -1784,10 +1789,10 @@ static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type
         a.cpre = tiles + li.pC;
         if (star_rows) {
             a.pre = tiles + li.pAu;
-            grid = (unsigned)Wp.tiles[li.pAu + li.cnt];
+            grid = (unsigned)HT[li.pAu + li.cnt];
         } else {
             a.pre = nullptr;
-            grid = (unsigned)(((nrows + TILE_ROWS - 1) / TILE_ROWS) * Wp.tiles[li.pC + li.cnt]);
+            grid = (unsigned)(((nrows + TILE_ROWS - 1) / TILE_ROWS) * HT[li.pC + li.cnt]);
         }
         if (grid) {
             if (atomic) {
@@ -1803,13 +1808,13 @@ static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type
         i64 ntile = 0;
         if (star_rows && !li.uniB) {
             a.pre = tiles + li.pB64;
-            grid = (unsigned)Wp.tiles[li.pB64 + li.cnt];
+            grid = (unsigned)HT[li.pB64 + li.cnt];
             ntile = grid / std::max<i64>(1, li.cnt);
         } else {
             a.pre = nullptr;
             if (star_rows) {
-                a.row_base = li.rowB_lo;
-                a.nrows = li.rowB_hi - li.rowB_lo;
+                a.row_base = rs ? rs->map(li.rowB_lo) : li.rowB_lo;
+                a.nrows = (rs ? rs->map(li.rowB_hi) : li.rowB_hi) - a.row_base;
             }
             ntile = (a.nrows + TILE_ROWS - 1) / TILE_ROWS;
             grid = (unsigned)(li.cnt * ((ntile + 7) / 8) * 8);
@@ -1846,25 +1851,28 @@ static void launch_blk(pp_ctx *ctx, bool fwd, typename S::value_type *X, i64 ld,
 
 template <class S>
 static void launch_blocks(pp_ctx *ctx, const pp_fac *fac, bool fwd, typename S::value_type *X, i64 ld, i64 nrows,
-                          const SweepPlan::List &li) {
+                          const SweepPlan::List &li, const RowSub *rs) {
     typedef typename S::value_type T;
     const SweepPlan &Wp = *fac->sym->splan;
     const DevPlan &d = fac->plan;
-    int q = sizeof(T) == 4 && Wp.tiles[li.pT[1] + li.cnt] >= 2 * ctx->num_cu ? 1 : 0;
+    const std::vector<int32_t> &HT = rs ? rs->tiles : Wp.tiles;
+    int q = sizeof(T) == 4 && HT[li.pT[1] + li.cnt] >= 2 * ctx->num_cu ? 1 : 0;
     BlkArgs a;
     a.ulist = d.plist + li.off;
-    a.pre = d.tiles + li.pT[q];
+    a.pre = (rs ? rs->d_tiles : d.tiles) + li.pT[q];
     a.nu = (int32_t)li.cnt;
     a.np = (int32_t)Wp.np;
-    a.ntask = Wp.tiles[li.pT[q] + li.cnt];
+    a.ntask = HT[li.pT[q] + li.cnt];
     a.nrows = nrows;
     a.p_c0 = d.p_c0;
     a.p_w = d.p_w;
     a.p_e = d.p_e;
-    a.rlo = fwd ? d.p_rowA_lo : d.p_rowB_lo;
-    a.rhi = fwd ? d.p_rowA_hi : d.p_rowB_hi;
-    a.olo = d.p_rowA_lo;
-    a.ohi = d.p_rowA_hi;
+    const int32_t *rAlo = rs ? rs->d_rowA_lo : d.p_rowA_lo, *rAhi = rs ? rs->d_rowA_hi : d.p_rowA_hi;
+    const int32_t *rBlo = rs ? rs->d_rowB_lo : d.p_rowB_lo, *rBhi = rs ? rs->d_rowB_hi : d.p_rowB_hi;
+    a.rlo = fwd ? rAlo : rBlo;
+    a.rhi = fwd ? rAhi : rBhi;
+    a.olo = rAlo;
+    a.ohi = rAhi;
     a.p_eoff = d.p_eoff;
     a.Eidx = d.Eidx;
     a.b_boff = d.b_boff;
@@ -1883,32 +1891,36 @@ static void launch_blocks(pp_ctx *ctx, const pp_fac *fac, bool fwd, typename S::
     else launch_blk<S, 4, 4>(ctx, fwd, X, ld, a, fac->Hpack, fac->Bpack);
 }
 
+// star_rows: each unit's own rows (those of the plan, or of the source subset rs); otherwise rows [0, nrows) for
+// every panel (the solves; atomic forward scatter).  star_lists: the star's units (blocks for the large fronts, the
+// small subtrees first forward and last backward; dmode 0 only) rather than panels only.
 template <class S>
 static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmode, typename S::value_type *X, i64 ld,
-                              bool star_rows, i64 nrows, const void *pack) {
+                              bool star_rows, i64 nrows, const void *pack, const RowSub *rs = nullptr,
+                              int star_lists = -1) {
     const SweepPlan &Wp = *fac->sym->splan;
     const DevPlan &d = fac->plan;
     hipStream_t st = ctx->stream;
-    // the star runs the blocks of the large fronts and the small subtrees (first forward, last backward); the solves
-    // run panels only
-    const auto &lists = star_rows ? (fwd ? Wp.sfwd : Wp.sbwd) : (fwd ? Wp.fwd : Wp.bwd);
+    const bool sl = star_lists < 0 ? star_rows : star_lists != 0;
+    const auto &lists = sl ? (fwd ? Wp.sfwd : Wp.sbwd) : (fwd ? Wp.fwd : Wp.bwd);
     if (nrows == 0) return "";
     auto subtrees = [&]() {
         typedef typename S::value_type T;
         const i64 nsub = (i64)Wp.sub_ptr.size() - 1;
-        const int32_t ntask = fwd ? Wp.sub_preF.back() : Wp.sub_preB.back();
+        const int32_t ntask = rs ? (fwd ? rs->sub_preF.back() : rs->sub_preB.back())
+                                 : (fwd ? Wp.sub_preF.back() : Wp.sub_preB.back());
         if (nsub <= 0 || ntask == 0) return;
         SubArgs b;
         b.ptr = d.sub_ptr;
         b.pan = d.sub_pan;
-        b.rows = d.sub_rows;
-        b.pre = fwd ? d.sub_preF : d.sub_preB;
+        b.rows = rs ? rs->d_sub_rows : d.sub_rows;
+        b.pre = rs ? (fwd ? rs->d_sub_preF : rs->d_sub_preB) : (fwd ? d.sub_preF : d.sub_preB);
         b.nsub = (int32_t)nsub;
         b.p_c0 = d.p_c0;
         b.p_w = d.p_w;
         b.p_e = d.p_e;
-        b.rowA_lo = d.p_rowA_lo;
-        b.rowA_hi = d.p_rowA_hi;
+        b.rowA_lo = rs ? rs->d_rowA_lo : d.p_rowA_lo;
+        b.rowA_hi = rs ? rs->d_rowA_hi : d.p_rowA_hi;
         b.p_eoff = d.p_eoff;
         b.p_poff = d.p_poff;
         b.p_doff = d.p_doff;
@@ -1916,19 +1928,19 @@ static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmod
         if (fwd) k_sub<S, true><<<(unsigned)ntask, 64, 0, st>>>(X, ld, b, (const T *)fac->Dpack, (const T *)pack);
         else k_sub<S, false><<<(unsigned)ntask, 64, 0, st>>>(X, ld, b, (const T *)fac->Dpack, (const T *)pack);
     };
-    if (star_rows && fwd) {
+    if (sl && fwd) {
         subtrees();
         LAUNCHCHK();
     }
     for (const auto &li : lists) {
         if (li.cls >= BLK_CLS) {
-            launch_blocks<S>(ctx, fac, fwd, X, ld, nrows, li);
+            launch_blocks<S>(ctx, fac, fwd, X, ld, nrows, li, rs);
             LAUNCHCHK();
             continue;
         }
         SweepArgs a;
         a.plist = d.plist + li.off;
-        a.pre = d.tiles;   // base of the prefix arrays; launch_list offsets it
+        a.pre = rs ? rs->d_tiles : d.tiles;   // base of the prefix arrays; launch_list offsets it
         a.cpre = nullptr;
         a.np = (int32_t)li.cnt;
         a.nrows = (int32_t)nrows;
@@ -1937,26 +1949,28 @@ static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmod
         a.p_w = d.p_w;
         a.p_e = d.p_e;
         a.p_chunks = d.p_chunks;
-        a.row_lo = fwd ? d.p_rowA_lo : d.p_rowB_lo;
-        a.row_hi = fwd ? d.p_rowA_hi : d.p_rowB_hi;
+        const int32_t *rAlo = rs ? rs->d_rowA_lo : d.p_rowA_lo, *rAhi = rs ? rs->d_rowA_hi : d.p_rowA_hi;
+        const int32_t *rBlo = rs ? rs->d_rowB_lo : d.p_rowB_lo, *rBhi = rs ? rs->d_rowB_hi : d.p_rowB_hi;
+        a.row_lo = fwd ? rAlo : rBlo;
+        a.row_hi = fwd ? rAhi : rBhi;
         a.p_eoff = d.p_eoff;
         a.p_poff = d.p_poff;
         a.p_doff = d.p_doff;
         a.Eidx = d.Eidx;
-        a.init_lo = star_rows ? d.p_rowA_lo : nullptr;
-        a.init_hi = star_rows ? d.p_rowA_hi : nullptr;
+        a.init_lo = star_rows ? rAlo : nullptr;
+        a.init_hi = star_rows ? rAhi : nullptr;
         const bool atomic = !star_rows;
         switch (li.cls) {
-        case 0: launch_list<S, 1>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
-        case 1: launch_list<S, 2>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
-        case 2: launch_list<S, 4>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
-        case 3: launch_list<S, 8>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
-        case 4: launch_list<S, 16>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
-        default: launch_list<S, 32>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st); break;
+        case 0: launch_list<S, 1>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st, rs); break;
+        case 1: launch_list<S, 2>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st, rs); break;
+        case 2: launch_list<S, 4>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st, rs); break;
+        case 3: launch_list<S, 8>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st, rs); break;
+        case 4: launch_list<S, 16>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st, rs); break;
+        default: launch_list<S, 32>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st, rs); break;
         }
         LAUNCHCHK();
     }
-    if (star_rows && !fwd) {
+    if (sl && !fwd) {
         subtrees();
         LAUNCHCHK();
     }
@@ -1993,7 +2007,7 @@ template <class S> struct StarRun {
         const DevPlan &d = fac->plan;
         const i64 nsu = (i64)fac->sym->splan->sunits.size();
         if (nsu > 0)
-            k_identity_panels<S><<<dim3((unsigned)nsu, PANEL_W), NT, 0, st>>>(X, n, d.sunits, d.p_c0, d.p_w,
+            k_identity_panels<S><<<dim3((unsigned)nsu, PANEL_W), NT, 0, st>>>(X, n, d.sunits, nullptr, n, d.p_c0, d.p_w,
                                                                             d.p_rowA_lo, d.p_rowA_hi, d.p_rowB_lo,
                                                                             d.p_rowB_hi);
         LAUNCHCHK();
@@ -2096,6 +2110,95 @@ template <class S> struct StarRun {
     }
 };
 
+// Rows of the star for sources: out[k + j ldo] = Y[pos[k], invp[j]] (Y m x n, leading dimension m); one workgroup per
+// output column j
+template <class T>
+__global__ __launch_bounds__(NT) void k_src_rows_out(const T *__restrict__ Y, i64 m, const int32_t *__restrict__ pos,
+                                                    i64 nsrc, const i64 *__restrict__ invp, T *__restrict__ out,
+                                                    i64 ldo) {
+    const i64 j = blockIdx.x;
+    const T *src = Y + invp[j] * m;
+    T *dst = out + j * ldo;
+    for (i64 k = threadIdx.x; k < nsrc; k += NT) dst[k] = src[pos[k]];
+}
+
+// Columns of the star for sources: out[i + k ldo] = Y[pos[k], invp[i]]; 32 x 32 tiles through LDS (reads down the
+// columns of Y, writes down the columns of out)
+template <class T>
+__global__ __launch_bounds__(NT) void k_src_cols_out(const T *__restrict__ Y, i64 m, const int32_t *__restrict__ pos,
+                                                    i64 nsrc, const i64 *__restrict__ invp, i64 n, T *__restrict__ out,
+                                                    i64 ldo) {
+    __shared__ T tile[32][33];
+    const i64 i0 = (i64)blockIdx.x * 32, k0 = (i64)blockIdx.y * 32;
+    const int tx = threadIdx.x % 32, ty = threadIdx.x / 32;   // 8 rows of 32
+    for (int r = ty; r < 32; r += 8) {
+        const i64 i = i0 + r, k = k0 + tx;
+        if (i < n && k < nsrc) tile[r][tx] = Y[pos[k] + invp[i] * m];
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8) {
+        const i64 k = k0 + r, i = i0 + tx;
+        if (i < n && k < nsrc) out[i + k * ldo] = tile[tx][r];
+    }
+}
+
+// Rows (cols = 0) or columns (cols = 1) of the star for a set of sources (the reference's sgetre!, chordal_slu.jl:
+// 445-493, for many sources at once): the sweep buffer Y has one row per source (sorted by elimination label); the
+// forward sweep visits, for each unit, only the sources in its subtree.  Rows run the star's units (blocks, subtrees,
+// panels) with X <- U* then X <- X L*; columns run the transposed panel sweeps (L^T forward, U^T backward), as lmul!.
+template <class S> struct StarSrcRun {
+    pp_ctx *ctx;
+    const pp_fac *fac;
+    const RowSub *R;
+    i64 nsrc;
+    int cols;
+    void *out;
+    i64 ldo;
+    std::string err;
+    void operator()() { err = run(); }
+    std::string run() {
+        typedef typename S::value_type T;
+        const i64 n = fac->sym->S.n, m = (i64)R->js.size();
+        hipStream_t st = ctx->stream;
+        if (n == 0 || m == 0) return "";
+        const SweepPlan &Wp = *fac->sym->splan;
+        const DevPlan &d = fac->plan;
+        T *Y = nullptr;
+        HIPCHK(hipMallocAsync((void **)&Y, m * n * sizeof(T), st));
+        timer_start(ctx, 4);
+        if (!cols) {
+            const i64 nsu = (i64)Wp.sunits.size();
+            if (nsu > 0)
+                k_identity_panels<S><<<dim3((unsigned)nsu, PANEL_W), NT, 0, st>>>(Y, m, d.sunits, R->d_js, n, d.p_c0, d.p_w,
+                                                                                R->d_rowA_lo, R->d_rowA_hi, R->d_rowB_lo,
+                                                                                R->d_rowB_hi);
+        } else if (Wp.np > 0) {
+            k_identity_panels<S><<<dim3((unsigned)Wp.np, PANEL_W), NT, 0, st>>>(Y, m, nullptr, R->d_js, n, d.p_c0, d.p_w,
+                                                                              R->d_rowA_lo, R->d_rowA_hi, R->d_rowB_lo,
+                                                                              R->d_rowB_hi);
+        }
+        LAUNCHCHK();
+        std::string e;
+        if (!cols) {
+            e = run_sweeps<S>(ctx, fac, true, 0, Y, m, true, m, fac->Upack, R, 1);
+            if (e.empty()) e = run_sweeps<S>(ctx, fac, false, 0, Y, m, true, m, fac->Lpack, R, 1);
+        } else {
+            e = run_sweeps<S>(ctx, fac, true, 1, Y, m, true, m, fac->Lpack, R, 0);
+            if (e.empty()) e = run_sweeps<S>(ctx, fac, false, 1, Y, m, true, m, fac->Upack, R, 0);
+        }
+        if (!e.empty()) return e;
+        if (!cols)
+            k_src_rows_out<T><<<(unsigned)n, NT, 0, st>>>(Y, m, R->d_pos, nsrc, d.invp, (T *)out, ldo);
+        else
+            k_src_cols_out<T><<<dim3((unsigned)((n + 31) / 32), (unsigned)((nsrc + 31) / 32)), NT, 0, st>>>(
+                Y, m, R->d_pos, nsrc, d.invp, n, (T *)out, ldo);
+        LAUNCHCHK();
+        timer_stop(ctx, 4);
+        HIPCHK(hipFreeAsync(Y, st));
+        return "";
+    }
+};
+
 template <class S> struct SolveRun {
     pp_ctx *ctx;
     const pp_fac *fac;
@@ -2187,6 +2290,12 @@ template <class S> std::string packs_impl(pp_ctx *ctx, pp_fac *fac) {
 }
 template <class S> std::string star_impl(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc, int host) {
     StarRun<S> r{ctx, fac, out, ldc, host};
+    r();
+    return r.err;
+}
+template <class S>
+std::string star_src_impl(pp_ctx *ctx, const pp_fac *fac, const RowSub &R, i64 nsrc, int cols, void *out, i64 ldo) {
+    StarSrcRun<S> r{ctx, fac, &R, nsrc, cols, out, ldo};
     r();
     return r.err;
 }

@@ -379,4 +379,59 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
     return "";
 }
 
+int32_t RowSub::map(int32_t r) const { return (int32_t)(std::lower_bound(js.begin(), js.end(), r) - js.begin()); }
+
+void build_row_subset(const SweepPlan &P, const Symbolic &S, RowSub &R) {
+    const i64 nu = (i64)P.front.size();
+    R.rowA_lo.resize(nu);
+    R.rowA_hi.resize(nu);
+    R.rowB_lo.resize(nu);
+    R.rowB_hi.resize(nu);
+    for (i64 p = 0; p < nu; p++) {
+        R.rowA_lo[p] = R.map(P.rowA_lo[p]);
+        R.rowA_hi[p] = R.map(P.rowA_hi[p]);
+        R.rowB_lo[p] = R.map(P.rowB_lo[p]);
+        R.rowB_hi[p] = R.map(P.rowB_hi[p]);
+    }
+    // the prefix arrays of every list, in the plan's layout (make_lists)
+    R.tiles = P.tiles;
+    auto tiles_of = [](i64 lo, i64 hi, i64 rows) { return hi > lo ? (hi - lo + rows - 1) / rows : 0; };
+    auto rowtiles = [](i64 lo, i64 hi, i64 bm) { return hi > lo ? (hi - lo / bm * bm + bm - 1) / bm : 0; };
+    auto redo = [&](const SweepPlan::List &li, bool fwd) {
+        auto prefix = [&](i64 off, auto units) {
+            int32_t acc = 0;
+            R.tiles[off] = 0;
+            for (i64 k = 0; k < li.cnt; k++) {
+                acc += (int32_t)units(P.plist[li.off + k]);
+                R.tiles[off + 1 + k] = acc;
+            }
+        };
+        prefix(li.pAu, [&](int32_t p) { return tiles_of(R.rowA_lo[p], R.rowA_hi[p], TILE_ROWS) * P.chunks[p]; });
+        prefix(li.pB64, [&](int32_t p) { return tiles_of(R.rowB_lo[p], R.rowB_hi[p], TILE_ROWS); });
+        if (li.cls >= BLK_CLS)
+            for (int q = 0; q < 2; q++) {
+                const i64 bm = 64 << q;
+                prefix(li.pT[q], [&](int32_t p) -> i64 {
+                    if (fwd) return P.e[p] > 0 ? rowtiles(R.rowA_lo[p], R.rowA_hi[p], bm) * ((P.e[p] + BLK_W - 1) / BLK_W) : 0;
+                    return rowtiles(R.rowB_lo[p], R.rowB_hi[p], bm);
+                });
+            }
+    };
+    for (const auto &li : P.fwd) redo(li, true);
+    for (const auto &li : P.bwd) redo(li, false);
+    for (const auto &li : P.sfwd) redo(li, true);
+    for (const auto &li : P.sbwd) redo(li, false);
+    // subtrees
+    const i64 nsub = (i64)P.sub_ptr.size() - 1;
+    R.sub_rows.resize(4 * std::max<i64>(nsub, 0));
+    R.sub_preF.assign(1, 0);
+    R.sub_preB.assign(1, 0);
+    for (i64 s = 0; s < nsub; s++) {
+        for (int k = 0; k < 4; k++) R.sub_rows[4 * s + k] = R.map(P.sub_rows[4 * s + k]);
+        R.sub_preF.push_back(R.sub_preF.back() + (int32_t)tiles_of(R.sub_rows[4 * s], R.sub_rows[4 * s + 1], TILE_ROWS));
+        R.sub_preB.push_back(R.sub_preB.back() + (int32_t)tiles_of(R.sub_rows[4 * s + 2], R.sub_rows[4 * s + 3], TILE_ROWS));
+    }
+    (void)S;
+}
+
 }  // namespace pp

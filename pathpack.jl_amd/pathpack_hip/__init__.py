@@ -30,7 +30,7 @@ from ._lib import (PathpackArgumentError, PathpackDeviceError, PathpackError, Pa
 
 __all__ = [
     "AbstractSemiring", "MinPlus", "MaxPlus", "MaxMin", "MinMax", "PlusProd", "OrAnd",
-    "szero", "sone", "mlu", "mstar", "lmul_", "rmul_", "Matrix", "Factorization", "Symbolic", "symbolic",
+    "szero", "sone", "mlu", "mstar", "lmul_", "rmul_", "Matrix", "star_rows", "star_cols", "Factorization", "Symbolic", "symbolic",
     "Context", "context", "DeviceArray", "PathpackError", "PathpackArgumentError", "PathpackMemoryError",
     "PathpackUnsupportedError", "PathpackDeviceError",
 ]
@@ -399,6 +399,37 @@ def Matrix(F: Factorization, device: bool = False, out=None):
 def mstar(s: AbstractSemiring, A, alg=None, amalgamate: bool = True, device: bool = False):
     """The star A* = I (+) A (+) A^2 (+) ... as a dense matrix (mstar, abstract_slu.jl:81-87)."""
     return Matrix(mlu(s, A, alg=alg, amalgamate=amalgamate), device=device)
+
+
+def _star_sources(F: Factorization, src, which: int, device: bool):
+    name = "star_rows" if which == 0 else "star_cols"
+    idx = np.ascontiguousarray(np.asarray(src, dtype=np.int64).reshape(-1))
+    if idx.size and (idx.min() < 0 or idx.max() >= F.n):
+        raise PathpackArgumentError(_lib.PP_EINVAL, f"{name}: source index out of range")
+    k, n = idx.size, F.n
+    shape = (k, n) if which == 0 else (n, k)
+    if device:
+        out = DeviceArray(shape, F.dtype, F.ctx)
+        if k and n:
+            F.ctx.check(lib().pp_star_sources(F.ctx.handle, F.handle, which, k, _p(idx), ctypes.c_void_p(out.ptr),
+                                              max(1, shape[0]), 1))
+        return out
+    out = np.empty(shape, dtype=F.dtype, order="F")
+    if k and n:
+        F.ctx.check(lib().pp_star_sources(F.ctx.handle, F.handle, which, k, _p(idx), _p(out), max(1, shape[0]), 0))
+    return out
+
+
+def star_rows(F: Factorization, src, device: bool = False):
+    """Rows src of A* (len(src) x n; row k is the least solution x of x = x A (+) e_src[k]^T), for many sources in
+    one pass: sgetre!(F, Val(:L), Val(:T), b, k) (chordal_slu.jl:445-493) over a batch of sources."""
+    return _star_sources(F, src, 0, device)
+
+
+def star_cols(F: Factorization, src, device: bool = False):
+    """Columns src of A* (n x len(src); column k is the least solution x of x = A x (+) e_src[k]), for many
+    sources in one pass: sgetre!(F, Val(:L), Val(:N), b, k) (chordal_slu.jl:445-493) over a batch of sources."""
+    return _star_sources(F, src, 1, device)
 
 
 def _solve(F: Factorization, B, left: bool):

@@ -8,8 +8,13 @@
 // launch writes, two writers of one element, and a read of an element nothing has initialised are reported.  The
 // relabelled result is compared with the oracle's star: bit for bit, or within 1e-4 relative error for PlusProd.
 //
-// usage: star_plan_emu graph.bin semiring dtype ncu   (graph.bin: n, nnz, colptr, rowval as int64, nzval)
-// exit status 0 when no error is reported and the star matches.
+// With a source modulus M > 0 the replay runs the rows of the star for a subset of sources instead (the source-row
+// path: the sweep buffer holds one row per source, and every unit's row ranges are those of the subset, as
+// build_row_subset maps them): the sources are the labels s with (s * 2654435761) mod 2^32 mod M == 0 (M = 1: all).
+//
+// usage: star_plan_emu graph.bin semiring dtype ncu [M]   (graph.bin: n, nnz, colptr, rowval as int64, nzval)
+// exit status 0 when no error is reported and the star (or its rows) matches.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -56,8 +61,24 @@ template <class T> struct Chk {
 template <class S> struct Emu {
     typedef typename S::value_type T;
     i64 n;
+    i64 m;                                     // rows of X (n, or the number of sources)
     Symbolic Sy;
     SweepPlan P;
+    // the rows of each unit and the launches' prefix arrays: the plan's, or the source subset's
+    std::vector<int32_t> rsrc;                 // row -> source label (empty: row i is label i)
+    const int32_t *rAlo = nullptr, *rAhi = nullptr, *rBlo = nullptr, *rBhi = nullptr;
+    const std::vector<int32_t> *TL = nullptr, *SR = nullptr, *SPF = nullptr, *SPB = nullptr;
+    void use_plan_rows() {
+        m = n;
+        rAlo = P.rowA_lo.data(); rAhi = P.rowA_hi.data(); rBlo = P.rowB_lo.data(); rBhi = P.rowB_hi.data();
+        TL = &P.tiles; SR = &P.sub_rows; SPF = &P.sub_preF; SPB = &P.sub_preB;
+    }
+    void use_subset(const RowSub &R) {
+        m = (i64)R.js.size();
+        rsrc = R.js;
+        rAlo = R.rowA_lo.data(); rAhi = R.rowA_hi.data(); rBlo = R.rowB_lo.data(); rBhi = R.rowB_hi.data();
+        TL = &R.tiles; SR = &R.sub_rows; SPF = &R.sub_preF; SPB = &R.sub_preB;
+    }
     std::vector<T> LD, LL, UL;                 // device layout
     std::vector<T> Bpack, Hpack, stars;
     std::vector<T> X, X0;                      // X0: snapshot before a launch
@@ -87,11 +108,11 @@ template <class S> struct Emu {
 
     // X access with launch semantics
     T rd(i64 r, i64 c, bool used) {
-        if (r < 0 || r >= n || c < 0 || c >= n) {
+        if (r < 0 || r >= m || c < 0 || c >= n) {
             FAIL("OOB X read (%lld, %lld)", (long long)r, (long long)c);
             return S::zero();
         }
-        i64 idx = r + c * n;
+        i64 idx = r + c * m;
         if (phase == 2 && used) {
             if (wtask[idx] >= 0 && wtask[idx] != cur) FAIL("race: task %d reads (%lld,%lld) written by task %d", cur, (long long)r, (long long)c, wtask[idx]);
             if (!init[idx]) FAIL("read of uninitialised X(%lld, %lld) by task %d", (long long)r, (long long)c, cur);
@@ -99,11 +120,11 @@ template <class S> struct Emu {
         return live ? X[idx] : X0[idx];
     }
     void wr(i64 r, i64 c, T v) {
-        if (r < 0 || r >= n || c < 0 || c >= n) {
+        if (r < 0 || r >= m || c < 0 || c >= n) {
             FAIL("OOB X write (%lld, %lld)", (long long)r, (long long)c);
             return;
         }
-        i64 idx = r + c * n;
+        i64 idx = r + c * m;
         if (phase == 1) {
             if (wtask[idx] >= 0 && wtask[idx] != cur) FAIL("race: two writers of (%lld,%lld): %d, %d", (long long)r, (long long)c, wtask[idx], cur);
             wtask[idx] = cur;
@@ -175,9 +196,13 @@ template <class S> struct Emu {
         for (int32_t p : P.sunits) {
             for (int j = 0; j < P.w[p]; j++) {
                 i64 col = P.c0[p] + j;
-                for (i64 i = P.rowA_lo[p]; i < P.rowA_hi[p]; i++) { X[i + col * n] = i == col ? S::one() : S::zero(); init[i + col * n] = 1; }
-                for (i64 i = 0; i < P.rowB_lo[p]; i++) { X[i + col * n] = S::zero(); init[i + col * n] = 1; }
-                for (i64 i = P.rowB_hi[p]; i < n; i++) { X[i + col * n] = S::zero(); init[i + col * n] = 1; }
+                for (i64 i = rAlo[p]; i < rAhi[p]; i++) {
+                    const i64 src = rsrc.empty() ? i : rsrc[i];
+                    X[i + col * m] = src == col ? S::one() : S::zero();
+                    init[i + col * m] = 1;
+                }
+                for (i64 i = 0; i < rBlo[p]; i++) { X[i + col * m] = S::zero(); init[i + col * m] = 1; }
+                for (i64 i = rBhi[p]; i < m; i++) { X[i + col * m] = S::zero(); init[i + col * m] = 1; }
             }
         }
     }
@@ -196,8 +221,8 @@ template <class S> struct Emu {
     void panel_fwd(int p, int task0) {
         int f = P.front[p], w = P.w[p], e = P.e[p], c0 = P.c0[p], lj0 = c0 - (int)Sy.Rptr[f], lo = P.lo_ext[p];
         i64 eo = P.eoff[p];
-        for (i64 r = P.rowA_lo[p]; r < P.rowA_hi[p]; r++) {
-            cur = task0 + (int)((r - P.rowA_lo[p]) / 64);
+        for (i64 r = rAlo[p]; r < rAhi[p]; r++) {
+            cur = task0 + (int)((r - rAlo[p]) / 64);
             std::vector<T> x(w);
             for (int j = 0; j < w; j++) x[j] = rd(r, c0 + j, true);
             for (int j = 0; j < w; j++) {
@@ -217,10 +242,10 @@ template <class S> struct Emu {
     void panel_bwd(int p, int task0) {
         int f = P.front[p], w = P.w[p], e = P.e[p], c0 = P.c0[p], lj0 = c0 - (int)Sy.Rptr[f], lo = P.lo_ext[p];
         i64 eo = P.eoff[p];
-        for (i64 r = P.rowB_lo[p]; r < P.rowB_hi[p]; r++) {
-            cur = task0 + (int)((r - P.rowB_lo[p]) / 64);
+        for (i64 r = rBlo[p]; r < rBhi[p]; r++) {
+            cur = task0 + (int)((r - rBlo[p]) / 64);
             std::vector<T> acc(w, S::zero());
-            if (r >= P.rowA_lo[p] && r < P.rowA_hi[p]) {
+            if (r >= rAlo[p] && r < rAhi[p]) {
                 for (int j = 0; j < w; j++) acc[j] = rd(r, c0 + j, true);
                 for (int j = 0; j < w; j++) {
                     T s = acc[j];
@@ -244,10 +269,10 @@ template <class S> struct Emu {
 
     // block launch (k_blk semantics)
     void blocks(const SweepPlan::List &li, bool fwd) {
-        const int q = sizeof(T) == 4 && P.tiles[li.pT[1] + li.cnt] >= 2 * ncu ? 1 : 0;
+        const int q = sizeof(T) == 4 && (*TL)[li.pT[1] + li.cnt] >= 2 * ncu ? 1 : 0;
         const int TM = q ? 8 : 4, TN = fwd || li.cls == BLK_CLS ? 8 : 4;
         const int BM = 16 * TM, BN = 16 * TN, BK = (!fwd && TN == 4) ? 32 : 16;
-        const int32_t *pre = &P.tiles[li.pT[q]];
+        const int32_t *pre = &(*TL)[li.pT[q]];
         const int32_t *ulist = &P.plist[li.off];
         int nu = (int)li.cnt, ntask = pre[nu];
         int grid = (ntask + 7) / 8 * 8, per = grid / 8;
@@ -263,13 +288,13 @@ template <class S> struct Emu {
             if (!fwd && P.b_bn[b] != BN) FAIL("block of tile width %d in a list of %d", P.b_bn[b], BN);
             int c0 = P.c0[id], w = P.w[id], e = P.e[id];
             i64 eo = P.eoff[id];
-            int lo = fwd ? P.rowA_lo[id] : P.rowB_lo[id], hi = fwd ? P.rowA_hi[id] : P.rowB_hi[id];
+            int lo = fwd ? rAlo[id] : rBlo[id], hi = fwd ? rAhi[id] : rBhi[id];
             int rt = u, ct = 0;
             if (fwd) { int nct = (e + BN - 1) / BN; if (nct == 0) { FAIL("fwd task with e = 0"); continue; } rt = u / nct; ct = u - rt * nct; }
             i64 r0 = (i64)(lo / BM) * BM + (i64)rt * BM;
             if (r0 >= hi) FAIL("tile beyond its rows");
             int K = fwd ? w : w + e;
-            int olo = fwd ? 0 : P.rowA_lo[id], ohi = fwd ? 0 : P.rowA_hi[id];
+            int olo = fwd ? 0 : rAlo[id], ohi = fwd ? 0 : rAhi[id];
             i64 boff = fwd ? P.b_hoff[b] + (i64)ct * BN : P.b_boff[b];
             i64 ldb = fwd ? P.b_ep[b] : BN;
             i64 plo = fwd ? P.b_hoff[b] : P.b_boff[b];
@@ -277,7 +302,7 @@ template <class S> struct Emu {
             const std::vector<T> &Pk = fwd ? Hpack : Bpack;
             bool own = fwd || (r0 < ohi && r0 + BM > olo);
             int kbeg = own ? 0 : (w / BK) * BK, kend = (K + BK - 1) / BK * BK;
-            bool vec = r0 + BM <= n && n % (16 / (int)sizeof(T)) == 0;
+            bool vec = r0 + BM <= m && m % (16 / (int)sizeof(T)) == 0;
             auto colA = [&](int k) -> i64 {
                 if (fwd) return c0 + std::min(k, w - 1);
                 if (k < w) return c0 + k;
@@ -293,7 +318,7 @@ template <class S> struct Emu {
             for (int rr = 0; rr < BM; rr++) {
                 i64 r = r0 + rr;
                 bool stored = r >= lo && r < hi;
-                if (!vec && r >= n) continue;   // not loaded (zero)
+                if (!vec && r >= m) continue;   // not loaded (zero)
                 for (int c = 0; c < BN; c++) {
                     T acc = S::zero();
                     if (fwd) {
@@ -331,7 +356,7 @@ template <class S> struct Emu {
     void subtrees(bool fwd) {
         const i64 nsub = (i64)P.sub_ptr.size() - 1;
         if (nsub <= 0) return;
-        const std::vector<int32_t> &pre = fwd ? P.sub_preF : P.sub_preB;
+        const std::vector<int32_t> &pre = fwd ? *SPF : *SPB;
         X0 = X;
         std::fill(wtask.begin(), wtask.end(), -1);
         live = true;
@@ -340,15 +365,15 @@ template <class S> struct Emu {
                 cur = task;
                 const int s = search(pre.data(), (int)nsub, task);
                 const int tile = task - pre[s];
-                const int lo = P.sub_rows[4 * s + (fwd ? 0 : 2)], hi = P.sub_rows[4 * s + (fwd ? 1 : 3)];
+                const int lo = (*SR)[4 * s + (fwd ? 0 : 2)], hi = (*SR)[4 * s + (fwd ? 1 : 3)];
                 const int k0 = P.sub_ptr[s], k1 = P.sub_ptr[s + 1];
                 for (int lane = 0; lane < 64; lane++) {
                     const i64 r = (i64)lo + (i64)tile * 64 + lane;
                     for (int kk = 0; kk < k1 - k0; kk++) {
                         const int p = P.sub_pan[fwd ? k0 + kk : k1 - 1 - kk];
-                        const int plo = fwd ? P.rowA_lo[p] : lo, phi = fwd ? P.rowA_hi[p] : hi;
+                        const int plo = fwd ? rAlo[p] : lo, phi = fwd ? rAhi[p] : hi;
                         const i64 t0 = (i64)lo + (i64)tile * 64;
-                        if (t0 >= phi || t0 + 64 <= plo) continue;
+                        if (plo >= phi || t0 >= phi || t0 + 64 <= plo) continue;
                         const bool store = r >= plo && r < phi;
                         const i64 rr = r < plo ? plo : (r >= phi ? phi - 1 : r);
                         int f = P.front[p], w = P.w[p], e = P.e[p], c0 = P.c0[p], lj0 = c0 - (int)Sy.Rptr[f], lo_ = P.lo_ext[p];
@@ -370,7 +395,7 @@ template <class S> struct Emu {
                             }
                         } else {
                             std::vector<T> acc(w, S::zero());
-                            if (rr >= P.rowA_lo[p] && rr < P.rowA_hi[p]) {
+                            if (rr >= rAlo[p] && rr < rAhi[p]) {
                                 for (int j = 0; j < w; j++) acc[j] = rd(rr, c0 + j, store);
                                 for (int j = 0; j < w; j++) {
                                     T sv = acc[j];
@@ -420,7 +445,7 @@ template <class S> struct Emu {
     }
 };
 
-template <class S> int run(const char *path, int sr, int dt, int ncu) {
+template <class S> int run(const char *path, int sr, int dt, int ncu, long mod) {
     typedef typename S::value_type T;
     FILE *fp = fopen(path, "rb");
     if (!fp) return 2;
@@ -461,23 +486,50 @@ template <class S> int run(const char *path, int sr, int dt, int ncu) {
            (long long)E.P.np, (long long)E.P.nb, E.P.sfwd.size(), E.P.sbwd.size(), (long long)E.P.nbpack,
            (long long)E.P.nhpack, E.P.sub_ptr.size() - 1, E.P.sub_pan.size());
     E.packs();
-    E.X.assign(n * n, S::zero());
-    E.init.assign(n * n, 0);
-    E.wtask.assign(n * n, -1);
+    E.use_plan_rows();
+    RowSub R;
+    std::vector<i64> srcs;   // requested sources, original labels
+    if (mod > 0) {
+        for (i64 s = 0; s < n; s++)
+            if ((uint32_t)((uint64_t)s * 2654435761ull) % (uint64_t)mod == 0) srcs.push_back(s);
+        for (i64 s : srcs) R.js.push_back((int32_t)Sy.invp[s]);
+        std::sort(R.js.begin(), R.js.end());
+        build_row_subset(E.P, Sy, R);
+        E.use_subset(R);
+        printf("sources %zu\n", srcs.size());
+    }
+    const i64 m = E.m;
+    E.X.assign(m * n, S::zero());
+    E.init.assign(m * n, 0);
+    E.wtask.assign(m * n, -1);
     E.identity();
     E.subtrees(true);
     for (auto &li : E.P.sfwd) E.run_list(li, true);
     for (auto &li : E.P.sbwd) E.run_list(li, false);
     E.subtrees(false);
     std::vector<T> C(n * n), Co(n * n);
-    for (i64 j = 0; j < n; j++)
-        for (i64 i = 0; i < n; i++) C[i + j * n] = E.X[Sy.invp[i] + Sy.invp[j] * n];
+    if (mod <= 0)
+        for (i64 j = 0; j < n; j++)
+            for (i64 i = 0; i < n; i++) C[i + j * n] = E.X[Sy.invp[i] + Sy.invp[j] * n];
     rc = ppo_star(sr, dt, n, Sy.nf, Sy.Rptr.data(), Sy.Sptr.data(), Sy.Stgt.data(), Sy.perm.data(), LDo.data(), UDo.data(),
                   LLo.data(), ULo.data(), Co.data(), 0, n, 1, 8);
     if (rc) { fprintf(stderr, "oracle star %d\n", rc); return 4; }
+    // the entries compared: all of the star, or the rows of the sources (row k of X is source js[k])
+    std::vector<i64> qs;
+    if (mod > 0) {
+        C.assign(n * n, S::zero());
+        for (i64 s : srcs) {
+            const i64 k = R.map((int32_t)Sy.invp[s]);
+            for (i64 j = 0; j < n; j++) {
+                C[s + j * n] = E.X[k + Sy.invp[j] * m];
+                qs.push_back(s + j * n);
+            }
+        }
+    } else
+        for (i64 q = 0; q < n * n; q++) qs.push_back(q);
     long ndiff = 0;
     double maxrel = 0;
-    for (i64 q = 0; q < n * n; q++) {
+    for (i64 q : qs) {
         T a = C[q], b = Co[q];
         if (sr == S_PLUSPROD) {
             double d = std::fabs((double)a - (double)b) / std::max(1e-300, std::fabs((double)b));
@@ -499,26 +551,27 @@ template <class S> int run(const char *path, int sr, int dt, int ncu) {
 }
 
 int main(int argc, char **argv) {
-    if (argc < 5) { fprintf(stderr, "usage: star_plan_emu graph.bin semiring dtype ncu\n"); return 2; }
+    if (argc < 5) { fprintf(stderr, "usage: star_plan_emu graph.bin semiring dtype ncu [M]\n"); return 2; }
     int sr = atoi(argv[2]), dt = atoi(argv[3]), ncu = atoi(argv[4]);
+    long mod = argc > 5 ? atol(argv[5]) : 0;
     if (dt == D_F32) {
         switch (sr) {
-        case S_MINPLUS: return run<MinPlus<float>>(argv[1], sr, dt, ncu);
-        case S_MAXPLUS: return run<MaxPlus<float>>(argv[1], sr, dt, ncu);
-        case S_MAXMIN: return run<MaxMin<float>>(argv[1], sr, dt, ncu);
-        case S_MINMAX: return run<MinMax<float>>(argv[1], sr, dt, ncu);
-        case S_PLUSPROD: return run<PlusProd<float>>(argv[1], sr, dt, ncu);
+        case S_MINPLUS: return run<MinPlus<float>>(argv[1], sr, dt, ncu, mod);
+        case S_MAXPLUS: return run<MaxPlus<float>>(argv[1], sr, dt, ncu, mod);
+        case S_MAXMIN: return run<MaxMin<float>>(argv[1], sr, dt, ncu, mod);
+        case S_MINMAX: return run<MinMax<float>>(argv[1], sr, dt, ncu, mod);
+        case S_PLUSPROD: return run<PlusProd<float>>(argv[1], sr, dt, ncu, mod);
         }
     } else if (dt == D_F64) {
         switch (sr) {
-        case S_MINPLUS: return run<MinPlus<double>>(argv[1], sr, dt, ncu);
-        case S_MAXPLUS: return run<MaxPlus<double>>(argv[1], sr, dt, ncu);
-        case S_MAXMIN: return run<MaxMin<double>>(argv[1], sr, dt, ncu);
-        case S_MINMAX: return run<MinMax<double>>(argv[1], sr, dt, ncu);
-        case S_PLUSPROD: return run<PlusProd<double>>(argv[1], sr, dt, ncu);
+        case S_MINPLUS: return run<MinPlus<double>>(argv[1], sr, dt, ncu, mod);
+        case S_MAXPLUS: return run<MaxPlus<double>>(argv[1], sr, dt, ncu, mod);
+        case S_MAXMIN: return run<MaxMin<double>>(argv[1], sr, dt, ncu, mod);
+        case S_MINMAX: return run<MinMax<double>>(argv[1], sr, dt, ncu, mod);
+        case S_PLUSPROD: return run<PlusProd<double>>(argv[1], sr, dt, ncu, mod);
         }
     } else if (dt == D_I32) {
-        return run<OrAnd>(argv[1], sr, dt, ncu);
+        return run<OrAnd>(argv[1], sr, dt, ncu, mod);
     }
     return 2;
 }

@@ -270,3 +270,50 @@ def test_star_to_host_in_chunks(ld_pad):
     assert np.array_equal(bits(C[:n, :]), bits(D))
     assert np.all(C[n:, :] == -1.0)
     assert np.array_equal(bits(D), bits(O.star(O.factor(O.MINPLUS, oracle_sym(F.sym), g.colptr, g.rowval, g.nzval))))
+
+
+SOURCE_CASES = [("components", O.MINPLUS, np.float32), ("components", O.PLUSPROD, np.float64),
+                ("components", O.ORAND, np.float32), ("rgg700", O.MAXPLUS, np.float64),
+                ("rgg700", O.MINMAX, np.float32), ("grid15x13x11", O.MINPLUS, np.float64),
+                ("grid15x13x11", O.MAXMIN, np.float32), ("grid15x13x11", O.PLUSPROD, np.float64)]
+
+
+@pytest.mark.parametrize("name,s,fdtype", SOURCE_CASES)
+def test_star_rows_and_cols_match_oracle(name, s, fdtype):
+    """Rows and columns of A* for batches of sources (sgetre!, chordal_slu.jl:445-493, over many sources): single
+    sources at both ends of the labels, a random subset, repeats in random order, every source reversed, and a
+    modulus-selected subset; against the rows / columns of the oracle's full star."""
+    dtype = dtype_for(s, fdtype)
+    g0 = BLOCK_GRAPHS[name]() if name in BLOCK_GRAPHS else graphs()[name]
+    g = weighted(g0, s, dtype)
+    n = g.n
+    print(f"case {name} s={s} dtype={np.dtype(dtype)} n={n}", flush=True)
+    sym, F, Fo = both(g, s, dtype)
+    Co = O.star(Fo)
+    rtol = rtol_for(s, dtype) * (10 if np.dtype(dtype) == np.float64 else 1)
+    rng = np.random.default_rng(7)
+    sets = {"first": np.array([0]), "last": np.array([n - 1]),
+            "subset": rng.choice(n, size=min(n, 37), replace=False),
+            "repeats": rng.integers(0, n, size=50), "all-reversed": np.arange(n)[::-1].copy(),
+            "mod17": np.arange(n)[(np.arange(n) * 2654435761 % 2**32) % 17 == 0]}
+    for label, src in sets.items():
+        print(f"  sources {label} ({len(src)})", flush=True)
+        Rw = P.star_rows(F, src)
+        assert Rw.shape == (len(src), n)
+        assert_star_equal(s, Rw, Co[src, :], rtol=rtol)
+        Cl = P.star_cols(F, src)
+        assert Cl.shape == (n, len(src))
+        assert_star_equal(s, Cl, Co[:, src], rtol=rtol)
+
+
+def test_star_sources_device_output_and_errors():
+    g = weighted(graphs()["rgg700"], O.MINPLUS, np.float32)
+    F = P.mlu(SEMIRINGS[O.MINPLUS], g)
+    src = np.array([5, 3, 699, 3, 0])
+    assert np.array_equal(bits(P.star_rows(F, src, device=True).numpy()), bits(P.star_rows(F, src)))
+    assert np.array_equal(bits(P.star_cols(F, src, device=True).numpy()), bits(P.star_cols(F, src)))
+    assert P.star_rows(F, np.zeros(0, np.int64)).shape == (0, g.n)
+    with pytest.raises(P.PathpackArgumentError):
+        P.star_rows(F, [g.n])
+    with pytest.raises(P.PathpackArgumentError):
+        P.star_cols(F, [-1])

@@ -3,7 +3,8 @@ kernels' index arithmetic launch by launch, bounds / race / initialisation check
 
 The replay is built with hipcc as host code (it includes the plan headers) and linked with the oracle library; it is
 skipped where hipcc is absent.  Graphs are chosen so that large fronts cut into 128- and 64-column blocks, blocks are
-followed by panels, small subtrees form, n is odd (guarded row loads) and the graph has several components.
+followed by panels, small subtrees form, n is odd (guarded row loads) and the graph has several components.  The source-row path (rows of the star for a
+subset of sources, each unit's rows mapped into the subset) is replayed the same way.
 """
 
 import os
@@ -74,3 +75,30 @@ def test_star_schedule_replay(emu, tmp_path, name, s, fdtype):
     for ncu in ([1, 1 << 20] if s == O.MINPLUS and np.dtype(dtype).itemsize == 4 else [1]):
         r = subprocess.run([emu, str(path), str(s), str(dcode), str(ncu)], capture_output=True, text=True, timeout=300)
         assert r.returncode == 0, f"ncu={ncu}: {r.stdout[-500:]} {r.stderr[-2000:]}"
+
+
+def _write(g, dtype, path):
+    with open(path, "wb") as f:
+        np.array([g.n, len(g.rowval)], np.int64).tofile(f)
+        np.asarray(g.colptr, np.int64).tofile(f)
+        np.asarray(g.rowval, np.int64).tofile(f)
+        np.asarray(g.nzval, dtype).tofile(f)
+
+
+SOURCE_CASES = [("grid15x13x11", O.MINPLUS, np.float32), ("components", O.MINPLUS, np.float64),
+                ("components", O.PLUSPROD, np.float64), ("grid9x9x9", O.MAXMIN, np.float32)]
+
+
+@pytest.mark.parametrize("name,s,fdtype", SOURCE_CASES)
+def test_source_rows_schedule_replay(emu, tmp_path, name, s, fdtype):
+    """Rows of the star for sources s with hash(s) mod M == 0: M = 1 (every source, the subset map is the
+    identity), 3, 17 and a modulus that leaves a handful of sources."""
+    dtype = dtype_for(s, fdtype)
+    g = weighted(GRAPHS[name](), s, dtype)
+    path = tmp_path / "graph.bin"
+    _write(g, dtype, path)
+    dcode = {np.dtype(np.float32): 0, np.dtype(np.float64): 1, np.dtype(np.int32): 2}[np.dtype(dtype)]
+    for mod in (1, 3, 17, max(2, g.n // 4)):
+        r = subprocess.run([emu, str(path), str(s), str(dcode), "1", str(mod)], capture_output=True, text=True,
+                           timeout=300)
+        assert r.returncode == 0, f"M={mod}: {r.stdout[-500:]} {r.stderr[-2000:]}"
