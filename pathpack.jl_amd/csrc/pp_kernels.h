@@ -1074,7 +1074,8 @@ __device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64
 // One wave per (subtree, 64-row tile): forward over the subtree's rows in postorder, or backward over the
 // component's rows in reverse postorder.  Every value a panel reads on row r was last written by this lane.
 template <class S, bool FWD>
-__global__ __launch_bounds__(64) void k_sub(typename S::value_type *__restrict__ X, i64 ld, SubArgs a,
+// (backward: at least 6 waves per SIMD, at the cost of a few spilled registers; the gathers need the occupancy)
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FWD ? 1 : 6))) void k_sub(typename S::value_type *__restrict__ X, i64 ld, SubArgs a,
                                             const typename S::value_type *__restrict__ Dpack,
                                             const typename S::value_type *__restrict__ Pk) {
     const int task = blockIdx.x;
@@ -1357,11 +1358,44 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
         return k < w ? c0 + k : (k < K ? E[k - w] : c0);
     };
     T ra[AQ * VW], rb[BQ * VW];
+    // backward: the extension indices of the A columns of the next step to load.  A wave's lanes of load q cover
+    // ND consecutive k (wave-uniform), so the indices are scalar loads (from clamped, always valid positions),
+    // issued a step ahead; each lane picks its own at the load.  No gathered load waits on a vector index load.
+    constexpr int ND = 64 * VW / BM;
+    static_assert(ND >= 1 && (64 * VW) % BM == 0, "a wave's loads cover whole k");
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int dl = (tid & 63) * VW / BM;
+    int32_t craw[AQ][ND];
+    auto cols = [&](int k0) {
+        if constexpr (!FWD) {
+#pragma unroll
+            for (int q = 0; q < AQ; q++) {
+                const int kl = k0 + (64 * wv + 256 * q) * VW / BM - w;
+#pragma unroll
+                for (int d = 0; d < ND; d++) craw[q][d] = E[min(max(kl + d, 0), max(e - 1, 0))];
+            }
+        }
+    };
+    auto pick = [&](int q) {
+        int32_t v = craw[q][0];
+#pragma unroll
+        for (int d = 1; d < ND; d++) v = dl == d ? craw[q][d] : v;
+        return v;
+    };
     auto gload = [&](int k0) {
+        const T *srcs[AQ];   // every address first: a load issued before an index is used would be waited for
 #pragma unroll
         for (int q = 0; q < AQ; q++) {
-            const int ev = (tid + 256 * q) * VW, r = ev % BM, kk = ev / BM, k = k0 + kk;
-            const T *src = X + (r0 + r) + colA(k) * ld;
+            const int ev = (tid + 256 * q) * VW, r = ev % BM, k = k0 + ev / BM;
+            i64 col;
+            if constexpr (FWD) col = c0 + min(k, w - 1);
+            else col = k < w ? c0 + k : (k < K ? pick(q) : c0);
+            srcs[q] = X + (r0 + r) + col * ld;
+        }
+#pragma unroll
+        for (int q = 0; q < AQ; q++) {
+            const int r = (tid + 256 * q) * VW % BM;
+            const T *src = srcs[q];
             if (vec) {
                 const V v = *reinterpret_cast<const V *>(src);
 #pragma unroll
@@ -1369,13 +1403,6 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
             } else {
 #pragma unroll
                 for (int t = 0; t < VW; t++) ra[q * VW + t] = r0 + r + t < a.nrows ? src[t] : S::zero();
-            }
-            if (!FWD && k < w) {
-#pragma unroll
-                for (int t = 0; t < VW; t++) {
-                    const i64 rr = r0 + r + t;
-                    if (rr < olo || rr >= ohi) ra[q * VW + t] = S::zero();
-                }
             }
         }
 #pragma unroll
@@ -1386,13 +1413,22 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
             for (int t = 0; t < VW; t++) rb[q * VW + t] = v[t];
         }
     };
-    auto sstore = [&](int buf) {
+    // the loaded step k0 into LDS buffer buf; the backward's own columns (k < w) are zero outside the rows
+    // [olo, ohi), applied here rather than at the load so that nothing waits on the load before the step's math
+    auto sstore = [&](int buf, int k0) {
 #pragma unroll
         for (int q = 0; q < AQ; q++) {
             const int ev = (tid + 256 * q) * VW;
             V v;
 #pragma unroll
             for (int t = 0; t < VW; t++) v[t] = ra[q * VW + t];
+            if (!FWD && k0 + ev / BM < w) {
+#pragma unroll
+                for (int t = 0; t < VW; t++) {
+                    const i64 rr = r0 + ev % BM + t;
+                    if (rr < olo || rr >= ohi) v[t] = S::zero();
+                }
+            }
             *reinterpret_cast<V *>(&As[buf][ev / BM][ev % BM]) = v;
         }
 #pragma unroll
@@ -1444,15 +1480,17 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
         }
     }
     if (kbeg < kend) {
+        cols(kbeg);
         gload(kbeg);
-        sstore(0);
+        if (kbeg + BK < kend) cols(kbeg + BK);
+        sstore(0, kbeg);
     }
     __syncthreads();
     int buf = 0;
     for (int k0 = kbeg; k0 < kend; k0 += BK) {
         const bool more = k0 + BK < kend;
         if (more) gload(k0 + BK);
-#pragma unroll 1
+#pragma unroll 2
         for (int kk = 0; kk < BK; kk += 2) {
             T a0[TM], a1[TM], b0[TN], b1[TN];
 #pragma unroll
@@ -1470,7 +1508,8 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
 #pragma unroll
                 for (int j = 0; j < TN; j++) acc[i][j] = S::muladd2(a0[i], b0[j], a1[i], b1[j], acc[i][j]);
         }
-        if (more) sstore(buf ^ 1);
+        if (k0 + 2 * BK < kend) cols(k0 + 2 * BK);
+        if (more) sstore(buf ^ 1, k0 + BK);
         __syncthreads();
         buf ^= 1;
     }
@@ -1844,9 +1883,8 @@ static void launch_blk(pp_ctx *ctx, bool fwd, typename S::value_type *X, i64 ld,
                        const void *Bp) {
     typedef typename S::value_type T;
     const unsigned grid = (unsigned)((a.ntask + 7) / 8 * 8);
-    constexpr int BK = TN == 4 ? 32 : 16;   // a 64-column tile takes twice the k per step (latency hiding)
     if (fwd) k_blk<S, TM, 8, 16, true><<<grid, 256, 0, ctx->stream>>>(X, ld, a, (const T *)Hp);
-    else k_blk<S, TM, TN, BK, false><<<grid, 256, 0, ctx->stream>>>(X, ld, a, (const T *)Bp);
+    else k_blk<S, TM, TN, 16, false><<<grid, 256, 0, ctx->stream>>>(X, ld, a, (const T *)Bp);
 }
 
 template <class S>

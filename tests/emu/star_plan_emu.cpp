@@ -271,7 +271,7 @@ template <class S> struct Emu {
     void blocks(const SweepPlan::List &li, bool fwd) {
         const int q = sizeof(T) == 4 && (*TL)[li.pT[1] + li.cnt] >= 2 * ncu ? 1 : 0;
         const int TM = q ? 8 : 4, TN = fwd || li.cls == BLK_CLS ? 8 : 4;
-        const int BM = 16 * TM, BN = 16 * TN, BK = (!fwd && TN == 4) ? 32 : 16;
+        const int BM = 16 * TM, BN = 16 * TN, BK = 16;
         const int32_t *pre = &(*TL)[li.pT[q]];
         const int32_t *ulist = &P.plist[li.off];
         int nu = (int)li.cnt, ntask = pre[nu];
