@@ -107,6 +107,18 @@ void pool_run(int n, const std::function<void(int)> &fn) {
 
 namespace {
 
+double now() {
+    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+// PP_SYMTIME=1 prints the time of each stage of the analysis to stderr
+void stage(const char *name, double &t) {
+    static const bool on = std::getenv("PP_SYMTIME") != nullptr;
+    const double t1 = now();
+    if (on) std::fprintf(stderr, "pp_symbolic: %-28s %8.2f ms\n", name, (t1 - t) * 1e3);
+    t = t1;
+}
+
 struct Adj {
     i64 n = 0;
     std::vector<i64> xadj;
@@ -447,6 +459,7 @@ struct ND {
 void etree_postorder(const Adj &G, const std::vector<i64> &perm, std::vector<i64> &post_perm,
                      std::vector<i64> &post_parent) {
     const i64 n = G.n;
+    double ts = now();
     std::vector<i64> invp(n);
     for (i64 k = 0; k < n; k++) invp[perm[k]] = k;
     std::vector<i64> parent(n, -1), anc(n, -1);
@@ -467,6 +480,7 @@ void etree_postorder(const Adj &G, const std::vector<i64> &perm, std::vector<i64
             }
         }
     }
+    stage("    etree", ts);
     // children lists in increasing order, then an iterative DFS from the roots
     std::vector<i64> head(n, -1), next(n, -1);
     for (i64 j = n - 1; j >= 0; j--)
@@ -497,6 +511,7 @@ void etree_postorder(const Adj &G, const std::vector<i64> &perm, std::vector<i64
     post_parent.assign(n, -1);
     for (i64 j = 0; j < n; j++)
         if (parent[j] >= 0) post_parent[post[j]] = post[parent[j]];
+    stage("    postorder", ts);
 }
 
 // ===== column counts of L (Gilbert, Ng & Peyton, "An efficient algorithm to compute row and column counts for
@@ -510,6 +525,7 @@ void etree_postorder(const Adj &G, const std::vector<i64> &perm, std::vector<i64
 // these weights over the subtree of j.  O(nnz(A) a(n)).
 void column_counts(const Adj &G, const std::vector<i64> &perm, const std::vector<i64> &parent, std::vector<i64> &cc) {
     const i64 n = G.n;
+    double ts = now();
     std::vector<i64> invp(n);
     for (i64 k = 0; k < n; k++) invp[perm[k]] = k;
     // first descendant of every node (labels are a postorder, so a subtree is the range [first[j], j])
@@ -548,6 +564,7 @@ void column_counts(const Adj &G, const std::vector<i64> &perm, const std::vector
     cc = delta;
     for (i64 j = 0; j < n; j++)
         if (parent[j] != -1) cc[parent[j]] += cc[j];
+    stage("    column counts", ts);
 }
 
 // ===== supernodal symbolic factorization for (perm, Rptr) =====
@@ -714,17 +731,7 @@ std::string supernodal_tree(const Adj &G, const std::vector<i64> &perm, const st
     return "";
 }
 
-double now() {
-    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
-}
 
-// PP_SYMTIME=1 prints the time of each stage of the analysis to stderr
-void stage(const char *name, double &t) {
-    static const bool on = std::getenv("PP_SYMTIME") != nullptr;
-    const double t1 = now();
-    if (on) std::fprintf(stderr, "pp_symbolic: %-28s %8.2f ms\n", name, (t1 - t) * 1e3);
-    t = t1;
-}
 
 // Work counts of a structure (the formulas of the reference's per-front costs): factor sum nn^3/3 + nn^2 na +
 // nn na^2; star n * sum nn (na + (nn-1)/2) for X <- X L* plus sum |subtree(f)| nn (na + (nn-1)/2) for X <- U*;
@@ -787,6 +794,7 @@ std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, st
     out.entry_front.resize(nnz);
     out.entry_row.resize(nnz);
     out.entry_col.resize(nnz);
+    stage("    entry arrays", ts);
     std::vector<i32> fof(n);
     for (i64 f = 0; f < nf; f++)
         for (i64 v = out.Rptr[f]; v < out.Rptr[f + 1]; v++) fof[v] = (i32)f;
@@ -800,6 +808,7 @@ std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, st
             eptr[f + 1]++;
         }
     }
+    stage("    entry fronts", ts);
     for (i64 f = 0; f < nf; f++) eptr[f + 1] += eptr[f];
     {
         std::vector<i64> pos(eptr.begin(), eptr.end() - 1);
@@ -978,6 +987,7 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
             if (k >= 0) idx[pos[k]++] = s;
         }
     };
+    stage("    amalgamation setup", ts);
     std::vector<i64> kptr, kidx;
     csr(ns, [&](i64 s) { return par1[s]; }, kptr, kidx);
     std::vector<i64> cs;
@@ -1002,6 +1012,7 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
             mtrue[rp] += mtrue[rc];
         }
     }
+    stage("    merges", ts);
     // 5. renumber: postorder of the merged tree; a merged front lists its members' columns in the members'
     //    (post)order, so the new order is still a topological order of the elimination tree
     std::vector<i64> root(ns);
