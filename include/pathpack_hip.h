@@ -8,6 +8,8 @@
  *   mlu(s, A; alg)        src/CPU/abstract_slu.jl:44-48      -> pp_symbolic + pp_factor
  *   mstar(s, A; alg)      src/CPU/abstract_slu.jl:85-87      -> pp_symbolic + pp_factor + pp_star
  *   Matrix(F)             src/CPU/abstract_slu.jl:10-14      -> pp_star
+ *   copyto!(F, A); lu!(F) src/CPU/chordal_slu.jl:116, abstract_slu.jl:119 -> pp_refactor
+ *   sgetre! (many k)      src/CPU/chordal_slu.jl:445-493     -> pp_star_sources   (rows / columns of A*)
  *   lmul!(F, B)           src/CPU/abstract_slu.jl:131-134    -> pp_lmul
  *   rmul!(B, F)           src/CPU/abstract_slu.jl:142-145    -> pp_rmul
  *   sgemx!(s, C, A, B)    src/CPU/dense/sgemx.jl:26-60       -> pp_sgemx           (dense kernel, device operands)
@@ -115,6 +117,12 @@ pp_status pp_factor(pp_ctx *ctx, const pp_sym *sym, int semiring, int dtype, con
 /* Same, with nzval already in device memory. */
 pp_status pp_factor_device(pp_ctx *ctx, const pp_sym *sym, int semiring, int dtype, const void *d_nzval,
                            pp_fac **fac);
+/* New values of the same pattern into an existing factor, factorized in place: copyto!(F, A) + lu!(F)
+ * (src/CPU/chordal_slu.jl:116-118, src/CPU/abstract_slu.jl:119-121), the repeated-weights plan of the reference's GPU
+ * API (apsp_plan / apsp_gpu(plan, A2), ext/PATHPACKCUDAExt/api.jl:545-600).  No analysis, no plan upload and no new
+ * factor buffers: nzval holds the values in the CSC order of the pattern given to pp_symbolic (the caller keeps the
+ * pattern; a device pointer when on_device != 0).  Later pp_star / pp_lmul / pp_rmul use the new factor. */
+pp_status pp_refactor(pp_ctx *ctx, pp_fac *fac, const void *nzval, int on_device);
 /* Copy the factor to the host in the reference's layout (CliqueTrees' FChordalTriangular storage):
  * LD/UD: diagonal blocks (sum nn^2; LD holds L (strict lower) + U, UD's upper triangle holds U),
  * LL: na x nn blocks of L (sum nn*na), UL: nn x na blocks of U.  Pointers may be NULL. */

@@ -440,6 +440,43 @@ pp_status pp_factor_device(pp_ctx *ctx, const pp_sym *sym, int semiring, int dty
     return factor_common(ctx, sym, semiring, dtype, d_nzval, true, fac);
 }
 
+pp_status pp_refactor(pp_ctx *ctx, pp_fac *fac, const void *nzval, int on_device) {
+    if (!ctx || !fac) return fail(ctx, PP_EINVAL, "pp_refactor: null argument");
+    if (fac->ctx != ctx) return fail(ctx, PP_EINVAL, "pp_refactor: the factor belongs to another context");
+    const pp::Symbolic &S = fac->sym->S;
+    if (S.nnz > 0 && !nzval) return fail(ctx, PP_EINVAL, "pp_refactor: null nzval");
+    CHECK_HIP(ctx, hipSetDevice(ctx->device));
+    const size_t es = (size_t)pp::dtype_size(fac->dtype);
+    const pp::SweepPlan &W = *fac->sym->splan;
+    // the factorization's fronts, the star blocks' scratch and the uploaded values: the factor's own buffers are reused
+    const size_t need = es * ((size_t)fac->sym->fplan->arena + (on_device ? 0 : (size_t)S.nnz) +
+                              (size_t)W.nb * 2 * pp::BLK_W * pp::BLK_W);
+    size_t freeb = 0, totalb = 0;
+    CHECK_HIP(ctx, hipMemGetInfo(&freeb, &totalb));
+    if (need > freeb)
+        return fail(ctx, PP_ENOMEM, "pp_refactor: needs " + std::to_string(need) + " bytes of device memory, " +
+                                        std::to_string(freeb) + " free");
+    hipStream_t st = ctx->stream;
+    const void *dnz = nzval;
+    void *tmpnz = nullptr;
+    if (!on_device && S.nnz > 0) {
+        if (hipMallocAsync(&tmpnz, S.nnz * es, st) != hipSuccess) return fail(ctx, PP_ENOMEM, "pp_refactor: hipMalloc of the values failed");
+        if (hipMemcpyAsync(tmpnz, nzval, S.nnz * es, hipMemcpyHostToDevice, st) != hipSuccess) {
+            hipFreeAsync(tmpnz, st);
+            hipStreamSynchronize(st);
+            return fail(ctx, PP_EHIP, "pp_refactor: upload of the values failed");
+        }
+        dnz = tmpnz;
+    }
+    std::string e = pp::device_factor(ctx, fac, dnz);
+    if (tmpnz) hipFreeAsync(tmpnz, st);
+    if (e.empty()) e = pp::device_factor_packs(ctx, fac);
+    hipError_t se = hipStreamSynchronize(st);
+    if (!e.empty() || se != hipSuccess)
+        return fail(ctx, PP_EHIP, "pp_refactor: " + (e.empty() ? std::string(hipGetErrorString(se)) : e));
+    return PP_OK;
+}
+
 pp_status pp_fac_export(pp_ctx *ctx, const pp_fac *fac, void *LD, void *UD, void *LL, void *UL) {
     if (!ctx || !fac) return fail(ctx, PP_EINVAL, "pp_fac_export: null argument");
     CHECK_HIP(ctx, hipSetDevice(ctx->device));

@@ -30,7 +30,7 @@ from ._lib import (PathpackArgumentError, PathpackDeviceError, PathpackError, Pa
 
 __all__ = [
     "AbstractSemiring", "MinPlus", "MaxPlus", "MaxMin", "MinMax", "PlusProd", "OrAnd",
-    "szero", "sone", "mlu", "mstar", "lmul_", "rmul_", "Matrix", "star_rows", "star_cols", "Factorization", "Symbolic", "symbolic",
+    "szero", "sone", "mlu", "lu_", "mstar", "lmul_", "rmul_", "Matrix", "star_rows", "star_cols", "Factorization", "Symbolic", "symbolic",
     "Context", "context", "DeviceArray", "PathpackError", "PathpackArgumentError", "PathpackMemoryError",
     "PathpackUnsupportedError", "PathpackDeviceError",
 ]
@@ -235,10 +235,13 @@ class Symbolic:
     """Ordering, supernodal elimination tree and separators of a pattern (pp_sym; ssymbolic,
     chordal_ssymbolic.jl:26-57).  Host only."""
 
-    def __init__(self, handle: ctypes.c_void_p, n: int, nnz: int):
+    def __init__(self, handle: ctypes.c_void_p, n: int, nnz: int, colptr=None, rowval=None):
         self.handle = handle
         self.n = n
         self.nnz = nnz
+        # the pattern, kept to check that later values (mlu(..., sym=), lu_) belong to it
+        self._colptr = None if colptr is None else np.array(colptr, np.int64)
+        self._rowval = None if rowval is None else np.array(rowval, np.int64)
         nn = ctypes.c_int64()
         nf = ctypes.c_int64()
         ns = ctypes.c_int64()
@@ -267,6 +270,15 @@ class Symbolic:
             self._export = {"perm": perm, "Rptr": R, "Sptr": S, "Stgt": T[:self.nstgt], "parent": P[:self.nf]}
         return self._export
 
+    def check_pattern(self, n: int, colptr, rowval):
+        """PathpackArgumentError unless (n, colptr, rowval) is the analysed pattern."""
+        same = n == self.n and len(rowval) == self.nnz
+        if same and self._colptr is not None:
+            same = np.array_equal(colptr, self._colptr) and np.array_equal(rowval, self._rowval)
+        if not same:
+            raise PathpackArgumentError(_lib.PP_EINVAL, "the matrix does not have the pattern of the analysis; "
+                                                        "analyse it again")
+
     def stats(self) -> dict:
         st = (ctypes.c_double * 10)()
         check(lib().pp_sym_stats(self.handle, st))
@@ -292,7 +304,7 @@ def symbolic(A, alg=None, amalgamate: bool = True) -> Symbolic:
         if perm.shape != (n,):
             raise PathpackArgumentError(_lib.PP_EINVAL, "the permutation must have n entries")
         check(lib().pp_symbolic(n, _p(cp), _p(rv), 2, 1 if amalgamate else 0, _p(perm), ctypes.byref(h)))
-    return Symbolic(h, n, int(cp[-1]))
+    return Symbolic(h, n, int(cp[-1]), cp, rv)
 
 
 def symbolic_given(A, perm, Rptr) -> Symbolic:
@@ -302,7 +314,7 @@ def symbolic_given(A, perm, Rptr) -> Symbolic:
     Rptr = np.ascontiguousarray(Rptr, np.int64)
     h = ctypes.c_void_p()
     check(lib().pp_symbolic_given(n, _p(cp), _p(rv), _p(perm), Rptr.size - 1, _p(Rptr), ctypes.byref(h)))
-    return Symbolic(h, n, int(cp[-1]))
+    return Symbolic(h, n, int(cp[-1]), cp, rv)
 
 
 # ===== factorization =====
@@ -371,11 +383,42 @@ def mlu(s: AbstractSemiring, A, alg=None, amalgamate: bool = True, device: int =
         csc = (n, cp, rv, nz)
         if sym is None:
             sym = symbolic_given(csc, np.arange(n), np.array([0, n]) if n > 0 else np.array([0]))
+        else:
+            sym.check_pattern(n, cp, rv)
         return _factor(s, sym, nz, ctx)
     n, cp, rv, nz = _as_csc(A)
     if sym is None:
         sym = symbolic((n, cp, rv, nz), alg=alg, amalgamate=amalgamate)
+    else:
+        sym.check_pattern(n, cp, rv)
     return _factor(s, sym, nz, ctx)
+
+
+def lu_(F: Factorization, A):
+    """copyto!(F, A) then lu!(F) (chordal_slu.jl:116-118, abstract_slu.jl:119-121): the values of A, which must
+    have the pattern F was analysed for, factorized in place on the device (no new analysis, plan upload or factor
+    buffers; the reference GPU API's repeated-weights plan, ext/PATHPACKCUDAExt/api.jl:545-600).  ``A`` may also be
+    a DeviceArray of the nnz values in the pattern's CSC order.  Returns F."""
+    if isinstance(A, DeviceArray):
+        if A.dtype != F.dtype or int(np.prod(A.shape)) != F.sym.nnz:
+            raise PathpackArgumentError(_lib.PP_EINVAL, "lu_: the values must be nnz entries of the factor's type")
+        F.ctx.check(lib().pp_refactor(F.ctx.handle, F.handle, ctypes.c_void_p(A.ptr), 1))
+        return F
+    if isinstance(A, np.ndarray):
+        n = A.shape[0]
+        if A.ndim != 2 or A.shape != (F.n, F.n):
+            raise PathpackArgumentError(_lib.PP_EINVAL, "lu_: the matrix must be n x n")
+        cp = np.arange(0, n * n + 1, n, dtype=np.int64)
+        rv = np.tile(np.arange(n, dtype=np.int64), n)
+        nz = np.asfortranarray(A).ravel(order="F")
+    else:
+        n, cp, rv, nz = _as_csc(A)
+    F.sym.check_pattern(n, cp, rv)
+    if nz.dtype != F.dtype:
+        raise PathpackArgumentError(_lib.PP_EINVAL, f"lu_: the values must have the factor's type {F.dtype}")
+    nz = np.ascontiguousarray(nz)
+    F.ctx.check(lib().pp_refactor(F.ctx.handle, F.handle, _p(nz), 0))
+    return F
 
 
 def Matrix(F: Factorization, device: bool = False, out=None):

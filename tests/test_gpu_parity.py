@@ -317,3 +317,44 @@ def test_star_sources_device_output_and_errors():
         P.star_rows(F, [g.n])
     with pytest.raises(P.PathpackArgumentError):
         P.star_cols(F, [-1])
+
+
+@pytest.mark.parametrize("s,fdtype", [(O.MINPLUS, np.float32), (O.MAXMIN, np.float64), (O.PLUSPROD, np.float64),
+                                      (O.ORAND, np.float32)])
+def test_refactor_new_weights_same_pattern(s, fdtype):
+    """copyto!(F, A2) + lu!(F) (pp_refactor) on a factor of A1 equals a fresh factorization of A2: factor arrays,
+    star and solves; a matrix of another pattern is refused."""
+    dtype = dtype_for(s, fdtype)
+    g0 = BLOCK_GRAPHS["grid15x13x11"]()
+    g1 = weighted(g0, s, dtype, seed=11)
+    g2 = weighted(g0, s, dtype, seed=12)
+    sym = P.symbolic(g1)
+    F = P.mlu(SEMIRINGS[s], g1, sym=sym)
+    C1 = P.Matrix(F)
+    P.lu_(F, g2)
+    F2 = P.mlu(SEMIRINGS[s], g2, sym=sym)
+    e, e2 = F.export(), F2.export()
+    for k in ("LD", "LL", "UL"):
+        assert np.array_equal(bits(e[k]), bits(e2[k])), k
+    C = P.Matrix(F)
+    assert np.array_equal(bits(C), bits(P.Matrix(F2)))
+    assert not np.array_equal(bits(C), bits(C1))
+    Fo = O.factor(s, oracle_sym(sym), g2.colptr, g2.rowval, g2.nzval)
+    assert_star_equal(s, C, O.star(Fo), rtol=rtol_for(s, dtype) * 10)
+    # device-resident values, then back to the first weights
+    dnz = P.DeviceArray.from_numpy(np.ascontiguousarray(g1.nzval).reshape(-1, 1))
+    P.lu_(F, dnz)
+    assert np.array_equal(bits(P.Matrix(F)), bits(C1))
+    # solves after a refactorization use the new factor
+    P.lu_(F, g2)
+    B = np.full((g0.n, 3), P.szero(SEMIRINGS[s], dtype), dtype, order="F")
+    B[[0, 7, g0.n - 1], [0, 1, 2]] = P.sone(SEMIRINGS[s], dtype)
+    B2 = B.copy(order="F")
+    P.lmul_(F, B)
+    P.lmul_(F2, B2)
+    assert np.array_equal(bits(B), bits(B2))
+    other = weighted(BLOCK_GRAPHS["grid16x17x15"](), s, dtype)
+    with pytest.raises(P.PathpackArgumentError):
+        P.lu_(F, other)
+    with pytest.raises(P.PathpackArgumentError):
+        P.mlu(SEMIRINGS[s], other, sym=sym)
