@@ -72,11 +72,14 @@ def factor_device(s, sym, dnz, ctx):
     return P.Factorization(s, sym, dnz.dtype, h, ctx)
 
 
+ORDERING = ["nd"]   # the analysis's fill-reducing order (--ordering)
+
+
 def step_mstar(g, dnz, out, ctx, timing):
     """One mstar: returns (seconds, symbolic, phases)."""
     ctx.synchronize()
     t0 = time.perf_counter()
-    sym = P.symbolic(g)
+    sym = P.symbolic(g, alg=ORDERING[0])
     t1 = time.perf_counter()
     F = factor_device(P.MinPlus(), sym, dnz, ctx)
     t2 = time.perf_counter()
@@ -185,7 +188,7 @@ def bench_mstar(args):
         "dtype": "f32" if g.nzval.dtype == np.float32 else "f64",
         "data": "synthetic",
         "config": {"workload": workload,
-                   "n": g.n, "nnz": g.nnz, "fronts": sym.nf, "madds_alg": madds,
+                   "n": g.n, "nnz": g.nnz, "fronts": sym.nf, "ordering": ORDERING[0], "madds_alg": madds,
                    "madds_executed": st["madds_factor"] + st["madds_star"], "nnzL_alg": st["nnzL_alg"],
                    "mstar_s": round(T, 5)},
         "phases_ms": {k: round(v * 1e3, 3) for k, v in ph.items()},
@@ -345,7 +348,7 @@ def bench_solve(args, cfg):
         B = np.zeros((nrhs, n), np.float64, order="F")
         B[np.arange(nrhs), src] = 1.0
     t0 = time.perf_counter()
-    sym = P.symbolic(g)
+    sym = P.symbolic(g, alg=ORDERING[0])
     t_sym = time.perf_counter() - t0
     dnz = P.DeviceArray.from_numpy(np.ascontiguousarray(g.nzval).reshape(-1, 1))
     ctx.synchronize()
@@ -392,7 +395,8 @@ def bench_solve(args, cfg):
                      if left else
                      f"PlusProd rmul! of 512 unit rows (1 at a seeded source) on the directed 256x256 grid, weights "
                      f"U(0,0.2) Float64 (seed 0x5EED+5)") + "; B in HBM, restored by a device copy in each step",
-                    {"n": n, "nrhs": nrhs, "madds_alg": madds, "fronts": sym.nf})
+                    {"n": n, "nrhs": nrhs, "madds_alg": madds, "fronts": sym.nf, "ordering": ORDERING[0],
+                     "nnzL_alg": st["nnzL_alg"]})
     r["phases_ms"] = {"symbolic_s": round(t_sym * 1e3, 3), "factor_s": round(t_fac * 1e3, 3),
                       "solve_device_s": round(t_dev * 1e3, 3)}
     r["unit_sources"] = {"entry": "pp_star_sources", "ms_per_step": round(T2 * 1e3, 3),
@@ -419,6 +423,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="3", choices=["1", "2a", "2b", "3", "4", "5"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--ordering", default="nd", choices=["nd", "amd"],
+                    help="fill-reducing order of the analysis: nested dissection (default) or approximate minimum degree")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-timing", dest="timing", action="store_false")
     ap.add_argument("--calibrate-valu", action="store_true",
@@ -427,6 +433,7 @@ def main():
                     help="only run the plain copy kernel (pp_copy) over this many MiB: the calibration of the memory "
                          "counters FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
+    ORDERING[0] = args.ordering
     if args.calibrate_valu:
         import ctypes
 

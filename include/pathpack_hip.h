@@ -63,7 +63,9 @@ typedef enum { PP_F32 = 0, PP_F64 = 1, PP_I32 = 2 } pp_dtype;
 typedef enum {
     PP_ORDER_ND = 0,       /* nested dissection (default) */
     PP_ORDER_NATURAL = 1,  /* identity */
-    PP_ORDER_GIVEN = 2     /* the permutation passed in `perm` (perm[new] = old, 0-based) */
+    PP_ORDER_GIVEN = 2,    /* the permutation passed in `perm` (perm[new] = old, 0-based) */
+    PP_ORDER_AMD = 3,      /* approximate minimum degree (for irregular graphs: road networks, meshes) */
+    PP_ORDER_AUTO = 4      /* both ND and AMD (concurrently), keeping the order whose factor has fewer entries */
 } pp_ordering;
 
 typedef struct pp_ctx pp_ctx;

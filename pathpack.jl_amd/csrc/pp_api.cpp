@@ -141,7 +141,7 @@ pp_status pp_symbolic(int64_t n, const int64_t *colptr, const int64_t *rowval, i
     if (!out) return fail(nullptr, PP_EINVAL, "pp_symbolic: null output");
     *out = nullptr;
     if (n < 0 || !colptr || (n > 0 && colptr[n] > 0 && !rowval)) return fail(nullptr, PP_EINVAL, "pp_symbolic: bad matrix");
-    if (ordering < 0 || ordering > 2) return fail(nullptr, PP_EINVAL, "pp_symbolic: unknown ordering");
+    if (ordering < 0 || ordering > 4) return fail(nullptr, PP_EINVAL, "pp_symbolic: unknown ordering");
     if (ordering == PP_ORDER_GIVEN && !perm) return fail(nullptr, PP_EINVAL, "pp_symbolic: ordering GIVEN needs perm");
     pp_sym *s = new (std::nothrow) pp_sym;
     if (!s) return fail(nullptr, PP_ENOMEM, "pp_symbolic: out of host memory");

@@ -1038,24 +1038,27 @@ __device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64
         }
     };
     if (e > 0) {
-        T A[4], B[4], C[4];
-        ld4(0, A);
-        if (4 < e) ld4(4, B);
+        // NS register sets of four in rotation: group g + NS - 1 is loaded while group g is multiplied (deeper
+        // rotations spill at the kernel's 80-register budget and run slower)
+        constexpr int NS = 3;
+        T xs[NS][4];
+#pragma unroll
+        for (int u = 0; u + 1 < NS; u++)
+            if (4 * u < e) ld4(4 * u, xs[u]);
         int t0 = 0;
-        for (; t0 + 12 <= e; t0 += 12) {
-            if (t0 + 8 < e) ld4(t0 + 8, C);
-            mad4(t0, A);
-            if (t0 + 12 < e) ld4(t0 + 12, A);
-            mad4(t0 + 4, B);
-            if (t0 + 16 < e) ld4(t0 + 16, B);
-            mad4(t0 + 8, C);
+        for (; t0 + 4 * NS <= e; t0 += 4 * NS) {
+#pragma unroll
+            for (int u = 0; u < NS; u++) {
+                if (t0 + 4 * (u + NS - 1) < e) ld4(t0 + 4 * (u + NS - 1), xs[(u + NS - 1) % NS]);
+                mad4(t0 + 4 * u, xs[u]);
+            }
         }
-        if (t0 < e) {
-            if (t0 + 8 < e) ld4(t0 + 8, C);
-            mad4(t0, A);
-            if (t0 + 4 < e) mad4(t0 + 4, B);
-            if (t0 + 8 < e) mad4(t0 + 8, C);
-        }
+#pragma unroll
+        for (int u = 0; u < NS; u++)
+            if (t0 + 4 * u < e) {
+                if (u == NS - 1) ld4(t0 + 4 * u, xs[u]);
+                mad4(t0 + 4 * u, xs[u]);
+            }
     }
 #pragma unroll
     for (int j = W - 1; j >= 0; j--) {

@@ -452,6 +452,193 @@ struct ND {
     }
 };
 
+// ===== approximate minimum degree (Amestoy, Davis & Duff, SIAM J. Matrix Anal. Appl. 17(4):886-905, 1996) =====
+//
+// The quotient graph: eliminating a pivot turns it into an element, the clique of its remaining neighbours (Lme),
+// which absorbs the elements adjacent to the pivot.  A variable's list holds its adjacent elements first, then its
+// adjacent variables.  Variables whose lists become equal merge into supervariables (nv = size); a variable left
+// adjacent to the new element only is eliminated with the pivot (mass elimination).  The degree of a variable is
+// the AMD upper bound min(n - k, d_old + |Lme \ i|, |A_i \ i| + |Lme \ i| + sum_e |Le \ Lme|), where |Le \ Lme| comes
+// from one pass over the elements adjacent to Lme.  The pivot is a variable of least degree.  Returns the
+// elimination order (order[k] = vertex eliminated k-th).
+std::vector<i64> amd_order(const Adj &G) {
+    const i64 n = G.n;
+    std::vector<i64> order;
+    order.reserve(n);
+    if (n == 0) return order;
+    std::vector<i32> iw(G.adj.begin(), G.adj.end());   // lists; element lists are appended at the end
+    std::vector<i64> pe(G.xadj.begin(), G.xadj.end() - 1);
+    std::vector<i32> len(n), elen(n, 0), nv(n, 1), degree(n);
+    std::vector<char> isel(n, 0), dead(n, 0);            // node is an element; node absorbed (element or variable)
+    std::vector<i64> w(n, 0);                           // element marks: |Le \ Lme| + wflg
+    std::vector<i32> head(n + 1, -1), next(n, -1), last(n, -1);
+    std::vector<i32> gnext(n, -1), gtail(n);            // members of each supervariable / pivot group
+    std::vector<i32> mark(n, -1);
+    std::vector<i64> hkey(n, 0);
+    for (i64 i = 0; i < n; i++) {
+        len[i] = (i32)(G.xadj[i + 1] - G.xadj[i]);
+        degree[i] = len[i];
+        gtail[i] = (i32)i;
+    }
+    auto dl_insert = [&](i32 i, i32 d) {
+        next[i] = head[d];
+        last[i] = -1;
+        if (head[d] >= 0) last[head[d]] = i;
+        head[d] = i;
+    };
+    auto dl_remove = [&](i32 i) {
+        if (last[i] >= 0) next[last[i]] = next[i];
+        else head[degree[i]] = next[i];
+        if (next[i] >= 0) last[next[i]] = last[i];
+    };
+    auto gappend = [&](i32 a, i32 b) {   // members of b after those of a
+        gnext[gtail[a]] = b;
+        gtail[a] = gtail[b];
+    };
+    for (i64 i = 0; i < n; i++) dl_insert((i32)i, degree[i]);
+    i64 nel = 0, mindeg = 0, wflg = 1;
+    std::vector<i32> lme, bucket_members;
+    while (nel < n) {
+        while (mindeg <= n && head[mindeg] < 0) mindeg++;
+        const i32 me = head[mindeg];
+        dl_remove(me);
+        i32 nvpiv = nv[me];
+        nv[me] = -nvpiv;
+        // 1. Lme: the principal variables of me's list and of its elements, which me absorbs
+        lme.clear();
+        i64 degme = 0;
+        auto take = [&](i32 i) {
+            if (isel[i] || dead[i] || nv[i] <= 0) return;   // an element, absorbed, already in Lme, or me
+            degme += nv[i];
+            nv[i] = -nv[i];
+            dl_remove(i);
+            lme.push_back(i);
+        };
+        for (i32 q = 0; q < len[me]; q++) {
+            const i32 x = iw[pe[me] + q];
+            if (q < elen[me]) {
+                if (dead[x]) continue;
+                for (i32 r = 0; r < len[x]; r++) take(iw[pe[x] + r]);
+                dead[x] = 1;   // absorbed into me
+                w[x] = 0;
+            } else {
+                take(x);
+            }
+        }
+        isel[me] = 1;
+        // 2. |Le \ Lme| for the elements adjacent to Lme
+        for (i32 i : lme) {
+            const i32 nvi = -nv[i];
+            for (i32 q = 0; q < elen[i]; q++) {
+                const i32 e = iw[pe[i] + q];
+                if (dead[e] || e == me) continue;
+                if (w[e] >= wflg) w[e] -= nvi;
+                else w[e] = degree[e] + wflg - nvi;
+            }
+        }
+        // 3. new lists and degree bounds of the variables of Lme; mass elimination
+        std::vector<i32> &keep = bucket_members;
+        i64 kept_lme = 0;
+        for (i32 i : lme) {
+            const i32 nvi = -nv[i];
+            const i64 p0 = pe[i];
+            i64 deg = 0, h = me;
+            keep.clear();
+            for (i32 q = 0; q < elen[i]; q++) {
+                const i32 e = iw[p0 + q];
+                if (dead[e] || e == me) continue;
+                const i64 we = w[e] - wflg;
+                if (we > 0) {
+                    deg += we;
+                    keep.push_back(e);
+                    h += e;
+                } else {
+                    dead[e] = 1;   // Le within Lme: absorbed into me (aggressive absorption)
+                    w[e] = 0;
+                }
+            }
+            const i32 ne = (i32)keep.size();
+            for (i32 q = elen[i]; q < len[i]; q++) {
+                const i32 j = iw[p0 + q];
+                if (isel[j] || dead[j] || nv[j] <= 0) continue;   // elements, absorbed, Lme (covered by me)
+                deg += nv[j];
+                keep.push_back(j);
+                h += j;
+            }
+            if (keep.empty()) {
+                // adjacent to me only: eliminated together with the pivot
+                dead[i] = 1;
+                nvpiv += nvi;
+                nv[i] = 0;
+                gappend(me, i);
+                continue;
+            }
+            iw[p0] = me;
+            for (i32 q = 0; q < (i32)keep.size(); q++) iw[p0 + 1 + q] = keep[q];
+            len[i] = (i32)keep.size() + 1;
+            elen[i] = ne + 1;
+            degree[i] = (i32)std::min<i64>(degree[i], deg);   // the two bounds without |Lme \ i|
+            hkey[i] = h % n;
+            lme[kept_lme++] = i;
+        }
+        lme.resize(kept_lme);
+        // 4. supervariables: variables of Lme with equal lists merge (candidates share a hash of their lists)
+        if (lme.size() > 1) {
+            std::sort(lme.begin(), lme.end(), [&](i32 a, i32 b) { return hkey[a] != hkey[b] ? hkey[a] < hkey[b] : a < b; });
+            for (size_t a = 0; a < lme.size(); a++) {
+                const i32 i = lme[a];
+                if (dead[i]) continue;
+                bool marked = false;
+                for (size_t b = a + 1; b < lme.size() && hkey[lme[b]] == hkey[i]; b++) {
+                    const i32 j = lme[b];
+                    if (dead[j] || len[j] != len[i] || elen[j] != elen[i]) continue;
+                    if (!marked) {
+                        for (i32 q = 0; q < len[i]; q++) mark[iw[pe[i] + q]] = i;
+                        marked = true;
+                    }
+                    bool same = true;
+                    for (i32 q = 0; q < len[j] && same; q++) same = mark[iw[pe[j] + q]] == i;
+                    if (!same) continue;
+                    nv[i] += nv[j];   // both negative while in Lme
+                    nv[j] = 0;
+                    dead[j] = 1;
+                    degree[i] = std::min(degree[i], degree[j]);
+                    gappend(i, j);
+                }
+                if (marked)
+                    for (i32 q = 0; q < len[i]; q++) mark[iw[pe[i] + q]] = -1;
+            }
+        }
+        // 5. the element me and the final degrees of its variables
+        nel += nvpiv;
+        i64 degme2 = 0;
+        const i64 start = (i64)iw.size();
+        for (i32 i : lme)
+            if (!dead[i]) {
+                degme2 += -nv[i];
+                iw.push_back(i);
+            }
+        for (i64 q = start; q < (i64)iw.size(); q++) {
+            const i32 i = iw[q];
+            const i32 nvi = -nv[i];
+            nv[i] = nvi;
+            const i64 d = std::min<i64>({(i64)degree[i] + degme2 - nvi, n - nel - nvi});
+            degree[i] = (i32)std::max<i64>(d, 0);
+            dl_insert(i, degree[i]);
+            mindeg = std::min<i64>(mindeg, degree[i]);
+        }
+        pe[me] = start;
+        len[me] = (i32)((i64)iw.size() - start);
+        elen[me] = 0;
+        degree[me] = (i32)degme2;
+        nv[me] = nvpiv;
+        if (len[me] == 0) dead[me] = 1;
+        for (i32 m = me; m >= 0; m = gnext[m]) order.push_back(m);
+        wflg += n + 1;
+    }
+    return order;
+}
+
 // ===== elimination tree and postorder (Liu 1986, path compression) =====
 
 // post_perm: a postorder of the elimination tree of perm (the children of a node in increasing order);
@@ -890,10 +1077,38 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
     }
     // 1. fill-reducing order
     std::vector<i64> perm0(n);
-    if (opts.ordering == 0) {
+    std::vector<i64> perm1, pcol, ccol;   // set here by the automatic choice (2. and 3. below otherwise)
+    if (opts.ordering == 4) {
+        // both orders (minimum degree on its own thread while nested dissection uses the pool); keep the one whose
+        // factor has fewer entries
+        std::vector<i64> pa;
+        std::thread tamd([&] { pa = amd_order(G); });
+        ND nd(G, opts.nd_leaf);
+        nd.run(analysis_threads(n));
+        tamd.join();
+        std::vector<i64> p1[2], pc[2], cc[2];
+        const std::vector<i64> *cand[2] = {&nd.order, &pa};
+        std::thread t1([&] {
+            etree_postorder(G, *cand[1], p1[1], pc[1]);
+            column_counts(G, p1[1], pc[1], cc[1]);
+        });
+        etree_postorder(G, *cand[0], p1[0], pc[0]);
+        column_counts(G, p1[0], pc[0], cc[0]);
+        t1.join();
+        i64 fill[2] = {0, 0};
+        for (int c = 0; c < 2; c++)
+            for (i64 v : cc[c]) fill[c] += v;
+        const int pick = fill[1] < fill[0] ? 1 : 0;
+        perm0 = *cand[pick];
+        perm1 = std::move(p1[pick]);
+        pcol = std::move(pc[pick]);
+        ccol = std::move(cc[pick]);
+    } else if (opts.ordering == 0) {
         ND nd(G, opts.nd_leaf);
         nd.run(analysis_threads(n));
         perm0 = nd.order;
+    } else if (opts.ordering == 3) {
+        perm0 = amd_order(G);
     } else if (opts.ordering == 1) {
         std::iota(perm0.begin(), perm0.end(), 0);
     } else {
@@ -909,13 +1124,11 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
     double ts = t0;
     stage("symmetrize + order", ts);
     // 2. postordered elimination tree
-    std::vector<i64> perm1, pcol;
-    etree_postorder(G, perm0, perm1, pcol);
+    if (opts.ordering != 4) etree_postorder(G, perm0, perm1, pcol);
     stage("etree + postorder", ts);
     // 3. column counts, then fundamental supernodes: j + 1 continues j's supernode when it is j's parent, has no
     //    other child, and its column holds exactly one entry fewer
-    std::vector<i64> ccol;
-    column_counts(G, perm1, pcol, ccol);
+    if (opts.ordering != 4) column_counts(G, perm1, pcol, ccol);
     std::vector<i64> nchild(n, 0);
     for (i64 j = 0; j < n; j++)
         if (pcol[j] >= 0) nchild[pcol[j]]++;

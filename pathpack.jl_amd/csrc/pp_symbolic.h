@@ -25,7 +25,8 @@ typedef int64_t i64;
 typedef int32_t i32;
 
 struct SymOptions {
-    int ordering = 0;          // 0 = nested dissection, 1 = natural (identity), 2 = given permutation
+    int ordering = 0;          // 0 = nested dissection, 1 = natural (identity), 2 = given permutation,
+                               // 3 = approximate minimum degree, 4 = the one of 0 and 3 with the smaller factor
     int amalgamate = 1;        // relaxed amalgamation on/off
     int nd_leaf = 32;          // subgraphs of at most this many vertices are ordered by minimum degree
     int relax_small = 4;       // fronts of at most this many columns always merge

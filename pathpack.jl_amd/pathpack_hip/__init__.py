@@ -287,12 +287,13 @@ class Symbolic:
         return dict(zip(keys, st[:]))
 
 
-_ALGS = {None: 0, "nd": 0, "ND": 0, "natural": 1}
+_ALGS = {None: 0, "nd": 0, "ND": 0, "natural": 1, "amd": 3, "AMD": 3, "auto": 4}
 
 
 def symbolic(A, alg=None, amalgamate: bool = True) -> Symbolic:
-    """Symbolic analysis of the pattern of A.  ``alg``: None / "nd" (nested dissection), "natural", or a permutation
-    (0-based, perm[new] = old) -- the reference's ``alg`` keyword (abstract_slu.jl:44)."""
+    """Symbolic analysis of the pattern of A.  ``alg``: None / "nd" (nested dissection), "amd" (approximate minimum
+    degree), "auto" (both, keeping the order with the smaller factor), "natural", or a permutation (0-based,
+    perm[new] = old) -- the reference's ``alg`` keyword (abstract_slu.jl:44)."""
     n, cp, rv, _ = _as_csc(A)
     h = ctypes.c_void_p()
     if isinstance(alg, (str, type(None))):

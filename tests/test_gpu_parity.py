@@ -358,3 +358,20 @@ def test_refactor_new_weights_same_pattern(s, fdtype):
         P.lu_(F, other)
     with pytest.raises(P.PathpackArgumentError):
         P.mlu(SEMIRINGS[s], other, sym=sym)
+
+
+@pytest.mark.parametrize("name", ["components", "digraph150", "rgg700"])
+@pytest.mark.parametrize("s,fdtype", [(O.MINPLUS, np.float32), (O.MAXMIN, np.float32), (O.PLUSPROD, np.float64)])
+def test_star_with_minimum_degree_ordering(name, s, fdtype):
+    """Factor and star under the approximate minimum degree order equal the oracle's for the same structure, and the
+    star equals the nested-dissection one (bit for bit with integer weights; the star does not depend on the order)."""
+    dtype = dtype_for(s, fdtype)
+    g = weighted(graphs()[name], s, dtype)
+    print(f"case {name} s={s} amd", flush=True)
+    sym = P.symbolic(g, alg="amd")
+    F = P.mlu(SEMIRINGS[s], g, sym=sym)
+    Fo = O.factor(s, oracle_sym(sym), g.colptr, g.rowval, g.nzval)
+    compare_factor(s, F, Fo, dtype)
+    C = P.Matrix(F)
+    assert_star_equal(s, C, O.star(Fo), rtol=rtol_for(s, dtype) * 10)
+    assert_star_equal(s, C, P.mstar(SEMIRINGS[s], g), rtol=rtol_for(s, dtype) * 10)
