@@ -533,6 +533,110 @@ __global__ __launch_bounds__(256) void k_gemm_tiled(typename S::value_type *__re
         }
 }
 
+// ===== PlusProd over doubles on the fp64 matrix cores =====
+//
+// PlusProd is the ordinary (+, x) algebra, so its GEMMs are dense contractions for v_mfma_f64_16x16x4f64.  Lane
+// layout of one 16 x 16 x 4 product, as measured on gfx950: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16]
+// and holds D[4 r + l / 16][l % 16] in element r of its four accumulators.
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+__device__ inline v4d mfma_f64_16x16x4(double a, double b, v4d c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
+// C <- C + A B (column-major, f64): a 64 x 64 tile per workgroup of four waves, each wave a 32 x 32 quarter
+// (2 x 2 products per k step of 4); K in steps of 16 through two LDS buffers with the next step's loads in registers,
+// as k_gemm_tiled.  Operands outside the matrices load as 0.
+template <class T>
+__global__ __launch_bounds__(256) void k_gemm_mfma64(T *__restrict__ C, i64 ldc, const T *__restrict__ A, i64 lda,
+                                                    const T *__restrict__ B, i64 ldb, i64 m, i64 n, i64 k) {
+    static_assert(std::is_same<T, double>::value, "the fp64 matrix cores");
+    constexpr int BM = 64, BN = 64, BK = 16, PAD = 4;
+    __shared__ __attribute__((aligned(16))) double As[2][BK][BM + PAD];
+    __shared__ __attribute__((aligned(16))) double Bs[2][BK][BN + PAD];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int li = lane & 15, lq = lane >> 4;
+    const int wr = (wv & 1) * 32, wc = (wv >> 1) * 32;   // the wave's quarter of the tile
+    const i64 r0 = (i64)blockIdx.x * BM, c0 = (i64)blockIdx.y * BN;
+    const bool vec = r0 + BM <= m && c0 + BN <= n && lda % 2 == 0 && ldb % 2 == 0 && ((uintptr_t)A & 15) == 0 &&
+                     ((uintptr_t)B & 15) == 0;
+    double ra[4], rb[4];   // two pairs of consecutive elements each: A down a column, B down a column (along k)
+    auto gload = [&](i64 k0) {
+        const bool full = vec && k0 + BK <= k;
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int e = (tid + 256 * q) * 2;
+            const int ar = e % BM, ak = e / BM, bk = e % BK, bc = e / BK;
+            if (full) {
+                const double2 va = *reinterpret_cast<const double2 *>(A + (r0 + ar) + (k0 + ak) * lda);
+                const double2 vb = *reinterpret_cast<const double2 *>(B + (k0 + bk) + (c0 + bc) * ldb);
+                ra[2 * q] = va.x;
+                ra[2 * q + 1] = va.y;
+                rb[2 * q] = vb.x;
+                rb[2 * q + 1] = vb.y;
+            } else {
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    ra[2 * q + u] = (r0 + ar + u < m && k0 + ak < k) ? A[(r0 + ar + u) + (k0 + ak) * lda] : 0.0;
+                    rb[2 * q + u] = (k0 + bk + u < k && c0 + bc < n) ? B[(k0 + bk + u) + (c0 + bc) * ldb] : 0.0;
+                }
+            }
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int e = (tid + 256 * q) * 2;
+            As[buf][e / BM][e % BM] = ra[2 * q];
+            As[buf][e / BM][e % BM + 1] = ra[2 * q + 1];
+            Bs[buf][e % BK][e / BK] = rb[2 * q];
+            Bs[buf][e % BK + 1][e / BK] = rb[2 * q + 1];
+        }
+    };
+    v4d acc[2][2];
+#pragma unroll
+    for (int bi = 0; bi < 2; bi++)
+#pragma unroll
+        for (int bj = 0; bj < 2; bj++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const i64 row = r0 + wr + 16 * bi + 4 * r + lq, col = c0 + wc + 16 * bj + li;
+                acc[bi][bj][r] = (row < m && col < n) ? C[row + col * ldc] : 0.0;
+            }
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    int buf = 0;
+    for (i64 k0 = 0; k0 < k; k0 += BK) {
+        const bool more = k0 + BK < k;
+        if (more) gload(k0 + BK);
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 4) {
+            double a[2], b[2];
+#pragma unroll
+            for (int bi = 0; bi < 2; bi++) a[bi] = As[buf][kk + lq][wr + 16 * bi + li];
+#pragma unroll
+            for (int bj = 0; bj < 2; bj++) b[bj] = Bs[buf][kk + lq][wc + 16 * bj + li];
+#pragma unroll
+            for (int bi = 0; bi < 2; bi++)
+#pragma unroll
+                for (int bj = 0; bj < 2; bj++) acc[bi][bj] = mfma_f64_16x16x4(a[bi], b[bj], acc[bi][bj]);
+        }
+        if (more) sstore(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+    }
+#pragma unroll
+    for (int bi = 0; bi < 2; bi++)
+#pragma unroll
+        for (int bj = 0; bj < 2; bj++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const i64 row = r0 + wr + 16 * bi + 4 * r + lq, col = c0 + wc + 16 * bj + li;
+                if (row < m && col < n) C[row + col * ldc] = acc[bi][bj][r];
+            }
+}
+
 // ===== factor extraction: the reference layout and the sweep packs =====
 
 // LD (nn x nn at Dptr), LL (na x nn at Lptr), UL (nn x na at Lptr); one workgroup per (front, EXTRACT_COLS columns)
@@ -2296,6 +2400,13 @@ template <class S> struct GemmRun {
     std::string run() {
         typedef typename S::value_type T;
         if (m == 0 || n == 0) return "";
+        if constexpr (std::is_same<S, PlusProd<double>>::value) {   // (+, x) over doubles: the matrix cores
+            dim3 g((unsigned)((m + 63) / 64), (unsigned)((n + 63) / 64));
+            k_gemm_mfma64<double><<<g, 256, 0, ctx->stream>>>((double *)C, ldc, (const double *)A, lda,
+                                                              (const double *)B, ldb, m, n, k);
+            LAUNCHCHK();
+            return "";
+        }
         constexpr int TM = sizeof(T) == 4 ? 8 : 4, BM = 16 * TM;
         dim3 g((unsigned)((m + BM - 1) / BM), (unsigned)((n + BM - 1) / BM));
         k_gemm_tiled<S, TM, TM><<<g, 256, 0, ctx->stream>>>((T *)C, ldc, (const T *)A, lda, (const T *)B, ldb, m, n, k);
