@@ -246,11 +246,41 @@ def base_result(args, metric, value, unit, T, dtype, workload, extra):
     return r
 
 
+def bench_gemm_plusprod(args):
+    """2a with --semiring plusprod: C <- C + A B over Float64, M = N = K = 8192, entries U[0, 1/N) (fp64 MFMA)."""
+    import ctypes
+
+    N = 8192
+    seed = W.SEED_BASE + 2
+    A, B, C = [np.asfortranarray((W.uniform_float(seed + 10 * q, N * N) / N).reshape(N, N).T) for q in range(3)]
+    ctx = P.context(0)
+    dA, dB, dC = P.DeviceArray.from_numpy(A), P.DeviceArray.from_numpy(B), P.DeviceArray.from_numpy(C)
+
+    def run():
+        ctx.check(P.lib().pp_sgemx(ctx.handle, 4, 1, N, N, N, ctypes.c_void_p(dA.ptr), N, ctypes.c_void_p(dB.ptr), N,
+                                   ctypes.c_void_p(dC.ptr), N))
+
+    T = timed(run, ctx, args.steps, args.warmup)
+    flops = 2.0 * float(N) ** 3
+    valu = bool(os.environ.get("PP_GEMM_VALU"))
+    r = base_result(args, "semiring GEMM TFLOP/s, PlusProd 8192^3 Float64; % fp64 MFMA roofline", flops / T / 1e12,
+                    "TFLOP/s", T, "f64",
+                    "dense PlusProd GEMM C <- C + A B, M=N=K=8192, entries U[0, 1/N) (SplitMix64 seeds 0x5EED+2, "
+                    "+12, +22), operands in HBM", {"m": N, "n": N, "k": N})
+    r["roofline"] = {"bound": "valu" if valu else "mfma",
+                     "kernel": "k_gemm_tiled<PlusProd<double>, 4, 4>" if valu else "k_gemm_mfma64<double>",
+                     "achieved": round(flops / T / 1e12, 3), "peak": 78.6, "unit": "TFLOP/s",
+                     "frac": round(flops / T / 78.6e12, 4), "traffic": None}
+    print(json.dumps(r), flush=True)
+
+
 def bench_gemm(args):
     """2a: C <- min(C, A + B), M = N = K = 8192, Float32, A/B/C ~ U{0..1000} with 10 % +Inf."""
     import ctypes
     import oracle as O
 
+    if args.semiring == "plusprod":
+        return bench_gemm_plusprod(args)
     N = 8192
     seed = W.SEED_BASE + 2
     A = W.dense_minplus(N, N, seed)
@@ -423,6 +453,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="3", choices=["1", "2a", "2b", "3", "4", "5"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--semiring", default="minplus", choices=["minplus", "plusprod"],
+                    help="configuration 2a only: MinPlus Float32 (default) or PlusProd Float64 (fp64 matrix cores)")
     ap.add_argument("--ordering", default="nd", choices=["nd", "amd"],
                     help="fill-reducing order of the analysis: nested dissection (default) or approximate minimum degree")
     ap.add_argument("--cpu-budget", type=float, default=15.0)

@@ -2400,7 +2400,9 @@ template <class S> struct GemmRun {
     std::string run() {
         typedef typename S::value_type T;
         if (m == 0 || n == 0) return "";
-        if constexpr (std::is_same<S, PlusProd<double>>::value) {   // (+, x) over doubles: the matrix cores
+        // (+, x) over doubles: the matrix cores (PP_GEMM_VALU=1 selects the VALU tile kernel instead, for comparison)
+        static const bool valu = std::getenv("PP_GEMM_VALU") != nullptr;
+        if constexpr (std::is_same<S, PlusProd<double>>::value) if (!valu) {
             dim3 g((unsigned)((m + 63) / 64), (unsigned)((n + 63) / 64));
             k_gemm_mfma64<double><<<g, 256, 0, ctx->stream>>>((double *)C, ldc, (const double *)A, lda,
                                                               (const double *)B, ldb, m, n, k);
