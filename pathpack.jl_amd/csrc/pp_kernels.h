@@ -1555,12 +1555,34 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
         if (r >= lo && r + 4 <= hi) return 2;
         return (r + 4 <= lo || r >= hi) ? 0 : 1;
     };
+    // PlusProd over doubles runs on the fp64 matrix cores: each wave takes 32 rows x BN / 2 columns as 2 x NBJ
+    // products of 16 x 16, computed transposed (C^T = Bpack^T X^T), so that lane l holds rows r0 + wr + 16 bi + l % 16
+    // of the columns wc + 16 bj + 4 r + l / 16: sixteen consecutive rows of a column per access
+    constexpr bool MF = std::is_same<S, PlusProd<double>>::value;
+    static_assert(!MF || BM == 64, "matrix-core tiles are 64 rows");
+    constexpr int NBJ = MF ? BN / 32 : 1;
+    const int lane = tid & 63, li = lane & 15, lq = lane >> 4;
+    const int wr = ((tid >> 6) & 1) * 32, wc = (tid >> 7) * (BN / 2);
+    v4d macc[2][NBJ];
+    if constexpr (MF) {
+#pragma unroll
+        for (int bi = 0; bi < 2; bi++) {
+            const i64 row = r0 + wr + 16 * bi + li;
+#pragma unroll
+            for (int bj = 0; bj < NBJ; bj++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int t = ct * BN + wc + 16 * bj + 4 * r + lq;
+                    macc[bi][bj][r] = (FWD && row >= lo && row < hi && t < e) ? X[row + (i64)E[t] * ld] : 0.0;
+                }
+        }
+    }
     T acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = S::zero();
-    if (FWD) {
+    if (FWD && !MF) {
 #pragma unroll
         for (int g = 0; g < TM / 4; g++) {
             const int st = rows_in(g);
@@ -1597,6 +1619,20 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
     for (int k0 = kbeg; k0 < kend; k0 += BK) {
         const bool more = k0 + BK < kend;
         if (more) gload(k0 + BK);
+        if constexpr (MF) {
+#pragma unroll
+            for (int kk = 0; kk < BK; kk += 4) {
+                double af[2], bf[NBJ];
+#pragma unroll
+                for (int bi = 0; bi < 2; bi++) af[bi] = As[buf][kk + lq][wr + 16 * bi + li];
+#pragma unroll
+                for (int bj = 0; bj < NBJ; bj++) bf[bj] = Bs[buf][kk + lq][wc + 16 * bj + li];
+#pragma unroll
+                for (int bi = 0; bi < 2; bi++)
+#pragma unroll
+                    for (int bj = 0; bj < NBJ; bj++) macc[bi][bj] = mfma_f64_16x16x4(bf[bj], af[bi], macc[bi][bj]);
+            }
+        } else
 #pragma unroll 2
         for (int kk = 0; kk < BK; kk += 2) {
             T a0[TM], a1[TM], b0[TN], b1[TN];
@@ -1619,6 +1655,30 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
         if (more) sstore(buf ^ 1, k0 + BK);
         __syncthreads();
         buf ^= 1;
+    }
+    if constexpr (MF) {
+#pragma unroll
+        for (int bi = 0; bi < 2; bi++) {
+            const i64 row = r0 + wr + 16 * bi + li;
+            if (row < lo || row >= hi) continue;
+#pragma unroll
+            for (int bj = 0; bj < NBJ; bj++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int cc = wc + 16 * bj + 4 * r + lq;
+                    i64 col;
+                    if (FWD) {
+                        const int t = ct * BN + cc;
+                        if (t >= e) continue;
+                        col = E[t];
+                    } else {
+                        if (cc >= w) continue;
+                        col = c0 + cc;
+                    }
+                    X[row + col * ld] = macc[bi][bj][r];
+                }
+        }
+        return;
     }
 #pragma unroll
     for (int g = 0; g < TM / 4; g++) {
