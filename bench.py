@@ -158,14 +158,16 @@ def bench_mstar(args):
     # repeated weights on one pattern (copyto! + lu! + Matrix, the plan idiom): the analysis, the plans and the
     # factor's buffers are reused; each step refactorizes from values in HBM and assembles the star (not `value`)
     import ctypes
-    Fp = factor_device(P.MinPlus(), sym, dnz, ctx)
+    Tp = None
+    if args.plan:
+        Fp = factor_device(P.MinPlus(), sym, dnz, ctx)
 
-    def plan_step():
-        ctx.check(P.lib().pp_refactor(ctx.handle, Fp.handle, ctypes.c_void_p(dnz.ptr), 1))
-        P.Matrix(Fp, out=out)
+        def plan_step():
+            ctx.check(P.lib().pp_refactor(ctx.handle, Fp.handle, ctypes.c_void_p(dnz.ptr), 1))
+            P.Matrix(Fp, out=out)
 
-    Tp = timed(plan_step, ctx, args.steps, 1)
-    del Fp
+        Tp = timed(plan_step, ctx, args.steps, 1)
+        del Fp
     if cfg == 3:
         metric = "mstar sec + semiring Gop/s, MinPlus 3D grid n=32768; % VALU/HBM roofline"
         workload = (f"MinPlus mstar, directed 32x32x32 grid, n=32768, 6-neighbour arcs both ways, "
@@ -192,9 +194,10 @@ def bench_mstar(args):
                    "madds_executed": st["madds_factor"] + st["madds_star"], "nnzL_alg": st["nnzL_alg"],
                    "mstar_s": round(T, 5)},
         "phases_ms": {k: round(v * 1e3, 3) for k, v in ph.items()},
-        "plan": {"ms_per_step": round(Tp * 1e3, 3), "semiring_Gops": round(madds / Tp / 1e9, 2),
-                 "step": "pp_refactor (new values of the same pattern, in HBM) + pp_star; analysis reused"},
     }
+    if Tp is not None:
+        result["plan"] = {"ms_per_step": round(Tp * 1e3, 3), "semiring_Gops": round(madds / Tp / 1e9, 2),
+                          "step": "pp_refactor (new values of the same pattern, in HBM) + pp_star; analysis reused"}
     if args.timing and cfg == 3:
         # dominant kernel family: the X <- X L* sweep (k_blk backward, k_sweep_bwd, k_sub backward), timed with HIP
         # events around all its launches on the context's stream; algorithmic work n * nnz(L) madds
@@ -453,6 +456,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="3", choices=["1", "2a", "2b", "3", "4", "5"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-plan", dest="plan", action="store_false",
+                    help="configurations 1 and 3: skip the repeated-weights (pp_refactor + pp_star) timing")
     ap.add_argument("--semiring", default="minplus", choices=["minplus", "plusprod"],
                     help="configuration 2a only: MinPlus Float32 (default) or PlusProd Float64 (fp64 matrix cores)")
     ap.add_argument("--ordering", default="nd", choices=["nd", "amd"],

@@ -929,24 +929,6 @@ __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(siz
     const int32_t *E = a.Eidx + a.p_eoff[p];
     const T *D = Dpack + a.p_doff[p];
     T acc[W];
-#pragma unroll
-    for (int j = 0; j < W; j++) acc[j] = S::zero();
-    if (q == 0 && (!a.init_lo || (r >= a.init_lo[p] && r < a.init_hi[p]))) {
-        // the panel's columns as the forward sweep left them, unsolved: finish its step x <- x D* here
-#pragma unroll
-        for (int j = 0; j < W; j++) {
-            const T v = xr[(i64)(c0 + min(j, w - 1)) * ld];
-            acc[j] = j < w ? v : S::zero();
-        }
-#pragma unroll
-        for (int j = 0; j < W; j++) {
-            T s = acc[j];
-#pragma unroll
-            for (int i = 0; i < j; i++) s = S::muladd(acc[i], DMODE == 0 ? D[i + j * W] : D[j + i * W], s);
-            if (DMODE == 0 && !S::integral) s = S::prod(s, S::star(D[j + j * W]));
-            acc[j] = s;
-        }
-    }
     // this wave's share of the gather list, in groups of four columns, with the next BWD_NSET - 1 groups' loads in
     // flight (register sets used in rotation, so no copy waits on a load); the lookahead reads up to
     // 4 (BWD_NSET - 1) entries past the share, into the following lists or the zero padding after the last one
@@ -968,10 +950,32 @@ __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(siz
         }
     };
     const int ngw = g1 - g0;
+    // the first groups are issued before wave 0 loads the panel's own columns (not among the gathered ones), so
+    // that the two loads' latencies overlap
+    T xs[BWD_NSET][4];
     if (ngw > 0) {
-        T xs[BWD_NSET][4];
 #pragma unroll
         for (int u = 0; u + 1 < BWD_NSET; u++) ld4(ep + 4 * u, xs[u]);
+    }
+#pragma unroll
+    for (int j = 0; j < W; j++) acc[j] = S::zero();
+    if (q == 0 && (!a.init_lo || (r >= a.init_lo[p] && r < a.init_hi[p]))) {
+        // the panel's columns as the forward sweep left them, unsolved: finish its step x <- x D* here
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            const T v = xr[(i64)(c0 + min(j, w - 1)) * ld];
+            acc[j] = j < w ? v : S::zero();
+        }
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            T s = acc[j];
+#pragma unroll
+            for (int i = 0; i < j; i++) s = S::muladd(acc[i], DMODE == 0 ? D[i + j * W] : D[j + i * W], s);
+            if (DMODE == 0 && !S::integral) s = S::prod(s, S::star(D[j + j * W]));
+            acc[j] = s;
+        }
+    }
+    if (ngw > 0) {
         int g = 0;
         for (; g + BWD_NSET <= ngw; g += BWD_NSET) {
 #pragma unroll
@@ -1102,23 +1106,6 @@ __device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64
     const int32_t *E = a.Eidx + a.p_eoff[p];
     const T *xr = X + r;
     T acc[W];
-#pragma unroll
-    for (int j = 0; j < W; j++) acc[j] = S::zero();
-    if (r >= a.rowA_lo[p] && r < a.rowA_hi[p]) {
-#pragma unroll
-        for (int j = 0; j < W; j++) {
-            const T v = xr[(i64)(c0 + min(j, w - 1)) * ld];
-            acc[j] = j < w ? v : S::zero();
-        }
-#pragma unroll
-        for (int j = 0; j < W; j++) {
-            T s = acc[j];
-#pragma unroll
-            for (int i = 0; i < j; i++) s = S::muladd(acc[i], D[i + j * W], s);
-            if (!S::integral) s = S::prod(s, S::star(D[j + j * W]));
-            acc[j] = s;
-        }
-    }
     // gathers in groups of four, three register sets in rotation (eight loads in flight)
     auto ld4 = [&](int t0, T(&v)[4]) {
 #pragma unroll
@@ -1141,14 +1128,32 @@ __device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64
                 }
         }
     };
-    if (e > 0) {
-        // NS register sets of four in rotation: group g + NS - 1 is loaded while group g is multiplied (deeper
-        // rotations spill at the kernel's 80-register budget and run slower)
-        constexpr int NS = 3;
-        T xs[NS][4];
+    // NS register sets of four in rotation: group g + NS - 1 is loaded while group g is multiplied (deeper rotations
+    // spill at the kernel's 80-register budget and run slower).  The first groups are issued before the panel's own
+    // columns are loaded, so that the two loads' latencies overlap (the gathered columns are not the panel's own).
+    constexpr int NS = 3;
+    T xs[NS][4];
 #pragma unroll
-        for (int u = 0; u + 1 < NS; u++)
-            if (4 * u < e) ld4(4 * u, xs[u]);
+    for (int u = 0; u + 1 < NS; u++)
+        if (4 * u < e) ld4(4 * u, xs[u]);
+#pragma unroll
+    for (int j = 0; j < W; j++) acc[j] = S::zero();
+    if (r >= a.rowA_lo[p] && r < a.rowA_hi[p]) {
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            const T v = xr[(i64)(c0 + min(j, w - 1)) * ld];
+            acc[j] = j < w ? v : S::zero();
+        }
+#pragma unroll
+        for (int j = 0; j < W; j++) {
+            T s = acc[j];
+#pragma unroll
+            for (int i = 0; i < j; i++) s = S::muladd(acc[i], D[i + j * W], s);
+            if (!S::integral) s = S::prod(s, S::star(D[j + j * W]));
+            acc[j] = s;
+        }
+    }
+    if (e > 0) {
         int t0 = 0;
         for (; t0 + 4 * NS <= e; t0 += 4 * NS) {
 #pragma unroll
