@@ -749,8 +749,15 @@ __device__ inline int search(const int32_t *pre, int np, int u) {
 
 // X[addr] <- X[addr] (+) v by compare-and-swap on the bit pattern; returns at once when (+) leaves the value
 // unchanged (the common case for min / max / or).  Exact and order-independent for the idempotent semirings.
+// PlusProd uses the hardware's atomic add (order-dependent rounding, as any parallel sum).
 template <class S> __device__ inline void atomic_plus(typename S::value_type *addr, typename S::value_type v) {
     typedef typename S::value_type T;
+    if constexpr (std::is_same<S, PlusProd<T>>::value) {
+        // (+) is the hardware's floating-point atomic add; a zero term changes nothing (unit right-hand sides make
+        // many of them)
+        if (v != T(0)) unsafeAtomicAdd(addr, v);
+        return;
+    }
     typedef typename std::conditional<sizeof(T) == 8, unsigned long long, unsigned int>::type U;
     U *a = reinterpret_cast<U *>(addr);
     U old = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
