@@ -23,8 +23,10 @@
  *   - Every function returns a pp_status; on failure pp_last_error(ctx) (or pp_last_error(NULL) for the functions
  *     without a context) returns a message.  Nothing aborts and nothing throws across the ABI.  Sizes are
  *     checked against free device memory before any work is launched (PP_ENOMEM).
- *   - A pp_ctx owns one HIP stream on one device and every device buffer it allocates.  A context must not be
- *     used by two threads at once; distinct contexts are independent.
+ *   - A pp_ctx owns one HIP stream on one device and every device buffer it allocates.  Every result a call
+ *     leaves in device memory is ordered on that stream.  (The packs of the star's large fronts are built on a
+ *     second, internal stream overlapped with the start of the star; the library orders its own readers and
+ *     writers of them.)  A context must not be used by two threads at once; distinct contexts are independent.
  *   - Host buffers passed in are borrowed for the duration of the call.
  */
 #ifndef PATHPACK_HIP_H
@@ -80,7 +82,7 @@ pp_status pp_init(pp_ctx **ctx, int device);
 pp_status pp_destroy(pp_ctx *ctx);
 /* Message of the last failure on ctx; with ctx == NULL, of the calling thread's last context-free call. */
 const char *pp_last_error(const pp_ctx *ctx);
-/* Wait for all work queued on the context's stream. */
+/* Wait for all work queued on the context's streams. */
 pp_status pp_synchronize(pp_ctx *ctx);
 /* The context's HIP stream (hipStream_t) as an opaque pointer, for callers that order their own work after it. */
 pp_status pp_stream(pp_ctx *ctx, void **stream);

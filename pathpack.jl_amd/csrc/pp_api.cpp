@@ -51,6 +51,32 @@ static bool supported(int semiring, int dtype) {
     return false;
 }
 
+// Free device memory for the size checks: the driver's free memory plus what the default pool holds cached (freed
+// stream-ordered allocations, which pp_init keeps in the pool for the next call).
+static hipError_t mem_free(pp_ctx *ctx, size_t *freeb, size_t *totalb) {
+    hipError_t e = hipMemGetInfo(freeb, totalb);
+    if (e != hipSuccess) return e;
+    hipMemPool_t pool = nullptr;
+    uint64_t res = 0, used = 0;
+    if (hipDeviceGetDefaultMemPool(&pool, ctx->device) == hipSuccess && pool &&
+        hipMemPoolGetAttribute(pool, hipMemPoolAttrReservedMemCurrent, &res) == hipSuccess &&
+        hipMemPoolGetAttribute(pool, hipMemPoolAttrUsedMemCurrent, &used) == hipSuccess && res > used)
+        *freeb += (size_t)(res - used);
+    return hipSuccess;
+}
+
+// hipMalloc outside the pool: when the driver is short, the pool's cached memory is returned to it first
+static hipError_t dev_malloc(pp_ctx *ctx, void **p, size_t bytes) {
+    hipError_t e = hipMalloc(p, bytes);
+    if (e == hipSuccess) return e;
+    (void)hipGetLastError();
+    hipStreamSynchronize(ctx->stream);
+    hipStreamSynchronize(ctx->aux_stream);
+    hipMemPool_t pool = nullptr;
+    if (hipDeviceGetDefaultMemPool(&pool, ctx->device) == hipSuccess && pool) hipMemPoolTrimTo(pool, 0);
+    return hipMalloc(p, bytes);
+}
+
 extern "C" {
 
 // The host analysis allocates a few dozen arrays of n or nnz elements per call.  glibc serves blocks above its mmap
@@ -89,9 +115,25 @@ pp_status pp_init(pp_ctx **out, int device) {
     }
     for (auto &e : ctx->ev)
         if (hipEventCreate(&e) != hipSuccess) {
-            delete ctx;
+            pp_destroy(ctx);
             return fail(nullptr, PP_EHIP, "pp_init: hipEventCreate failed");
         }
+    {
+        // stream-ordered allocations (fronts, the n x n star buffer, scratch) come from the device's default pool;
+        // keep what is freed there for the next call instead of returning it to the driver at every
+        // synchronization (re-mapping the 4 GB star buffer of a 32768-vertex graph costs about a millisecond)
+        hipMemPool_t pool = nullptr;
+        if (hipDeviceGetDefaultMemPool(&pool, device) == hipSuccess && pool) {
+            uint64_t keep = UINT64_MAX;
+            hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+        }
+    }
+    if (hipStreamCreateWithFlags(&ctx->aux_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&ctx->aux_from, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&ctx->aux_done, hipEventDisableTiming) != hipSuccess) {
+        pp_destroy(ctx);
+        return fail(nullptr, PP_EHIP, "pp_init: creating the second stream failed");
+    }
     *out = ctx;
     return PP_OK;
 }
@@ -99,6 +141,12 @@ pp_status pp_init(pp_ctx **out, int device) {
 pp_status pp_destroy(pp_ctx *ctx) {
     if (!ctx) return PP_OK;
     hipSetDevice(ctx->device);
+    if (ctx->aux_stream) {
+        hipStreamSynchronize(ctx->aux_stream);
+        hipStreamDestroy(ctx->aux_stream);
+    }
+    if (ctx->aux_from) hipEventDestroy(ctx->aux_from);
+    if (ctx->aux_done) hipEventDestroy(ctx->aux_done);
     if (ctx->stream) {
         hipStreamSynchronize(ctx->stream);
         hipStreamDestroy(ctx->stream);
@@ -115,6 +163,11 @@ pp_status pp_destroy(pp_ctx *ctx) {
         if (e) hipEventDestroy(e);
     for (auto &p : ctx->outpin)
         if (p) hipHostFree(p);
+    {
+        // give the pool's cached memory back (other contexts on the device allocate again as they need)
+        hipMemPool_t pool = nullptr;
+        if (hipDeviceGetDefaultMemPool(&pool, ctx->device) == hipSuccess && pool) hipMemPoolTrimTo(pool, 0);
+    }
     delete ctx;
     return PP_OK;
 }
@@ -124,6 +177,7 @@ const char *pp_last_error(const pp_ctx *ctx) { return ctx ? ctx->err.c_str() : g
 pp_status pp_synchronize(pp_ctx *ctx) {
     if (!ctx) return fail(nullptr, PP_EINVAL, "pp_synchronize: null context");
     CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    CHECK_HIP(ctx, hipStreamSynchronize(ctx->aux_stream));
     return PP_OK;
 }
 
@@ -312,7 +366,7 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
                         sizeof(int32_t) * (P.stask.size() + P.flist.size() + P.atask.size() + P.etask.size() +
                                            P.relpos.size());
     size_t freeb = 0, totalb = 0;
-    if (hipMemGetInfo(&freeb, &totalb) != hipSuccess) return failj(PP_EHIP, "pp_factor: hipMemGetInfo failed");
+    if (mem_free(ctx, &freeb, &totalb) != hipSuccess) return failj(PP_EHIP, "pp_factor: hipMemGetInfo failed");
     if (need > freeb)
         return failj(PP_ENOMEM, "pp_factor: needs " + std::to_string(need) + " bytes of device memory, " +
                                     std::to_string(freeb) + " free");
@@ -409,7 +463,7 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     const size_t plan2 = u2.total;
     const size_t oD = u2.place(W.ndpack * es), oU = u2.place(W.npack * es), oL = u2.place(W.npack * es);
     const size_t oB = u2.place(W.nbpack * es), oH = u2.place(W.nhpack * es);
-    if (hipMemGetInfo(&freeb, &totalb) != hipSuccess) return failf(PP_EHIP, "pp_factor: hipMemGetInfo failed");
+    if (mem_free(ctx, &freeb, &totalb) != hipSuccess) return failf(PP_EHIP, "pp_factor: hipMemGetInfo failed");
     if (u2.total > freeb)
         return failf(PP_ENOMEM, "pp_factor: the sweep packs need " + std::to_string(u2.total) + " bytes of device memory, " +
                                     std::to_string(freeb) + " free");
@@ -452,7 +506,7 @@ pp_status pp_refactor(pp_ctx *ctx, pp_fac *fac, const void *nzval, int on_device
     const size_t need = es * ((size_t)fac->sym->fplan->arena + (on_device ? 0 : (size_t)S.nnz) +
                               (size_t)W.nb * 2 * pp::BLK_W * pp::BLK_W);
     size_t freeb = 0, totalb = 0;
-    CHECK_HIP(ctx, hipMemGetInfo(&freeb, &totalb));
+    CHECK_HIP(ctx, mem_free(ctx, &freeb, &totalb));
     if (need > freeb)
         return fail(ctx, PP_ENOMEM, "pp_refactor: needs " + std::to_string(need) + " bytes of device memory, " +
                                         std::to_string(freeb) + " free");
@@ -494,6 +548,7 @@ pp_status pp_fac_destroy(pp_fac *fac) {
     if (!fac) return PP_OK;
     hipSetDevice(fac->ctx->device);
     hipStreamSynchronize(fac->ctx->stream);
+    hipStreamSynchronize(fac->ctx->aux_stream);
     delete fac;
     return PP_OK;
 }
@@ -507,7 +562,7 @@ pp_status pp_star(pp_ctx *ctx, const pp_fac *fac, void *out, int64_t ldc, int ou
     CHECK_HIP(ctx, hipSetDevice(ctx->device));
     const size_t es = (size_t)pp::dtype_size(fac->dtype);
     size_t freeb = 0, totalb = 0;
-    CHECK_HIP(ctx, hipMemGetInfo(&freeb, &totalb));
+    CHECK_HIP(ctx, mem_free(ctx, &freeb, &totalb));
     // the star buffer X, plus two column chunks of at most STAR_CHUNK_BYTES each when the output is in host memory
     const size_t need = (size_t)n * n * es + (out_on_device ? 0 : 2 * (size_t)pp::STAR_CHUNK_BYTES + 2 * (size_t)n * es);
     if (need > freeb)
@@ -566,17 +621,17 @@ pp_status pp_star_sources(pp_ctx *ctx, const pp_fac *fac, int which, int64_t nsr
     add(R.sub_preB, &R.d_sub_preB);
     add(pos, &R.d_pos);
     size_t freeb = 0, totalb = 0;
-    CHECK_HIP(ctx, hipMemGetInfo(&freeb, &totalb));
+    CHECK_HIP(ctx, mem_free(ctx, &freeb, &totalb));
     const size_t need = (size_t)m * n * es + blk.size() * sizeof(int32_t) + (out_on_device ? 0 : bytesO);
     if (need > freeb)
         return fail(ctx, PP_ENOMEM, "pp_star_sources: needs " + std::to_string(need) + " bytes of device memory, " +
                                         std::to_string(freeb) + " free");
     void *dblk = nullptr;
-    CHECK_HIP(ctx, hipMalloc(&dblk, blk.size() * sizeof(int32_t)));
+    CHECK_HIP(ctx, dev_malloc(ctx, &dblk, blk.size() * sizeof(int32_t)));
     for (auto &w : where) *w.first = (int32_t *)dblk + w.second;
     void *dO = out;
     hipError_t ue = hipMemcpy(dblk, blk.data(), blk.size() * sizeof(int32_t), hipMemcpyHostToDevice);
-    if (ue == hipSuccess && !out_on_device) ue = hipMalloc(&dO, bytesO);
+    if (ue == hipSuccess && !out_on_device) ue = dev_malloc(ctx, &dO, bytesO);
     if (ue != hipSuccess) {
         hipFree(dblk);
         return fail(ctx, PP_EHIP, std::string("pp_star_sources: ") + hipGetErrorString(ue));
@@ -602,12 +657,12 @@ static pp_status solve(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int
     const size_t es = (size_t)pp::dtype_size(fac->dtype);
     const size_t bytesB = (size_t)ldb * (size_t)(left ? nrhs : n) * es;
     size_t freeb = 0, totalb = 0;
-    CHECK_HIP(ctx, hipMemGetInfo(&freeb, &totalb));
+    CHECK_HIP(ctx, mem_free(ctx, &freeb, &totalb));
     const size_t need = (size_t)n * nrhs * es + (on_device ? 0 : bytesB);
     if (need > freeb) return fail(ctx, PP_ENOMEM, std::string(name) + ": not enough device memory");
     void *dB = B;
     if (!on_device) {
-        CHECK_HIP(ctx, hipMalloc(&dB, bytesB));
+        CHECK_HIP(ctx, dev_malloc(ctx, &dB, bytesB));
         hipError_t ue = hipMemcpy(dB, B, bytesB, hipMemcpyHostToDevice);
         if (ue != hipSuccess) {
             hipFree(dB);
@@ -666,9 +721,9 @@ pp_status pp_buffer_alloc(pp_ctx *ctx, size_t bytes, void **dptr) {
     if (!ctx || !dptr) return fail(ctx, PP_EINVAL, "pp_buffer_alloc: null argument");
     CHECK_HIP(ctx, hipSetDevice(ctx->device));
     size_t freeb = 0, totalb = 0;
-    CHECK_HIP(ctx, hipMemGetInfo(&freeb, &totalb));
+    CHECK_HIP(ctx, mem_free(ctx, &freeb, &totalb));
     if (bytes > freeb) return fail(ctx, PP_ENOMEM, "pp_buffer_alloc: not enough device memory");
-    if (hipMalloc(dptr, std::max<size_t>(1, bytes)) != hipSuccess) return fail(ctx, PP_ENOMEM, "pp_buffer_alloc: hipMalloc failed");
+    if (dev_malloc(ctx, dptr, std::max<size_t>(1, bytes)) != hipSuccess) return fail(ctx, PP_ENOMEM, "pp_buffer_alloc: hipMalloc failed");
     return PP_OK;
 }
 

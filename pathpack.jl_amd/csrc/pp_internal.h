@@ -48,7 +48,7 @@
 namespace pp {
 
 constexpr int SMALL_NJ = 64;   // fronts up to this size are factorized in one workgroup's LDS
-constexpr int ASM_BLOCK = 16;  // parent columns per extend-add workgroup
+constexpr int ASM_BLOCK = 16;  // parent columns per extend-add workgroup (at most; 4 at least)
 constexpr int EXTRACT_COLS = 32;  // frontal columns per factor-extraction workgroup
 constexpr int EIDX_PAD = 32;      // zero entries after the last gather list: sweeps read up to 16 entries ahead
 constexpr int NB = 32;         // pivot block of the blocked front factorization
@@ -84,6 +84,7 @@ struct FactorPlan {
     };
     struct Level {
         i64 asm_off, asm_cnt;        // extend-add tasks (front, first parent column) in atask
+        int32_t asm_blk;             // parent columns per extend-add task (ASM_BLOCK, or fewer on a narrow level)
         i64 small_off, small_cnt;    // fronts with nj <= SMALL_NJ, in flist
         std::vector<Step> steps;     // blocked steps for the larger fronts
     };
@@ -201,6 +202,12 @@ struct pp_ctx {
     // chunk buffers (kept between calls)
     hipStream_t copy_stream = nullptr;
     hipEvent_t pev[4] = {};
+    // the star blocks' packs are built on a second stream, overlapped with the start of the star: aux_from orders
+    // them after the factorization, aux_done orders every later reader (block GEMMs) and writer (the next
+    // factorization of the same buffers) after them
+    hipStream_t aux_stream = nullptr;
+    hipEvent_t aux_from = nullptr, aux_done = nullptr;
+    bool aux_pending = false;        // aux_done is recorded
     void *outpin[2] = {nullptr, nullptr};
     size_t outpin_bytes = 0;
 };

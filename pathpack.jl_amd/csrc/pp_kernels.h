@@ -81,7 +81,8 @@ __global__ __launch_bounds__(NT) void k_identity_panels(typename S::value_type *
 
 // ===== extend-add: F_f <- F_f (+) inj M_c inj^T for every child c (sgetrf_send!, chordal/sgetrf.jl:257-290) =====
 //
-// One workgroup per (parent front, block of ASM_BLOCK parent columns).  A child's map into its parent's bag (relpos)
+// One workgroup per (parent front, block of `blk` parent columns; blk = ASM_BLOCK, or down to 4 on a level with few
+// parent columns).  A child's map into its parent's bag (relpos)
 // is increasing, so the child columns landing in the block are a contiguous range found by binary search; blocks of
 // one parent never write the same entry, and the children of a parent are added one after another.
 template <class S>
@@ -89,11 +90,12 @@ __global__ __launch_bounds__(NT) void k_assemble(typename S::value_type *__restr
                                                  const int32_t *__restrict__ nn, const int32_t *__restrict__ na,
                                                  const int32_t *__restrict__ nj, const i64 *__restrict__ Sptr,
                                                  const int32_t *__restrict__ relpos, const int32_t *__restrict__ chptr,
-                                                 const int32_t *__restrict__ chidx, const int32_t *__restrict__ tasks) {
+                                                 const int32_t *__restrict__ chidx, const int32_t *__restrict__ tasks,
+                                                 int blk) {
     typedef typename S::value_type T;
     const int f = tasks[2 * blockIdx.x], a = tasks[2 * blockIdx.x + 1];
     const int ldf = nj[f];
-    const int b = min(ldf, a + ASM_BLOCK);
+    const int b = min(ldf, a + blk);
     T *Ff = F + Foff[f];
     for (int q = chptr[f]; q < chptr[f + 1]; q++) {
         const int c = chidx[q];
@@ -113,7 +115,23 @@ __global__ __launch_bounds__(NT) void k_assemble(typename S::value_type *__restr
         for (int w = lo + wave; w < w1; w += NT / 64) {
             T *dcol = Ff + (i64)rp[w] * ldf;
             const T *scol = M + (i64)w * ldc;
-            for (int v = lane; v < nc; v += 64) dcol[rp[v]] = S::plus(dcol[rp[v]], scol[v]);
+            // four rows per lane in flight: every load of a batch is issued before its stores (the rows of one child
+            // column land on distinct parent rows, and the child's update block does not overlap the parent front)
+            int v = lane;
+            for (; v + 192 < nc; v += 256) {
+                int q[4];
+                T x[4], y[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    q[u] = rp[v + 64 * u];
+                    x[u] = scol[v + 64 * u];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) y[u] = dcol[q[u]];
+#pragma unroll
+                for (int u = 0; u < 4; u++) dcol[q[u]] = S::plus(y[u], x[u]);
+            }
+            for (; v < nc; v += 64) dcol[rp[v]] = S::plus(dcol[rp[v]], scol[v]);
         }
         __syncthreads();
     }
@@ -1911,6 +1929,8 @@ template <class S> struct FactorRun {
         const FactorPlan &P = *fac->sym->fplan;
         const DevPlan &d = fac->plan;
         hipStream_t st = ctx->stream;
+        // the previous star blocks' packs read the factor buffers this run overwrites
+        if (ctx->aux_pending) HIPCHK(hipStreamWaitEvent(st, ctx->aux_done, 0));
         timer_start(ctx, 0);
         T *F = nullptr;
         HIPCHK(hipMallocAsync((void **)&F, std::max<i64>(1, P.arena) * sizeof(T), st));
@@ -1922,7 +1942,7 @@ template <class S> struct FactorRun {
         for (const auto &L : P.levels) {
             if (L.asm_cnt)
                 k_assemble<S><<<(unsigned)L.asm_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.na, d.nj, d.Sptr, d.relpos, d.chptr,
-                                                                 d.chidx, d.atask + 2 * L.asm_off);
+                                                                 d.chidx, d.atask + 2 * L.asm_off, L.asm_blk);
             if (L.small_cnt)
                 k_front_small<S, SMALL_NJ><<<(unsigned)L.small_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.nj,
                                                                                   d.flist + L.small_off);
@@ -1959,20 +1979,28 @@ template <class S> struct PacksRun {
                                                             (T *)fac->Upack, (T *)fac->Lpack);
         LAUNCHCHK();
         if (W.nb > 0) {
-            // star blocks: L_bb*, U_bb* into a scratch, then the GEMM packs (zero padding first)
+            // star blocks: L_bb*, U_bb* into a scratch, then the GEMM packs (zero padding first).  They run on the
+            // second stream, after everything queued so far (the factorization, and any earlier star still reading
+            // the packs), while the star's first launches (identity, small subtrees, panels) need only the panel
+            // packs; block GEMMs and the next factorization wait for aux_done.
+            hipStream_t as = ctx->aux_stream;
+            HIPCHK(hipEventRecord(ctx->aux_from, st));
+            HIPCHK(hipStreamWaitEvent(as, ctx->aux_from, 0));
             T *stars = nullptr;
-            HIPCHK(hipMallocAsync((void **)&stars, (size_t)W.nb * 2 * BLK_W * BLK_W * sizeof(T), st));
-            k_fill<T><<<grid1(W.nbpack), NT, 0, st>>>((T *)fac->Bpack, W.nbpack, S::zero());
-            if (W.nhpack) k_fill<T><<<grid1(W.nhpack), NT, 0, st>>>((T *)fac->Hpack, W.nhpack, S::zero());
-            k_blk_stars<S><<<(unsigned)W.nb, NT, 0, st>>>((const T *)fac->LD, d.Dptr, d.nn, d.Rptr, d.p_front, d.p_c0,
+            HIPCHK(hipMallocAsync((void **)&stars, (size_t)W.nb * 2 * BLK_W * BLK_W * sizeof(T), as));
+            k_fill<T><<<grid1(W.nbpack), NT, 0, as>>>((T *)fac->Bpack, W.nbpack, S::zero());
+            if (W.nhpack) k_fill<T><<<grid1(W.nhpack), NT, 0, as>>>((T *)fac->Hpack, W.nhpack, S::zero());
+            k_blk_stars<S><<<(unsigned)W.nb, NT, 0, as>>>((const T *)fac->LD, d.Dptr, d.nn, d.Rptr, d.p_front, d.p_c0,
                                                           d.p_w, (int)W.np, stars);
             if (W.prep.size())
-                k_blk_prep<S><<<(unsigned)(W.prep.size() / 4), NT, 0, st>>>(
+                k_blk_prep<S><<<(unsigned)(W.prep.size() / 4), NT, 0, as>>>(
                     (const T *)fac->LD, (const T *)fac->LL, (const T *)fac->UL, d.Dptr, d.Lptr, d.nn, d.nj, d.Rptr,
                     d.p_front, d.p_c0, d.p_w, d.p_e, d.p_lo, (int)W.np, d.prep, stars, d.b_boff, d.b_hoff, d.b_ep,
                     d.b_bn, (T *)fac->Bpack, (T *)fac->Hpack);
             LAUNCHCHK();
-            HIPCHK(hipFreeAsync(stars, st));
+            HIPCHK(hipFreeAsync(stars, as));
+            HIPCHK(hipEventRecord(ctx->aux_done, as));
+            ctx->aux_pending = true;
         }
         timer_stop(ctx, 0);
         return "";
@@ -2149,8 +2177,14 @@ static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmod
         subtrees();
         LAUNCHCHK();
     }
+    bool packs_ready = !ctx->aux_pending;
     for (const auto &li : lists) {
         if (li.cls >= BLK_CLS) {
+            if (!packs_ready) {
+                // the block packs come from the second stream
+                if (hipStreamWaitEvent(st, ctx->aux_done, 0) != hipSuccess) return "hipStreamWaitEvent failed";
+                packs_ready = true;
+            }
             launch_blocks<S>(ctx, fac, fwd, X, ld, nrows, li, rs);
             LAUNCHCHK();
             continue;

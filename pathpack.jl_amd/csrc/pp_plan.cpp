@@ -96,9 +96,17 @@ std::string build_factor_plan(const Symbolic &S, FactorPlan &P) {
     for (i64 l = 0; l < H; l++) {
         FactorPlan::Level L;
         L.asm_off = (i64)P.atask.size() / 2;
+        // narrower column blocks while the level has fewer than four tasks per compute unit (the upper levels: few
+        // parents with large update matrices), down to one column per wave
+        i64 ncols = 0;
+        for (int32_t f : byh[l])
+            if (P.chptr[f + 1] > P.chptr[f]) ncols += P.nj[f];
+        int32_t blk = ASM_BLOCK;
+        while (blk > 4 && ncols / blk < 1024) blk /= 2;
+        L.asm_blk = blk;
         for (int32_t f : byh[l])
             if (P.chptr[f + 1] > P.chptr[f])
-                for (int32_t a = 0; a < P.nj[f]; a += ASM_BLOCK) {
+                for (int32_t a = 0; a < P.nj[f]; a += blk) {
                     P.atask.push_back(f);
                     P.atask.push_back(a);
                 }
