@@ -6,7 +6,7 @@
  * file:line in AlgebraicJulia/PATHPACK.jl):
  *
  *   mlu(s, A; alg)        src/CPU/abstract_slu.jl:44-48      -> pp_symbolic + pp_factor
- *   mstar(s, A; alg)      src/CPU/abstract_slu.jl:85-87      -> pp_symbolic + pp_factor + pp_star
+ *   mstar(s, A; alg)      src/CPU/abstract_slu.jl:85-87      -> pp_symbolic + pp_mstar (= pp_factor + pp_star)
  *   Matrix(F)             src/CPU/abstract_slu.jl:10-14      -> pp_star
  *   copyto!(F, A); lu!(F) src/CPU/chordal_slu.jl:116, abstract_slu.jl:119 -> pp_refactor
  *   sgetre! (many k)      src/CPU/chordal_slu.jl:445-493     -> pp_star_sources   (rows / columns of A*)
@@ -139,6 +139,12 @@ pp_status pp_fac_destroy(pp_fac *fac);
  * out_on_device != 0, else a host pointer (the star is assembled in HBM, then copied back).  Replaces sgetri!(F, C)
  * (src/CPU/chordal_slu.jl:501-513 -> chordal/sgetri.jl:13-31, utils.jl:261-505). */
 pp_status pp_star(pp_ctx *ctx, const pp_fac *fac, void *out, int64_t ldc, int out_on_device);
+/* mstar: pp_factor then pp_star in one call, the star queued behind the factorization with no wait in between.
+ * Replaces mstar(s, A) = Matrix(mlu(s, A)) (src/CPU/abstract_slu.jl:85-87) after the symbolic analysis.  nzval is in
+ * host memory (nz_on_device == 0) or device memory; out and ldc as for pp_star.  fac_out may be NULL (the factor is
+ * freed before returning), else it receives the factor for later solves. */
+pp_status pp_mstar(pp_ctx *ctx, const pp_sym *sym, int semiring, int dtype, const void *nzval, int nz_on_device,
+                   void *out, int64_t ldc, int out_on_device, pp_fac **fac_out);
 /* Rows (which = 0) or columns (which = 1) of A* for the sources src[0..nsrc) (0-based original labels, in any
  * order, repeats allowed): rows: out (nsrc x n, ldo >= nsrc) row k <- row src[k] of A*; columns: out (n x nsrc,
  * ldo >= n) column k <- column src[k] of A*.  The sweeps visit, for each front, only the sources of its subtree

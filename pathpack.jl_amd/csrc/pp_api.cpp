@@ -316,8 +316,9 @@ struct Upload {
     }
 };
 
+// finish: wait for the factorization before returning (pp_factor); pp_mstar queues the star behind it instead
 static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, int dtype, const void *nzval,
-                               bool on_device, pp_fac **out) {
+                               bool on_device, pp_fac **out, bool finish = true) {
     if (!ctx) return fail(nullptr, PP_EINVAL, "pp_factor: null context");
     if (!csym || !out) return fail(ctx, PP_EINVAL, "pp_factor: null argument");
     *out = nullptr;
@@ -463,10 +464,8 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     const size_t plan2 = u2.total;
     const size_t oD = u2.place(W.ndpack * es), oU = u2.place(W.npack * es), oL = u2.place(W.npack * es);
     const size_t oB = u2.place(W.nbpack * es), oH = u2.place(W.nhpack * es);
-    if (mem_free(ctx, &freeb, &totalb) != hipSuccess) return failf(PP_EHIP, "pp_factor: hipMemGetInfo failed");
-    if (u2.total > freeb)
-        return failf(PP_ENOMEM, "pp_factor: the sweep packs need " + std::to_string(u2.total) + " bytes of device memory, " +
-                                    std::to_string(freeb) + " free");
+    // (no free-memory query here: the factorization is already queued and the query would wait for it; the packs'
+    // stream-ordered allocation reports a shortage itself)
     void *block2 = nullptr;
     e = u2.run(st, ctx->staging2, ctx->staging2_bytes, plan2, &block2);
     if (!e.empty()) return failf(PP_ENOMEM, "pp_factor: " + e);
@@ -477,7 +476,7 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     fac->Bpack = (char *)block2 + oB;
     fac->Hpack = (char *)block2 + oH;
     e = pp::device_factor_packs(ctx, fac);
-    hipError_t se = hipStreamSynchronize(st);
+    hipError_t se = finish ? hipStreamSynchronize(st) : hipGetLastError();
     if (!e.empty() || se != hipSuccess)
         return failf(PP_EHIP, "pp_factor: " + (e.empty() ? std::string(hipGetErrorString(se)) : e));
     *out = fac;
@@ -555,23 +554,73 @@ pp_status pp_fac_destroy(pp_fac *fac) {
 
 // ===== star and solves =====
 
+// Device memory the star needs: the star buffer X, plus two column chunks of at most STAR_CHUNK_BYTES each when the
+// output is in host memory
+static size_t star_bytes(i64 n, size_t es, int out_on_device) {
+    return (size_t)n * n * es + (out_on_device ? 0 : 2 * (size_t)pp::STAR_CHUNK_BYTES + 2 * (size_t)n * es);
+}
+
+static pp_status star_common(pp_ctx *ctx, const pp_fac *fac, void *out, int64_t ldc, int out_on_device, bool check);
+
 pp_status pp_star(pp_ctx *ctx, const pp_fac *fac, void *out, int64_t ldc, int out_on_device) {
     if (!ctx || !fac || !out) return fail(ctx, PP_EINVAL, "pp_star: null argument");
+    return star_common(ctx, fac, out, ldc, out_on_device, true);
+}
+
+// check: compare the star's memory with the free memory first (pp_mstar checks before it queues the factorization:
+// the query would wait for the queued work)
+static pp_status star_common(pp_ctx *ctx, const pp_fac *fac, void *out, int64_t ldc, int out_on_device, bool check) {
     const i64 n = fac->sym->S.n;
     if (ldc < n) return fail(ctx, PP_EINVAL, "pp_star: ldc < n");
     CHECK_HIP(ctx, hipSetDevice(ctx->device));
     const size_t es = (size_t)pp::dtype_size(fac->dtype);
     size_t freeb = 0, totalb = 0;
-    CHECK_HIP(ctx, mem_free(ctx, &freeb, &totalb));
-    // the star buffer X, plus two column chunks of at most STAR_CHUNK_BYTES each when the output is in host memory
-    const size_t need = (size_t)n * n * es + (out_on_device ? 0 : 2 * (size_t)pp::STAR_CHUNK_BYTES + 2 * (size_t)n * es);
-    if (need > freeb)
+    const size_t need = star_bytes(n, es, out_on_device);
+    if (check) CHECK_HIP(ctx, mem_free(ctx, &freeb, &totalb));
+    if (check && need > freeb) {
+        // work still queued (a factorization's fronts) may hold memory: wait for it and look again
+        CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        CHECK_HIP(ctx, hipStreamSynchronize(ctx->aux_stream));
+        CHECK_HIP(ctx, mem_free(ctx, &freeb, &totalb));
+    }
+    if (check && need > freeb)
         return fail(ctx, PP_ENOMEM, "pp_star: needs " + std::to_string(need) + " bytes of device memory, " +
                                         std::to_string(freeb) + " free");
     std::string e = pp::device_star(ctx, fac, out, ldc, out_on_device ? 0 : 1);
     hipError_t se = hipStreamSynchronize(ctx->stream);
     if (!e.empty() || se != hipSuccess)
         return fail(ctx, PP_EHIP, "pp_star: " + (e.empty() ? std::string(hipGetErrorString(se)) : e));
+    return PP_OK;
+}
+
+pp_status pp_mstar(pp_ctx *ctx, const pp_sym *sym, int semiring, int dtype, const void *nzval, int nz_on_device,
+                   void *out, int64_t ldc, int out_on_device, pp_fac **fac_out) {
+    if (fac_out) *fac_out = nullptr;
+    if (!ctx) return fail(nullptr, PP_EINVAL, "pp_mstar: null context");
+    if (!sym || !out) return fail(ctx, PP_EINVAL, "pp_mstar: null argument");
+    if (ldc < sym->S.n) return fail(ctx, PP_EINVAL, "pp_mstar: ldc < n");
+    if (!supported(semiring, dtype)) return fail(ctx, PP_EUNSUPPORTED, "pp_mstar: unsupported semiring / element type");
+    CHECK_HIP(ctx, hipSetDevice(ctx->device));
+    {
+        size_t freeb = 0, totalb = 0;
+        CHECK_HIP(ctx, mem_free(ctx, &freeb, &totalb));
+        const size_t need = star_bytes(sym->S.n, (size_t)pp::dtype_size(dtype), out_on_device);
+        if (need > freeb)
+            return fail(ctx, PP_ENOMEM, "pp_mstar: the star needs " + std::to_string(need) + " bytes of device memory, " +
+                                            std::to_string(freeb) + " free");
+    }
+    pp_fac *fac = nullptr;
+    // the factorization is queued without waiting for it; the star's launches follow it on the same stream
+    pp_status st = factor_common(ctx, sym, semiring, dtype, nzval, nz_on_device != 0, &fac, false);
+    if (st != PP_OK) return st;
+    st = star_common(ctx, fac, out, ldc, out_on_device, false);
+    if (st != PP_OK || !fac_out) {
+        const std::string msg = ctx->err;
+        pp_fac_destroy(fac);
+        ctx->err = msg;
+        return st;
+    }
+    *fac_out = fac;
     return PP_OK;
 }
 

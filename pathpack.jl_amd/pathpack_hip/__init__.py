@@ -440,9 +440,52 @@ def Matrix(F: Factorization, device: bool = False, out=None):
     return C
 
 
-def mstar(s: AbstractSemiring, A, alg=None, amalgamate: bool = True, device: bool = False):
-    """The star A* = I (+) A (+) A^2 (+) ... as a dense matrix (mstar, abstract_slu.jl:81-87)."""
-    return Matrix(mlu(s, A, alg=alg, amalgamate=amalgamate), device=device)
+def mstar(s: AbstractSemiring, A, alg=None, amalgamate: bool = True, device: bool = False, sym: Symbolic | None = None,
+          out=None, keep_factor: bool = False):
+    """The star A* = I (+) A (+) A^2 (+) ... as a dense matrix (mstar, abstract_slu.jl:81-87): the symbolic analysis,
+    then factorization and star in one device call (pp_mstar).  ``A`` may be a CSC triple / scipy matrix, or
+    ``(n, colptr, rowval, values)`` with the values a DeviceArray already in HBM.  ``device=True`` (or a DeviceArray
+    ``out``) leaves the star in HBM.  ``keep_factor=True`` returns ``(star, F)``."""
+    if isinstance(A, np.ndarray):
+        F = mlu(s, A, alg=alg, amalgamate=amalgamate, sym=sym)
+        C = Matrix(F, device=device, out=out)
+        return (C, F) if keep_factor else C
+    ctx = context(0)
+    if isinstance(A, tuple) and len(A) == 4 and isinstance(A[3], DeviceArray):
+        n, cp, rv, dnz = A
+        cp = np.ascontiguousarray(cp, np.int64)
+        rv = np.ascontiguousarray(rv, np.int64)
+        if int(np.prod(dnz.shape)) != int(cp[-1]):
+            raise PathpackArgumentError(_lib.PP_EINVAL, "mstar: the device values must hold nnz entries")
+        dtype, nzp, on_dev, keep = dnz.dtype, ctypes.c_void_p(dnz.ptr), 1, None
+        if sym is None:
+            sym = symbolic((n, cp, rv, np.zeros(cp[-1], dtype)), alg=alg, amalgamate=amalgamate)
+    else:
+        n, cp, rv, nz = _as_csc(A)
+        keep = np.ascontiguousarray(nz)
+        dtype, nzp, on_dev = keep.dtype, _p(keep), 0
+        if sym is None:
+            sym = symbolic((n, cp, rv, nz), alg=alg, amalgamate=amalgamate)
+    sym.check_pattern(n, cp, rv)
+    dt = _dtype_code(dtype)
+    if (dt == I32) != isinstance(s, OrAnd):
+        raise PathpackUnsupportedError(_lib.PP_EUNSUPPORTED, f"{s.name} does not support {dtype}")
+    h = ctypes.c_void_p()
+    hp = ctypes.byref(h) if keep_factor else None
+    if device or isinstance(out, DeviceArray):
+        C = out if out is not None else DeviceArray((n, n), dtype, ctx)
+        if C.shape != (n, n) or C.dtype != dtype:
+            raise PathpackArgumentError(_lib.PP_EINVAL, "out must be an n x n DeviceArray of the values' type")
+        ctx.check(lib().pp_mstar(ctx.handle, sym.handle, s.id, dt, nzp, on_dev, ctypes.c_void_p(C.ptr), n, 1, hp))
+    else:
+        C = out if out is not None else np.empty((n, n), dtype=dtype, order="F")
+        if not C.flags.f_contiguous or C.shape != (n, n) or C.dtype != dtype:
+            raise PathpackArgumentError(_lib.PP_EINVAL, "out must be a Fortran-ordered n x n array of the values' type")
+        ctx.check(lib().pp_mstar(ctx.handle, sym.handle, s.id, dt, nzp, on_dev, _p(C), n, 0, hp))
+    del keep
+    if keep_factor:
+        return C, Factorization(s, sym, np.dtype(dtype), h, ctx)
+    return C
 
 
 def _star_sources(F: Factorization, src, which: int, device: bool):

@@ -18,7 +18,7 @@ EXPORTS = [
     "pp_init", "pp_destroy", "pp_last_error", "pp_synchronize", "pp_stream",
     "pp_symbolic", "pp_symbolic_given", "pp_sym_size", "pp_sym_export", "pp_sym_stats", "pp_sym_destroy",
     "pp_factor", "pp_factor_device", "pp_refactor", "pp_fac_export", "pp_fac_destroy",
-    "pp_star", "pp_star_sources", "pp_lmul", "pp_rmul", "pp_sgemx", "pp_getrf_star_batched",
+    "pp_star", "pp_mstar", "pp_star_sources", "pp_lmul", "pp_rmul", "pp_sgemx", "pp_getrf_star_batched",
     "pp_buffer_alloc", "pp_buffer_free", "pp_upload", "pp_download", "pp_copy", "pp_calibrate_valu", "pp_set_timing",
     "pp_get_timing",
 ]
@@ -88,6 +88,8 @@ def lib() -> ctypes.CDLL:
         L.pp_fac_export.argtypes = [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]
         L.pp_fac_destroy.argtypes = [c_vp]
         L.pp_star.argtypes = [c_vp, c_vp, c_vp, c_i64, ctypes.c_int]
+        L.pp_mstar.argtypes = [c_vp, c_vp, ctypes.c_int, ctypes.c_int, c_vp, ctypes.c_int, c_vp, c_i64, ctypes.c_int,
+                               ctypes.POINTER(c_vp)]
         L.pp_star_sources.argtypes = [c_vp, c_vp, ctypes.c_int, c_i64, c_vp, c_vp, c_i64, ctypes.c_int]
         L.pp_lmul.argtypes = [c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_int]
         L.pp_rmul.argtypes = [c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_int]

@@ -254,6 +254,27 @@ def test_device_resident_star_and_solves():
     assert np.array_equal(bits(dR.numpy()), bits(C[[0, 10, 20, 30, 89], :]))
 
 
+@pytest.mark.parametrize("name,s,fdtype", [("grid6x7x5", O.MINPLUS, np.float32), ("components", O.MAXMIN, np.float64),
+                                            ("digraph150", O.PLUSPROD, np.float64), ("digraph40", O.ORAND, np.float32)])
+def test_mstar_one_call_matches_factor_then_star(name, s, fdtype):
+    """pp_mstar (the factorization and the star in one call, no wait in between; mstar, abstract_slu.jl:85-87) gives
+    the bits of pp_factor + pp_star and the oracle's star, with host and device values and outputs; the factor it
+    keeps gives the same star again."""
+    dtype = dtype_for(s, fdtype)
+    g = weighted(graphs()[name], s, dtype)
+    print(f"case mstar {name} s={s} dtype={np.dtype(dtype)}", flush=True)
+    sym, F, Fo = both(g, s, dtype)
+    C = P.Matrix(F)
+    sem = SEMIRINGS[s]
+    M1 = P.mstar(sem, g, sym=sym)
+    assert np.array_equal(bits(M1), bits(C))
+    assert_star_equal(s, M1, O.star(Fo), rtol=rtol_for(s, dtype))
+    dnz = P.DeviceArray.from_numpy(np.ascontiguousarray(g.nzval).reshape(-1, 1))
+    M2, F2 = P.mstar(sem, (g.n, g.colptr, g.rowval, dnz), sym=sym, device=True, keep_factor=True)
+    assert np.array_equal(bits(M2.numpy()), bits(C))
+    assert np.array_equal(bits(P.Matrix(F2)), bits(C))
+
+
 @pytest.mark.parametrize("ld_pad", [0, 3])
 def test_star_to_host_in_chunks(ld_pad):
     """pp_star into host memory goes through pinned column chunks (at least four) and the host's copy threads; with
