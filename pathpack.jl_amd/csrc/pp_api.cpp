@@ -381,6 +381,7 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     pp::DevPlan &d = fac->plan;
     auto failf = [&](pp_status code, const std::string &msg) {
         hipStreamSynchronize(st);
+        hipStreamSynchronize(ctx->aux_stream);   // the block packs may still read and write this factor
         delete fac;
         return failj(code, msg);
     };
