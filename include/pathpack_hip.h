@@ -198,6 +198,13 @@ pp_status pp_calibrate_valu(pp_ctx *ctx, int kind, int64_t iters, double *second
 pp_status pp_set_timing(pp_ctx *ctx, int on);
 pp_status pp_get_timing(const pp_ctx *ctx, double *t);
 
+/* Debug flags of a context (replaces nothing in the reference).  PP_DEBUG_POISON: every sweep buffer (the n x n star,
+ * the rows of pp_star_sources, the right-hand sides of the solves) is filled with the all-ones bit pattern -- NaN in
+ * Float32 and Float64, -1 in Int32 -- before the sweeps start, so that a kernel reading an element that nothing wrote
+ * shows it in the result.  Costs one extra pass over each buffer. */
+enum { PP_DEBUG_POISON = 1 };
+pp_status pp_set_debug(pp_ctx *ctx, int flags);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,16 +51,14 @@ static bool supported(int semiring, int dtype) {
     return false;
 }
 
-// Free device memory for the size checks: the driver's free memory plus what the default pool holds cached (freed
-// stream-ordered allocations, which pp_init keeps in the pool for the next call).
+// Free device memory for the size checks: the driver's free memory plus what the context's pool holds cached (freed
+// stream-ordered allocations, which the pool keeps for the next call).
 static hipError_t mem_free(pp_ctx *ctx, size_t *freeb, size_t *totalb) {
     hipError_t e = hipMemGetInfo(freeb, totalb);
     if (e != hipSuccess) return e;
-    hipMemPool_t pool = nullptr;
     uint64_t res = 0, used = 0;
-    if (hipDeviceGetDefaultMemPool(&pool, ctx->device) == hipSuccess && pool &&
-        hipMemPoolGetAttribute(pool, hipMemPoolAttrReservedMemCurrent, &res) == hipSuccess &&
-        hipMemPoolGetAttribute(pool, hipMemPoolAttrUsedMemCurrent, &used) == hipSuccess && res > used)
+    if (ctx->pool && hipMemPoolGetAttribute(ctx->pool, hipMemPoolAttrReservedMemCurrent, &res) == hipSuccess &&
+        hipMemPoolGetAttribute(ctx->pool, hipMemPoolAttrUsedMemCurrent, &used) == hipSuccess && res > used)
         *freeb += (size_t)(res - used);
     return hipSuccess;
 }
@@ -72,8 +70,7 @@ static hipError_t dev_malloc(pp_ctx *ctx, void **p, size_t bytes) {
     (void)hipGetLastError();
     hipStreamSynchronize(ctx->stream);
     hipStreamSynchronize(ctx->aux_stream);
-    hipMemPool_t pool = nullptr;
-    if (hipDeviceGetDefaultMemPool(&pool, ctx->device) == hipSuccess && pool) hipMemPoolTrimTo(pool, 0);
+    if (ctx->pool) hipMemPoolTrimTo(ctx->pool, 0);
     return hipMalloc(p, bytes);
 }
 
@@ -119,13 +116,17 @@ pp_status pp_init(pp_ctx **out, int device) {
             return fail(nullptr, PP_EHIP, "pp_init: hipEventCreate failed");
         }
     {
-        // stream-ordered allocations (fronts, the n x n star buffer, scratch) come from the device's default pool;
-        // keep what is freed there for the next call instead of returning it to the driver at every
-        // synchronization (re-mapping the 4 GB star buffer of a 32768-vertex graph costs about a millisecond)
-        hipMemPool_t pool = nullptr;
-        if (hipDeviceGetDefaultMemPool(&pool, device) == hipSuccess && pool) {
-            uint64_t keep = UINT64_MAX;
-            hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+        // the context's own pool (stream-ordered allocations), which keeps freed memory until the context ends
+        hipMemPoolProps props = {};
+        props.allocType = hipMemAllocationTypePinned;
+        props.handleTypes = hipMemHandleTypeNone;
+        props.location.type = hipMemLocationTypeDevice;
+        props.location.id = device;
+        uint64_t keep = UINT64_MAX;
+        if (hipMemPoolCreate(&ctx->pool, &props) != hipSuccess ||
+            hipMemPoolSetAttribute(ctx->pool, hipMemPoolAttrReleaseThreshold, &keep) != hipSuccess) {
+            pp_destroy(ctx);
+            return fail(nullptr, PP_EHIP, "pp_init: creating the memory pool failed");
         }
     }
     if (hipStreamCreateWithFlags(&ctx->aux_stream, hipStreamNonBlocking) != hipSuccess ||
@@ -163,10 +164,11 @@ pp_status pp_destroy(pp_ctx *ctx) {
         if (e) hipEventDestroy(e);
     for (auto &p : ctx->outpin)
         if (p) hipHostFree(p);
-    {
-        // give the pool's cached memory back (other contexts on the device allocate again as they need)
-        hipMemPool_t pool = nullptr;
-        if (hipDeviceGetDefaultMemPool(&pool, ctx->device) == hipSuccess && pool) hipMemPoolTrimTo(pool, 0);
+    if (ctx->pool) {
+        // every stream is synchronized: the pool's memory goes back to the driver (the factors of a context are
+        // destroyed before it)
+        hipMemPoolTrimTo(ctx->pool, 0);
+        hipMemPoolDestroy(ctx->pool);
     }
     delete ctx;
     return PP_OK;
@@ -297,7 +299,7 @@ struct Upload {
         parts.push_back({vec.data(), bytes, place(bytes), (void **)ptr});
     }
     // allocate the block (stream-ordered pool), stage and upload the parts; the block's address into *block
-    std::string run(hipStream_t st, void *&staging, size_t &staging_bytes, size_t plan_bytes, void **block) {
+    std::string run(pp_ctx *ctx, hipStream_t st, void *&staging, size_t &staging_bytes, size_t plan_bytes, void **block) {
         if (staging_bytes < plan_bytes) {
             if (staging) hipHostFree(staging);
             staging = nullptr;
@@ -308,7 +310,7 @@ struct Upload {
         }
         for (const Part &q : parts)
             if (q.bytes) std::memcpy((char *)staging + q.off, q.src, q.bytes);
-        if (hipMallocAsync(block, total, st) != hipSuccess) return "hipMallocAsync of the factor failed";
+        if (pp::ctx_alloc(ctx, block, total, st) != hipSuccess) return "stream-ordered allocation of the factor failed";
         for (const Part &q : parts) *q.dst = q.bytes ? (void *)((char *)*block + q.off) : nullptr;
         if (hipMemcpyAsync(*block, staging, plan_bytes, hipMemcpyHostToDevice, st) != hipSuccess)
             return "upload of the plans failed";
@@ -316,9 +318,32 @@ struct Upload {
     }
 };
 
-// finish: wait for the factorization before returning (pp_factor); pp_mstar queues the star behind it instead
+// Device memory of a factorization, from the structure alone (nothing is queued before the check): the plans and
+// the factor, then the larger of the factorization's scratch (the frontal arena, the uploaded values) and what the
+// sweeps keep (their plan, the panel and block packs, the block stars' scratch) plus `extra` (the star of pp_mstar).
+// The plan arrays are bounded per unit (panels and blocks); everything else is exact.
+static size_t factor_bytes(const pp::Symbolic &S, const pp::FactorPlan &P, size_t es, bool values_on_device,
+                           size_t extra) {
+    const size_t nD = (size_t)S.Dptr[S.nf], nL = (size_t)S.Lptr[S.nf];
+    const pp::SweepSizes z = pp::sweep_sizes(S);
+    const size_t plan1 = sizeof(i64) * (3 * (size_t)S.nnz + 6 * (size_t)S.nf + 2 * (size_t)S.n) +
+                         sizeof(int32_t) * (P.stask.size() + P.flist.size() + P.atask.size() + P.etask.size() +
+                                            P.relpos.size() + 3 * (size_t)S.nf) +
+                         32 * 256;
+    const size_t factor = es * (nD + 2 * nL);
+    const size_t scratch = es * ((size_t)P.arena + (values_on_device ? 0 : (size_t)S.nnz));
+    const size_t plan2 = sizeof(int32_t) * ((size_t)z.eidx + 80 * (size_t)z.units + 4 * (size_t)z.prep + (size_t)S.n) +
+                         sizeof(i64) * (5 * (size_t)z.units + 2 * (size_t)S.n) + 40 * 256;
+    const size_t packs = es * (2 * (size_t)z.npack + (size_t)z.ndpack + (size_t)z.nbpack + (size_t)z.nhpack +
+                               (size_t)z.nb * 2 * pp::BLK_W * pp::BLK_W);
+    return plan1 + factor + std::max(scratch, plan2 + packs + extra);
+}
+
+// finish: wait for the factorization before returning (pp_factor); pp_mstar queues the star behind it instead, and
+// passes the star's bytes as `extra` so that the one check covers both before anything is queued
 static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, int dtype, const void *nzval,
-                               bool on_device, pp_fac **out, bool finish = true) {
+                               bool on_device, pp_fac **out, bool finish = true, size_t extra = 0,
+                               const char *who = "pp_factor") {
     if (!ctx) return fail(nullptr, PP_EINVAL, "pp_factor: null context");
     if (!csym || !out) return fail(ctx, PP_EINVAL, "pp_factor: null argument");
     *out = nullptr;
@@ -360,17 +385,19 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
         sym->fplan = f;
     }
     const pp::FactorPlan &P = *sym->fplan;
-    // device memory at the peak (the packs are checked again once their size is known)
     const size_t nD = (size_t)S.Dptr[S.nf], nL = (size_t)S.Lptr[S.nf];
-    const size_t need = es * ((size_t)P.arena + nD + 2 * nL + (size_t)S.nnz) +
-                        sizeof(i64) * (3 * (size_t)S.nnz + 6 * (size_t)S.nf + 2 * (size_t)S.n) +
-                        sizeof(int32_t) * (P.stask.size() + P.flist.size() + P.atask.size() + P.etask.size() +
-                                           P.relpos.size());
+    const size_t need = factor_bytes(S, P, es, on_device, extra);
     size_t freeb = 0, totalb = 0;
-    if (mem_free(ctx, &freeb, &totalb) != hipSuccess) return failj(PP_EHIP, "pp_factor: hipMemGetInfo failed");
+    if (mem_free(ctx, &freeb, &totalb) != hipSuccess) return failj(PP_EHIP, std::string(who) + ": hipMemGetInfo failed");
+    if (need > freeb) {
+        // work still queued on the context may hold pool memory that it is about to free: wait and look again
+        hipStreamSynchronize(ctx->stream);
+        hipStreamSynchronize(ctx->aux_stream);
+        if (mem_free(ctx, &freeb, &totalb) != hipSuccess) return failj(PP_EHIP, std::string(who) + ": hipMemGetInfo failed");
+    }
     if (need > freeb)
-        return failj(PP_ENOMEM, "pp_factor: needs " + std::to_string(need) + " bytes of device memory, " +
-                                    std::to_string(freeb) + " free");
+        return failj(PP_ENOMEM, std::string(who) + ": needs " + std::to_string(need) + " bytes of device memory, " +
+                                    std::to_string(freeb) + " free; nothing was launched");
     pp_fac *fac = new (std::nothrow) pp_fac;
     if (!fac) return failj(PP_ENOMEM, "pp_factor: out of host memory");
     fac->ctx = ctx;
@@ -406,7 +433,7 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     const size_t plan1 = u1.total;
     const size_t oLD = u1.place(nD * es), oLL = u1.place(nL * es), oUL = u1.place(nL * es);
     void *block1 = nullptr;
-    std::string e = u1.run(st, ctx->staging, ctx->staging_bytes, plan1, &block1);
+    std::string e = u1.run(ctx, st, ctx->staging, ctx->staging_bytes, plan1, &block1);
     if (!e.empty()) return failf(PP_ENOMEM, "pp_factor: " + e);
     d.owned.push_back(block1);
     fac->LD = (char *)block1 + oLD;
@@ -415,7 +442,7 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     const void *dnz = nzval;
     void *tmpnz = nullptr;
     if (!on_device && S.nnz > 0) {
-        if (hipMallocAsync(&tmpnz, S.nnz * es, st) != hipSuccess) return failf(PP_ENOMEM, "pp_factor: hipMalloc of the values failed");
+        if (pp::ctx_alloc(ctx, &tmpnz, S.nnz * es, st) != hipSuccess) return failf(PP_ENOMEM, "pp_factor: hipMalloc of the values failed");
         if (hipMemcpyAsync(tmpnz, nzval, S.nnz * es, hipMemcpyHostToDevice, st) != hipSuccess) {
             hipFreeAsync(tmpnz, st);
             return failf(PP_EHIP, "pp_factor: upload of the values failed");
@@ -468,7 +495,7 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     // (no free-memory query here: the factorization is already queued and the query would wait for it; the packs'
     // stream-ordered allocation reports a shortage itself)
     void *block2 = nullptr;
-    e = u2.run(st, ctx->staging2, ctx->staging2_bytes, plan2, &block2);
+    e = u2.run(ctx, st, ctx->staging2, ctx->staging2_bytes, plan2, &block2);
     if (!e.empty()) return failf(PP_ENOMEM, "pp_factor: " + e);
     d.owned.push_back(block2);
     fac->Dpack = (char *)block2 + oD;
@@ -514,7 +541,7 @@ pp_status pp_refactor(pp_ctx *ctx, pp_fac *fac, const void *nzval, int on_device
     const void *dnz = nzval;
     void *tmpnz = nullptr;
     if (!on_device && S.nnz > 0) {
-        if (hipMallocAsync(&tmpnz, S.nnz * es, st) != hipSuccess) return fail(ctx, PP_ENOMEM, "pp_refactor: hipMalloc of the values failed");
+        if (pp::ctx_alloc(ctx, &tmpnz, S.nnz * es, st) != hipSuccess) return fail(ctx, PP_ENOMEM, "pp_refactor: hipMalloc of the values failed");
         if (hipMemcpyAsync(tmpnz, nzval, S.nnz * es, hipMemcpyHostToDevice, st) != hipSuccess) {
             hipFreeAsync(tmpnz, st);
             hipStreamSynchronize(st);
@@ -602,17 +629,11 @@ pp_status pp_mstar(pp_ctx *ctx, const pp_sym *sym, int semiring, int dtype, cons
     if (ldc < sym->S.n) return fail(ctx, PP_EINVAL, "pp_mstar: ldc < n");
     if (!supported(semiring, dtype)) return fail(ctx, PP_EUNSUPPORTED, "pp_mstar: unsupported semiring / element type");
     CHECK_HIP(ctx, hipSetDevice(ctx->device));
-    {
-        size_t freeb = 0, totalb = 0;
-        CHECK_HIP(ctx, mem_free(ctx, &freeb, &totalb));
-        const size_t need = star_bytes(sym->S.n, (size_t)pp::dtype_size(dtype), out_on_device);
-        if (need > freeb)
-            return fail(ctx, PP_ENOMEM, "pp_mstar: the star needs " + std::to_string(need) + " bytes of device memory, " +
-                                            std::to_string(freeb) + " free");
-    }
     pp_fac *fac = nullptr;
-    // the factorization is queued without waiting for it; the star's launches follow it on the same stream
-    pp_status st = factor_common(ctx, sym, semiring, dtype, nzval, nz_on_device != 0, &fac, false);
+    // the factorization is queued without waiting for it; the star's launches follow it on the same stream.  Its
+    // memory check includes the star's, so a request that does not fit is refused before anything is queued.
+    pp_status st = factor_common(ctx, sym, semiring, dtype, nzval, nz_on_device != 0, &fac, false,
+                                 star_bytes(sym->S.n, (size_t)pp::dtype_size(dtype), out_on_device), "pp_mstar");
     if (st != PP_OK) return st;
     st = star_common(ctx, fac, out, ldc, out_on_device, false);
     if (st != PP_OK || !fac_out) {
@@ -819,6 +840,13 @@ pp_status pp_calibrate_valu(pp_ctx *ctx, int kind, int64_t iters, double *second
 pp_status pp_set_timing(pp_ctx *ctx, int on) {
     if (!ctx) return fail(nullptr, PP_EINVAL, "pp_set_timing: null context");
     ctx->timing = on;
+    return PP_OK;
+}
+
+pp_status pp_set_debug(pp_ctx *ctx, int flags) {
+    if (!ctx) return fail(nullptr, PP_EINVAL, "pp_set_debug: null context");
+    if (flags & ~PP_DEBUG_POISON) return fail(ctx, PP_EINVAL, "pp_set_debug: unknown flag");
+    ctx->debug = flags;
     return PP_OK;
 }
 

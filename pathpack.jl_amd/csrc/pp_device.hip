@@ -73,7 +73,7 @@ std::string device_valu_peak(pp_ctx *ctx, int kind, int iters, double *seconds, 
     const int blocks = ctx->num_cu * 8;
     float *out = nullptr;
     hipStream_t st = ctx->stream;
-    if (hipMallocAsync((void **)&out, (size_t)blocks * 256 * sizeof(float), st) != hipSuccess) return "hipMallocAsync failed";
+    if (ctx_alloc(ctx, (void **)&out, (size_t)blocks * 256 * sizeof(float), st) != hipSuccess) return "hipMallocAsync failed";
     hipEvent_t e0, e1;
     hipEventCreate(&e0);
     hipEventCreate(&e1);

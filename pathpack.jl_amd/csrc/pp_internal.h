@@ -69,6 +69,14 @@ inline int width_class(int w) {
     return c;
 }
 
+inline i64 round_up(i64 x, i64 m) { return (x + m - 1) / m * m; }
+// The star's cut of a front wider than PANEL_W: blocks of BLK_W columns while more than 3/4 BLK_W remain, then one
+// block of the rest if it is wider than PANEL_W (a BLK_W / 2 tile class when it fits), then panels.
+inline i64 star_block_w(i64 rest) {
+    return rest > BLK_W * 3 / 4 ? (rest < BLK_W ? rest : BLK_W) : rest > BLK_W / 2 ? BLK_W / 2 : rest;
+}
+inline i64 star_block_bn(i64 w) { return w > BLK_W / 2 ? BLK_W : BLK_W / 2; }
+
 struct FactorPlan {
     i64 nf = 0;
     std::vector<int32_t> nn, na, nj;
@@ -136,6 +144,16 @@ struct SweepPlan {
 std::string build_factor_plan(const Symbolic &S, FactorPlan &P);
 std::string build_sweep_plan(const Symbolic &S, SweepPlan &P);
 
+// Element counts of the sweep plan's packs and index lists, from the front sizes alone (the cut of build_sweep_plan,
+// without building the plan): for the device-memory checks made before anything is queued.
+struct SweepSizes {
+    i64 units = 0, nb = 0;           // panels plus star blocks; star blocks
+    i64 eidx = 0;                    // gather-list entries (with the padding)
+    i64 npack = 0, ndpack = 0, nbpack = 0, nhpack = 0;
+    i64 prep = 0;                    // block-pack GEMM tiles
+};
+SweepSizes sweep_sizes(const Symbolic &S);
+
 // The sweeps over the rows of a set of sources instead of all n (rows or columns of the star for chosen vertices).
 // Row k of the sweep buffer starts as the unit vector of source js[k] (elimination labels, ascending).  A unit's
 // forward rows are then the sources in its subtree, a contiguous range of js, and its backward rows the sources of
@@ -189,8 +207,13 @@ struct pp_ctx {
     int device = 0;
     int num_cu = 256;                // compute units of the device
     hipStream_t stream = nullptr;
+    // the context's own stream-ordered memory pool: fronts, the n x n star buffer, scratch.  It keeps freed memory
+    // for the next call (re-mapping the 4 GB star buffer of a 32768-vertex graph costs about a millisecond) and is
+    // trimmed and destroyed with the context; the device's default pool and other contexts are not touched.
+    hipMemPool_t pool = nullptr;
     std::string err;
     int timing = 0;
+    int debug = 0;                   // PP_DEBUG_* flags (pp_set_debug)
     double t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     hipEvent_t ev[16] = {};          // start and stop event of each timing slot
     bool pending[8] = {};            // a slot's events are recorded and its time not yet read
@@ -224,6 +247,11 @@ struct pp_fac {
 };
 
 namespace pp {
+// A stream-ordered allocation from the context's pool (freed with hipFreeAsync).
+inline hipError_t ctx_alloc(pp_ctx *ctx, void **p, size_t bytes, hipStream_t st) {
+    return hipMallocFromPoolAsync(p, bytes, ctx->pool, st);
+}
+
 // Numeric drivers (pp_device.hip).  Return "" or an error message.
 std::string device_factor(pp_ctx *ctx, pp_fac *fac, const void *d_nzval);   // up to the reference layout
 std::string device_factor_packs(pp_ctx *ctx, pp_fac *fac);                 // the sweep packs; frees the fronts

@@ -17,6 +17,7 @@
 #include <cstring>
 #include <type_traits>
 
+#include "pathpack_hip.h"
 #include "pp_internal.h"
 #include "pp_semiring.h"
 
@@ -737,7 +738,9 @@ __global__ __launch_bounds__(NT) void k_build_packs(const typename S::value_type
 // DMODE 0 reads the panel block as stored (U upper with star for forward, L strict lower unit for backward);
 // DMODE 1 reads it transposed (L^T unit for forward, U^T with star for backward): lmul! runs on B^T.
 // A panel of width w runs in the kernel of its width class W (power of two >= w); its packs are padded to W columns
-// with the semiring zero, so every inner loop runs over W without branches (a zero term changes nothing).
+// with the semiring zero, so every inner loop runs over W without branches (a zero term changes nothing).  The padded
+// unknowns j >= w are reset to the semiring zero after each triangular solve: under PlusProd an Inf times a zero pad
+// entry is NaN, which must not reach a real column.
 // The column indices and pack values are wave-uniform (scalar loads); X is read and written one row per lane, so
 // each gathered column is a coalesced 256-byte wave access.
 
@@ -856,7 +859,7 @@ __global__ __launch_bounds__(NT) void k_fwd(typename S::value_type *__restrict__
 #pragma unroll
             for (int i = 0; i < j; i++) acc = S::muladd(x[i], DMODE == 0 ? D[i + j * W] : D[j + i * W], acc);
             if (DMODE == 0 && !S::integral) acc = S::prod(acc, S::star(D[j + j * W]));
-            x[j] = acc;
+            x[j] = j < w ? acc : S::zero();
         }
 #pragma unroll
         for (int j = 0; j < W; j++) xsh[j][lane] = x[j];
@@ -997,7 +1000,7 @@ __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(siz
 #pragma unroll
             for (int i = 0; i < j; i++) s = S::muladd(acc[i], DMODE == 0 ? D[i + j * W] : D[j + i * W], s);
             if (DMODE == 0 && !S::integral) s = S::prod(s, S::star(D[j + j * W]));
-            acc[j] = s;
+            acc[j] = j < w ? s : S::zero();
         }
     }
     if (ngw > 0) {
@@ -1039,7 +1042,7 @@ __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(siz
 #pragma unroll
         for (int i = j + 1; i < W; i++) s = S::muladd(acc[i], DMODE == 0 ? D[i + j * W] : D[j + i * W], s);
         if (DMODE == 1 && !S::integral) s = S::prod(s, S::star(D[j + j * W]));
-        acc[j] = s;
+        acc[j] = j < w ? s : S::zero();
     }
     if (valid) {
 #pragma unroll
@@ -1083,7 +1086,7 @@ __device__ inline void sub_fwd_panel(typename S::value_type *__restrict__ X, i64
 #pragma unroll
         for (int i = 0; i < j; i++) acc = S::muladd(x[i], D[i + j * W], acc);
         if (!S::integral) acc = S::prod(acc, S::star(D[j + j * W]));
-        x[j] = acc;
+        x[j] = j < w ? acc : S::zero();
     }
     if (e == 0) return;
     T A[4], B[4];
@@ -1175,7 +1178,7 @@ __device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64
 #pragma unroll
             for (int i = 0; i < j; i++) s = S::muladd(acc[i], D[i + j * W], s);
             if (!S::integral) s = S::prod(s, S::star(D[j + j * W]));
-            acc[j] = s;
+            acc[j] = j < w ? s : S::zero();
         }
     }
     if (e > 0) {
@@ -1199,7 +1202,7 @@ __device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64
         T s = acc[j];
 #pragma unroll
         for (int i = j + 1; i < W; i++) s = S::muladd(acc[i], D[i + j * W], s);
-        acc[j] = s;
+        acc[j] = j < w ? s : S::zero();
     }
     if (store) {
 #pragma unroll
@@ -1551,15 +1554,22 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
         }
     };
     // the loaded step k0 into LDS buffer buf; the backward's own columns (k < w) are zero outside the rows
-    // [olo, ohi), applied here rather than at the load so that nothing waits on the load before the step's math
+    // [olo, ohi), applied here rather than at the load so that nothing waits on the load before the step's math.
+    // The padded steps k >= K load an in-range column (c0, or the block's last column forward) whose rows outside
+    // the block's subtree no kernel has written yet: they are replaced by the semiring zero too (a zero pack row
+    // times such a value is not zero for PlusProd when it holds Inf or NaN).
     auto sstore = [&](int buf, int k0) {
 #pragma unroll
         for (int q = 0; q < AQ; q++) {
             const int ev = (tid + 256 * q) * VW;
+            const int kq = k0 + ev / BM;
             V v;
 #pragma unroll
             for (int t = 0; t < VW; t++) v[t] = ra[q * VW + t];
-            if (!FWD && k0 + ev / BM < w) {
+            if (kq >= K) {
+#pragma unroll
+                for (int t = 0; t < VW; t++) v[t] = S::zero();
+            } else if (!FWD && kq < w) {
 #pragma unroll
                 for (int t = 0; t < VW; t++) {
                     const i64 rr = r0 + ev % BM + t;
@@ -1918,6 +1928,17 @@ inline void timer_stop(pp_ctx *ctx, int slot) {
     ctx->pending[slot] = true;
 }
 
+// Debug (PP_DEBUG_POISON): fill a fresh sweep buffer with the all-ones bit pattern (NaN in both float types, -1 for
+// OrAnd) before the sweeps, so that any read of an element no kernel has written shows in the result.  A fill kernel,
+// not a memset, on the context's stream.
+inline std::string poison_fill(pp_ctx *ctx, void *p, size_t bytes) {
+    if (!(ctx->debug & PP_DEBUG_POISON) || bytes < 4) return "";
+    const i64 words = (i64)(bytes / 4);
+    k_fill<uint32_t><<<grid1(words), NT, 0, ctx->stream>>>((uint32_t *)p, words, 0xffffffffu);
+    LAUNCHCHK();
+    return "";
+}
+
 template <class S> struct FactorRun {
     pp_ctx *ctx;
     pp_fac *fac;
@@ -1933,7 +1954,7 @@ template <class S> struct FactorRun {
         if (ctx->aux_pending) HIPCHK(hipStreamWaitEvent(st, ctx->aux_done, 0));
         timer_start(ctx, 0);
         T *F = nullptr;
-        HIPCHK(hipMallocAsync((void **)&F, std::max<i64>(1, P.arena) * sizeof(T), st));
+        HIPCHK(ctx_alloc(ctx, (void **)&F, std::max<i64>(1, P.arena) * sizeof(T), st));
         k_fill<T><<<grid1(P.arena), NT, 0, st>>>(F, P.arena, S::zero());
         LAUNCHCHK();
         if (fac->sym->S.nnz > 0)
@@ -1987,7 +2008,7 @@ template <class S> struct PacksRun {
             HIPCHK(hipEventRecord(ctx->aux_from, st));
             HIPCHK(hipStreamWaitEvent(as, ctx->aux_from, 0));
             T *stars = nullptr;
-            HIPCHK(hipMallocAsync((void **)&stars, (size_t)W.nb * 2 * BLK_W * BLK_W * sizeof(T), as));
+            HIPCHK(ctx_alloc(ctx, (void **)&stars, (size_t)W.nb * 2 * BLK_W * BLK_W * sizeof(T), as));
             k_fill<T><<<grid1(W.nbpack), NT, 0, as>>>((T *)fac->Bpack, W.nbpack, S::zero());
             if (W.nhpack) k_fill<T><<<grid1(W.nhpack), NT, 0, as>>>((T *)fac->Hpack, W.nhpack, S::zero());
             k_blk_stars<S><<<(unsigned)W.nb, NT, 0, as>>>((const T *)fac->LD, d.Dptr, d.nn, d.Rptr, d.p_front, d.p_c0,
@@ -2253,7 +2274,9 @@ template <class S> struct StarRun {
         const i64 n = fac->sym->S.n;
         hipStream_t st = ctx->stream;
         T *X = nullptr;
-        HIPCHK(hipMallocAsync((void **)&X, std::max<i64>(1, n * n) * sizeof(T), st));
+        HIPCHK(ctx_alloc(ctx, (void **)&X, std::max<i64>(1, n * n) * sizeof(T), st));
+        std::string pe = poison_fill(ctx, X, (size_t)(n * n) * sizeof(T));
+        if (!pe.empty()) return pe;
         timer_start(ctx, 1);
         const DevPlan &d = fac->plan;
         const i64 nsu = (i64)fac->sym->splan->sunits.size();
@@ -2310,7 +2333,7 @@ template <class S> struct StarRun {
             ctx->outpin_bytes = cbytes;
         }
         T *dc[2] = {nullptr, nullptr};
-        HIPCHK(hipMallocAsync((void **)&dc[0], 2 * cbytes, st));
+        HIPCHK(ctx_alloc(ctx, (void **)&dc[0], 2 * cbytes, st));
         dc[1] = dc[0] + CB * n;
         hipStream_t cs = ctx->copy_stream;
         auto cols = [&](i64 k, i64 &j0, i64 &j1) {
@@ -2415,7 +2438,9 @@ template <class S> struct StarSrcRun {
         const SweepPlan &Wp = *fac->sym->splan;
         const DevPlan &d = fac->plan;
         T *Y = nullptr;
-        HIPCHK(hipMallocAsync((void **)&Y, m * n * sizeof(T), st));
+        HIPCHK(ctx_alloc(ctx, (void **)&Y, m * n * sizeof(T), st));
+        std::string pe = poison_fill(ctx, Y, (size_t)(m * n) * sizeof(T));
+        if (!pe.empty()) return pe;
         timer_start(ctx, 4);
         if (!cols) {
             const i64 nsu = (i64)Wp.sunits.size();
@@ -2464,7 +2489,9 @@ template <class S> struct SolveRun {
         hipStream_t st = ctx->stream;
         if (n == 0 || nrhs == 0) return "";
         T *Y = nullptr;
-        HIPCHK(hipMallocAsync((void **)&Y, n * nrhs * sizeof(T), st));
+        HIPCHK(ctx_alloc(ctx, (void **)&Y, n * nrhs * sizeof(T), st));
+        std::string pe = poison_fill(ctx, Y, (size_t)(n * nrhs) * sizeof(T));
+        if (!pe.empty()) return pe;
         timer_start(ctx, 4);
         std::string e;
         if (!left) {

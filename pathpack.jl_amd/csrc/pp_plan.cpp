@@ -209,14 +209,11 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
     P.prep.clear();
     P.nbpack = 0;
     P.nhpack = 0;
-    auto up = [](i64 x, i64 m) { return (x + m - 1) / m * m; };
     for (i64 f = 0; f < nf; f++) {
         const i64 Rp = S.Rptr[f], nn = S.Rptr[f + 1] - Rp, nj = nn + (S.Sptr[f + 1] - S.Sptr[f]);
         i64 done = 0;
         while (nn > PANEL_W && nn - done > PANEL_W) {
-            const i64 rest = nn - done;
-            const i64 w = rest > BLK_W * 3 / 4 ? std::min<i64>(BLK_W, rest) : rest > BLK_W / 2 ? BLK_W / 2 : rest;
-            const i64 bn = w > BLK_W / 2 ? BLK_W : BLK_W / 2;
+            const i64 w = star_block_w(nn - done), bn = star_block_bn(w);
             const i64 c0 = Rp + done, lo = done + w, e = nj - lo;
             const i64 b = (i64)P.b_boff.size();
             su[f].push_back((int32_t)P.front.size());
@@ -236,7 +233,7 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
             P.rowB_lo.push_back((int32_t)S.Rptr[S.fdsc[root[f]]]);
             P.rowB_hi.push_back((int32_t)S.Rptr[root[f] + 1]);
             P.max_e = std::max(P.max_e, e);
-            const i64 kp = up(w + e, BLK_K), wp = up(w, BLK_K), ep = up(e, BLK_W);
+            const i64 kp = round_up(w + e, BLK_K), wp = round_up(w, BLK_K), ep = round_up(e, BLK_W);
             P.b_boff.push_back(P.nbpack);
             P.b_kp.push_back((int32_t)kp);
             P.b_bn.push_back((int32_t)bn);
@@ -385,6 +382,34 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
     make_lists(slvA, true, P.sfwd);
     make_lists(slvB, false, P.sbwd);
     return "";
+}
+
+SweepSizes sweep_sizes(const Symbolic &S) {
+    SweepSizes z;
+    for (i64 f = 0; f < S.nf; f++) {
+        const i64 nn = S.Rptr[f + 1] - S.Rptr[f], nj = nn + (S.Sptr[f + 1] - S.Sptr[f]);
+        for (i64 k = 0; k * PANEL_W < nn; k++) {   // panels (every front)
+            const i64 w = std::min<i64>(PANEL_W, nn - k * PANEL_W), e = nj - (k * PANEL_W + w);
+            const i64 Wc = (i64)1 << width_class((int)w);
+            z.units++;
+            z.eidx += e;
+            z.npack += Wc * e;
+            z.ndpack += Wc * Wc;
+        }
+        for (i64 done = 0; nn > PANEL_W && nn - done > PANEL_W;) {   // star blocks (fronts wider than a panel)
+            const i64 w = star_block_w(nn - done), e = nj - (done + w);
+            z.units++;
+            z.eidx += e;
+            z.nbpack += round_up(w + e, BLK_K) * star_block_bn(w);
+            z.nhpack += round_up(w, BLK_K) * round_up(e, BLK_W);
+            const i64 tw = (w + PREP_T - 1) / PREP_T, te = (e + PREP_T - 1) / PREP_T;
+            z.prep += tw * tw + 2 * te * tw;
+            z.nb++;
+            done += w;
+        }
+    }
+    z.eidx += EIDX_PAD;
+    return z;
 }
 
 int32_t RowSub::map(int32_t r) const { return (int32_t)(std::lower_bound(js.begin(), js.end(), r) - js.begin()); }

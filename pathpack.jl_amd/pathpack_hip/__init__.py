@@ -142,6 +142,10 @@ class Context:
     def set_timing(self, on: bool):
         self.check(lib().pp_set_timing(self.handle, 1 if on else 0))
 
+    def set_poison(self, on: bool):
+        """Fill every sweep buffer with NaN (-1 for OrAnd) before the sweeps (pp_set_debug, PP_DEBUG_POISON)."""
+        self.check(lib().pp_set_debug(self.handle, 1 if on else 0))
+
     def timing(self) -> np.ndarray:
         t = (ctypes.c_double * 8)()
         self.check(lib().pp_get_timing(self.handle, t))

@@ -45,6 +45,11 @@ static long nerr = 0;
         }                                  \
     } while (0)
 
+template <class T> T poison() {
+    if constexpr (std::is_floating_point<T>::value) return std::numeric_limits<T>::quiet_NaN();
+    else return T(-1);
+}
+
 template <class T> struct Chk {
     const std::vector<T> *v;
     const char *name;
@@ -331,8 +336,11 @@ template <class S> struct Emu {
                             for (int h = 0; h < 2; h++) {
                                 int kk = k + h;
                                 i64 col = colA(kk);
-                                bool masked = !fwd && kk < w && (r < olo || r >= ohi);
-                                T v = rd(r, col, stored && !masked && kk < K);
+                                // the kernel's LDS store selects the semiring zero for the backward's own columns
+                                // outside [olo, ohi) and for the padded steps k >= K; every other value read enters
+                                // the accumulator (also on rows that are not stored, which only this lane computes)
+                                bool masked = !fwd && ((kk < w && (r < olo || r >= ohi)) || kk >= K);
+                                T v = rd(r, col, stored && !masked);
                                 if (masked) v = S::zero();
                                 av[h] = v;
                                 i64 pos = boff + (i64)kk * ldb + c;
@@ -499,7 +507,9 @@ template <class S> int run(const char *path, int sr, int dt, int ncu, long mod) 
         printf("sources %zu\n", srcs.size());
     }
     const i64 m = E.m;
-    E.X.assign(m * n, S::zero());
+    // X starts poisoned, as device memory that no kernel wrote: NaN (a bit pattern with every bit set for OrAnd), so
+    // that a value read before it is written shows in the result as well as in the initialisation check
+    E.X.assign(m * n, poison<T>());
     E.init.assign(m * n, 0);
     E.wtask.assign(m * n, -1);
     E.identity();

@@ -2,9 +2,11 @@
 
 The oracle's dense star is out of reach at these sizes (a 32768 x 32768 star is 4.3 GB and about 3e11 semiring
 operations), so each workload is checked against what the mathematics fixes:
-- MinPlus mstar, directed 32 x 32 x 32 grid (Float32, integer weights): sampled rows and columns of the star, taken
-  from the full n x n result delivered to host memory, equal Dijkstra's distances bit for bit (path lengths are
-  integers below 2^24, so Float32 holds them exactly); the diagonal is zero.
+- MinPlus mstar, directed 32 x 32 x 32 grid (Float32, integer weights): the whole n x n star, delivered to host
+  memory, satisfies C = I (+) C (x) A entry by entry, bit for bit.  With every arc weight >= 1 that equation has
+  exactly one solution, the star (a finite entry not given by a path would need an infinite strictly decreasing
+  chain of finite entries); path lengths are integers below 2^24, so Float32 holds every candidate exactly.  Sampled
+  rows and columns also equal Dijkstra's distances bit for bit.
 - MaxMin lmul! of 1024 unit columns on the n = 65536 geometric graph: sampled columns equal widest-path (bottleneck
   Dijkstra) values exactly, -Inf between components; every column equals the batched source path bit for bit.
 - PlusProd rmul! of 512 unit rows on the directed 256 x 256 grid (Float64): every row x satisfies its defining
@@ -51,13 +53,42 @@ def widest_to(g: W.Graph, s: int) -> np.ndarray:
     return best
 
 
+def minplus_fixed_point_violations(C: np.ndarray, g: W.Graph, cols: np.ndarray) -> int:
+    """Entries of the columns `cols` of C with C[:, j] != min(I[:, j], min over arcs k -> j of C[:, k] + w(k -> j)),
+    compared bit for bit.  Column j of the CSC matrix lists the arcs into j; the columns of the column-major C are
+    the rows of its transpose, so every gather reads whole contiguous rows."""
+    CT = C.T
+    lo, hi = g.colptr[cols], g.colptr[cols + 1]
+    q = np.concatenate([np.arange(a, b) for a, b in zip(lo, hi)]).astype(np.int64)
+    G = CT[g.rowval[q], :]
+    G += g.nzval[q].astype(np.float32)[:, None]   # one gathered column per arc
+    starts = np.concatenate([[0], np.cumsum(hi - lo)[:-1]])
+    R = np.full((cols.size, C.shape[0]), np.inf, np.float32)
+    has = hi > lo
+    R[has, :] = np.minimum.reduceat(G, starts[has], axis=0)
+    R[np.arange(cols.size), cols] = np.minimum(R[np.arange(cols.size), cols], 0)
+    return int(np.count_nonzero(R.view(np.uint32) != CT[cols, :].view(np.uint32)))
+
+
 def test_config3_mstar_full_size_vs_dijkstra():
+    from concurrent.futures import ThreadPoolExecutor
+
     g = W.config_graph(3)
     n = g.n
     print(f"MinPlus mstar n={n}", flush=True)
     C = P.mstar(P.MinPlus(), g)               # the full star, through the chunked copy to host memory
     assert C.shape == (n, n) and C.dtype == np.float32
     assert np.all(np.diag(C) == 0)
+    assert g.nzval.min() >= 1
+    # the whole star against its defining equation, 256 columns at a time on the host's threads
+    chunks = [np.arange(j, min(n, j + 256)) for j in range(0, n, 256)]
+    bad = 0
+    with ThreadPoolExecutor(max_workers=8) as ex:
+        for k, v in enumerate(ex.map(lambda c: minplus_fixed_point_violations(C, g, c), chunks)):
+            bad += v
+            if k % 32 == 31:
+                print(f"  fixed point: {k + 1} of {len(chunks)} column chunks, {bad} violations", flush=True)
+    assert bad == 0
     rng = np.random.default_rng(3)
     src = np.concatenate([[0, n - 1, n // 2], rng.choice(n, 5, replace=False)])
     rows = O.dijkstra_rows(g, src)           # rows: distances from each source

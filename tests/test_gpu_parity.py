@@ -1,8 +1,9 @@
 """Parity of the HIP path with the oracle, through the C ABI (libpathpack_hip.so), on one MI355X.
 
-Bit-exact for MinPlus / MaxPlus / MaxMin / MinMax / OrAnd (integer-valued weights), relative error <= 1e-12 for
-PlusProd in float64 (1e-5 in float32).  Both sides use the same symbolic structure, so the factors themselves are
-compared, as the reference's GPU suite does (test/gpu/test_factor.jl:31,52).
+Bit-exact for MinPlus / MaxPlus / MaxMin / MinMax / OrAnd (integer-valued weights).  PlusProd in float64: relative
+error <= 1e-12 for factors, stars, rows, columns and solves (the contract).  PlusProd in float32: 2e-3 relative
+(float32 rounding compounds along paths of tens of arcs; see rtol_for).  Both sides use the same symbolic structure,
+so the factors themselves are compared, as the reference's GPU suite does (test/gpu/test_factor.jl:31,52).
 """
 
 import numpy as np
@@ -50,7 +51,7 @@ def compare_factor(s, F, Fo, dtype):
     e = F.export()
     if s == O.PLUSPROD:
         for a, b in ((e["LD"], Fo.LD), (e["LL"], Fo.LL), (e["UL"], Fo.UL)):
-            assert_star_equal(s, a, b, rtol=1e-10 if np.dtype(dtype) == np.float64 else 1e-4)
+            assert_star_equal(s, a, b, rtol=1e-12 if np.dtype(dtype) == np.float64 else 1e-4)
         return
     assert np.array_equal(bits(e["LD"]), bits(Fo.LD))
     assert np.array_equal(bits(e["LL"]), bits(Fo.LL))
@@ -70,7 +71,7 @@ def test_factor_and_star_match_oracle(name, s, fdtype):
     compare_factor(s, F, Fo, dtype)
     C = P.Matrix(F)
     Co = O.star(Fo)
-    assert_star_equal(s, C, Co, rtol=rtol_for(s, dtype) * (10 if np.dtype(dtype) == np.float64 else 1))
+    assert_star_equal(s, C, Co, rtol=rtol_for(s, dtype))
 
 
 BLOCK_GRAPHS = {
@@ -311,7 +312,7 @@ def test_star_rows_and_cols_match_oracle(name, s, fdtype):
     print(f"case {name} s={s} dtype={np.dtype(dtype)} n={n}", flush=True)
     sym, F, Fo = both(g, s, dtype)
     Co = O.star(Fo)
-    rtol = rtol_for(s, dtype) * (10 if np.dtype(dtype) == np.float64 else 1)
+    rtol = rtol_for(s, dtype)
     rng = np.random.default_rng(7)
     sets = {"first": np.array([0]), "last": np.array([n - 1]),
             "subset": rng.choice(n, size=min(n, 37), replace=False),
@@ -361,7 +362,7 @@ def test_refactor_new_weights_same_pattern(s, fdtype):
     assert np.array_equal(bits(C), bits(P.Matrix(F2)))
     assert not np.array_equal(bits(C), bits(C1))
     Fo = O.factor(s, oracle_sym(sym), g2.colptr, g2.rowval, g2.nzval)
-    assert_star_equal(s, C, O.star(Fo), rtol=rtol_for(s, dtype) * 10)
+    assert_star_equal(s, C, O.star(Fo), rtol=rtol_for(s, dtype))
     # device-resident values, then back to the first weights
     dnz = P.DeviceArray.from_numpy(np.ascontiguousarray(g1.nzval).reshape(-1, 1))
     P.lu_(F, dnz)
@@ -394,5 +395,72 @@ def test_star_with_minimum_degree_ordering(name, s, fdtype):
     Fo = O.factor(s, oracle_sym(sym), g.colptr, g.rowval, g.nzval)
     compare_factor(s, F, Fo, dtype)
     C = P.Matrix(F)
-    assert_star_equal(s, C, O.star(Fo), rtol=rtol_for(s, dtype) * 10)
-    assert_star_equal(s, C, P.mstar(SEMIRINGS[s], g), rtol=rtol_for(s, dtype) * 10)
+    assert_star_equal(s, C, O.star(Fo), rtol=rtol_for(s, dtype))
+    assert_star_equal(s, C, P.mstar(SEMIRINGS[s], g), rtol=rtol_for(s, dtype))
+
+
+POISON_GRAPHS = {
+    # a 64-wide star block whose component rows reach far outside its subtree (the padded K steps of the backward
+    # block GEMM once read such rows before anything wrote them)
+    "digraph300": lambda: W.random_digraph(300, 0.01, 3),
+    "grid15x13x11": lambda: W.grid((15, 13, 11)),
+    "grid16x17x15": lambda: W.grid((16, 17, 15)),
+}
+
+
+@pytest.mark.parametrize("name", list(POISON_GRAPHS))
+@pytest.mark.parametrize("s,fdtype", [(O.PLUSPROD, np.float64), (O.PLUSPROD, np.float32), (O.MINPLUS, np.float32),
+                                      (O.MAXPLUS, np.float64), (O.ORAND, np.float32)])
+def test_star_with_poisoned_buffers_matches_oracle(name, s, fdtype):
+    """With every sweep buffer filled with NaN (-1 for OrAnd) before the sweeps (pp_set_debug, PP_DEBUG_POISON), the
+    star, its rows and columns for a batch of sources, and the solves equal the oracle's: no kernel reads an element
+    that nothing wrote.  Without the poison such a read returns whatever an earlier call left in the pool."""
+    dtype = dtype_for(s, fdtype)
+    g = weighted(POISON_GRAPHS[name](), s, dtype)
+    print(f"case poison {name} s={s} dtype={np.dtype(dtype)}", flush=True)
+    ctx = P.context(0)
+    ctx.set_poison(True)
+    try:
+        sym, F, Fo = both(g, s, dtype)
+        Co = O.star(Fo)
+        rtol = rtol_for(s, dtype)
+        assert_star_equal(s, P.Matrix(F), Co, rtol=rtol)
+        assert_star_equal(s, P.mstar(SEMIRINGS[s], g, sym=sym), Co, rtol=rtol)
+        src = np.random.default_rng(5).choice(g.n, size=23, replace=False)
+        assert_star_equal(s, P.star_rows(F, src), Co[src, :], rtol=rtol)
+        assert_star_equal(s, P.star_cols(F, src), Co[:, src], rtol=rtol)
+        B = np.full((g.n, src.size), O.zero(s, dtype), dtype=dtype, order="F")
+        B[src, np.arange(src.size)] = O.one(s, dtype)
+        assert_star_equal(s, P.lmul_(F, B.copy(order="F")), Co[:, src], rtol=rtol)
+        assert_star_equal(s, P.rmul_(np.asfortranarray(B.T), F), Co[src, :], rtol=rtol)
+    finally:
+        ctx.set_poison(False)
+
+
+def test_oversized_requests_are_refused_before_launch():
+    """A star larger than the device's memory is refused with PP_ENOMEM before anything is queued (the reference
+    refuses the same before any work, test/gpu/test_api.jl:195-201): pp_mstar returns no factor, pp_star on a small
+    factor of the same graph refuses too, and the context keeps working.  n = 300000 in Float32 is a 360 GB star."""
+    import ctypes
+
+    n = 300_000
+    src = np.arange(n - 1)
+    g = W.from_arcs(n, src, src + 1, np.ones(n - 1, np.float32))
+    sym = P.symbolic(g)
+    ctx = P.context(0)
+    out = np.zeros(16, np.float32)
+    fac = ctypes.c_void_p()
+    st = P.lib().pp_mstar(ctx.handle, sym.handle, O.MINPLUS, 0, ctypes.c_void_p(g.nzval.ctypes.data), 0,
+                          ctypes.c_void_p(out.ctypes.data), n, 0, ctypes.byref(fac))
+    assert st == 2, P.lib().pp_last_error(ctx.handle)   # PP_ENOMEM
+    assert not fac.value
+    assert b"nothing was launched" in P.lib().pp_last_error(ctx.handle)
+    F = P.mlu(P.MinPlus(), g, sym=sym)                  # the factor alone is small
+    st = P.lib().pp_star(ctx.handle, F.handle, ctypes.c_void_p(out.ctypes.data), n, 0)
+    assert st == 2, P.lib().pp_last_error(ctx.handle)
+    ctx.synchronize()
+    # the context and the factor still work: rows of the star of the path graph are distances along it
+    R = P.star_rows(F, [0, n - 1])
+    assert R[0, 0] == 0 and R[0, n - 1] == n - 1 and R[1, 0] == np.inf
+    small = weighted(W.random_digraph(90, 0.05, 12), O.MINPLUS, np.float32)
+    assert np.array_equal(P.mstar(P.MinPlus(), small), O.floyd_warshall(O.MINPLUS, small.dense(np.float32(np.inf))))

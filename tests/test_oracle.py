@@ -126,52 +126,110 @@ def test_grid_minplus_vs_dijkstra():
     assert np.array_equal(C, O.dijkstra_rows(g))
 
 
-def test_solves_are_rows_and_columns_of_the_star():
-    g = weighted(W.random_digraph(120, 0.03, 5), O.MINPLUS, np.float64)
+ALL = [O.MINPLUS, O.MAXPLUS, O.MAXMIN, O.MINMAX, O.PLUSPROD, O.ORAND]
+
+
+def semiring_matmul(s, A, B):
+    """A (x) B over the semiring by brute force (numpy broadcasting; PlusProd by BLAS)."""
+    if s == O.PLUSPROD:
+        return A @ B
+    C = np.full((A.shape[0], B.shape[1]), O.zero(s, A.dtype), dtype=A.dtype)
+    for k in range(A.shape[1]):
+        C = O.plus(s, C, O.times(s, A[:, k:k + 1], B[k:k + 1, :]))
+    return C
+
+
+def dense_rhs(s, dtype, shape, rng):
+    if s == O.ORAND:
+        return rng.integers(0, 128, shape).astype(np.int32)
+    if s == O.PLUSPROD:
+        return rng.random(shape).astype(dtype)
+    B = rng.integers(0, 50, shape).astype(dtype)
+    B[rng.random(shape) < 0.3] = O.zero(s, dtype)
+    return B
+
+
+@pytest.mark.parametrize("s", ALL)
+def test_solves_are_rows_and_columns_of_the_star(s):
+    """lmul!(F, I) and rmul!(I, F) are the star itself (abstract_slu.jl:123-145: B <- A* B, B <- B A*), and for dense
+    right-hand sides lmul!(F, B) = A* (x) B and rmul!(B, F) = B (x) A*, with the star pinned against Floyd-Warshall
+    or (I - A)^-1 and the products computed by brute force; all six semirings."""
+    dtype = dtype_for(s)
+    g = weighted(W.random_digraph(120, 0.03, 5), s, dtype)
     sym = P.symbolic(g)
-    F = O.factor(O.MINPLUS, oracle_sym(sym), g.colptr, g.rowval, g.nzval)
+    F = O.factor(s, oracle_sym(sym), g.colptr, g.rowval, g.nzval)
     C = O.star(F)
-    I = np.full((g.n, g.n), np.inf)
-    np.fill_diagonal(I, 0)
-    assert np.array_equal(O.rmul(F, I), C)
-    assert np.array_equal(O.lmul(F, I), C)
+    ref = O.plusprod_inverse(g.dense(0.0)) if s == O.PLUSPROD else O.floyd_warshall(s, g.dense(O.zero(s, dtype)))
+    assert_star_equal(s, C, ref)
+    I = np.full((g.n, g.n), O.zero(s, dtype), dtype=dtype)
+    np.fill_diagonal(I, O.one(s, dtype))
+    assert_star_equal(s, O.rmul(F, I), C)
+    assert_star_equal(s, O.lmul(F, I), C)
+    rng = np.random.default_rng(s)
+    B = dense_rhs(s, dtype, (g.n, 7), rng)
+    assert_star_equal(s, O.lmul(F, B), semiring_matmul(s, ref, B))
+    Bt = np.asfortranarray(dense_rhs(s, dtype, (5, g.n), rng))
+    assert_star_equal(s, O.rmul(F, Bt), semiring_matmul(s, Bt, ref))
 
 
-def test_dense_sgemx_vs_brute_force():
+@pytest.mark.parametrize("s", ALL)
+def test_dense_sgemx_vs_brute_force(s):
+    """sgemx!: C <- C (+) A (x) B (dense/sgemx.jl:606-635) against a brute-force loop over k for every semiring, and
+    PlusProd against BLAS (A B + C)."""
     rng = np.random.default_rng(0)
-    A = rng.integers(0, 1000, (37, 19)).astype(np.float32)
-    B = rng.integers(0, 1000, (19, 23)).astype(np.float32)
-    A[rng.random(A.shape) < 0.1] = np.inf
-    B[rng.random(B.shape) < 0.1] = np.inf
-    C = rng.integers(0, 3000, (37, 23)).astype(np.float32)
-    ref = np.minimum(C, (A[:, :, None] + B[None, :, :]).min(axis=1))
-    assert np.array_equal(O.sgemx(O.MINPLUS, A, B, C), ref)
-    refmm = np.maximum(C, np.minimum(A[:, :, None], B[None, :, :]).max(axis=1))
-    assert np.array_equal(O.sgemx(O.MAXMIN, A, B, C), refmm)
+    dtype = dtype_for(s, np.float32 if s != O.PLUSPROD else np.float64)
+    if s == O.ORAND:
+        A, B, C = (rng.integers(0, 2 ** 20, sh).astype(np.int32) for sh in ((37, 19), (19, 23), (37, 23)))
+    elif s == O.PLUSPROD:
+        A, B, C = (rng.random(sh) for sh in ((37, 19), (19, 23), (37, 23)))
+    else:
+        A = rng.integers(0, 1000, (37, 19)).astype(dtype)
+        B = rng.integers(0, 1000, (19, 23)).astype(dtype)
+        C = rng.integers(0, 3000, (37, 23)).astype(dtype)
+        A[rng.random(A.shape) < 0.1] = O.zero(s, dtype)
+        B[rng.random(B.shape) < 0.1] = O.zero(s, dtype)
+    got = O.sgemx(s, A, B, C)
+    if s == O.PLUSPROD:
+        ref = A @ B + C
+        assert np.max(np.abs(got - ref) / np.abs(ref)) < 1e-14
+        return
+    ref = O.plus(s, C, semiring_matmul(s, A, B))
+    assert np.array_equal(bits(got), bits(ref))
+    # the same with every (x) spelled out for MinPlus / MaxMin
+    if s == O.MINPLUS:
+        assert np.array_equal(got, np.minimum(C, (A[:, :, None] + B[None, :, :]).min(axis=1)))
+    if s == O.MAXMIN:
+        assert np.array_equal(got, np.maximum(C, np.minimum(A[:, :, None], B[None, :, :]).max(axis=1)))
 
 
-@pytest.mark.parametrize("s", [O.MINPLUS, O.MAXMIN, O.ORAND])
+@pytest.mark.parametrize("s", ALL)
 def test_getrf_star_gives_the_closure(s):
     """A* = U* L* for a dense front: the semiring product of the batched kernel's TU and TL is Floyd-Warshall's
-    closure of A (dense/sgetrf.jl:151-175; batched/sgetrf.jl:11-120)."""
-    dtype = dtype_for(s, np.float32)
+    closure of A (dense/sgetrf.jl:151-175; batched/sgetrf.jl:11-120); for PlusProd it is (I - A)^-1, and MaxPlus
+    takes nonpositive weights (no positive cycle)."""
+    dtype = dtype_for(s, np.float32 if s != O.PLUSPROD else np.float64)
     rng = np.random.default_rng(1)
     nb, batch = 24, 3
     if s == O.ORAND:
         A = rng.integers(0, 64, (batch, nb, nb)).astype(np.int32)
+    elif s == O.PLUSPROD:
+        A = rng.random((batch, nb, nb)) * (0.9 / nb)
     else:
         A = rng.integers(0, 1000, (batch, nb, nb)).astype(dtype)
-        A[rng.random(A.shape) < 0.1] = np.inf if s == O.MINPLUS else -np.inf
-        if s == O.MINPLUS:
+        if s == O.MAXPLUS:
+            A = -A
+        A[rng.random(A.shape) < 0.1] = O.zero(s, dtype)
+        if s in (O.MINPLUS, O.MAXPLUS):
             A[:, np.arange(nb), np.arange(nb)] = 0
     LU, TL, TU = O.getrf_star_batched(s, A)
     for b in range(batch):
         a = A[b].T   # each front is column-major: element (i, j) at A[b][j, i]
         tu, tl = TU[b].T, TL[b].T
-        prod = np.full((nb, nb), O.zero(s, dtype), dtype=dtype)
-        for k in range(nb):
-            prod = O.plus(s, prod, O.times(s, tu[:, k:k + 1], tl[k:k + 1, :]))
-        assert np.array_equal(prod, O.floyd_warshall(s, a))
+        prod = semiring_matmul(s, tu, tl)
+        if s == O.PLUSPROD:
+            assert_star_equal(s, prod, O.plusprod_inverse(a), rtol=1e-12)
+        else:
+            assert np.array_equal(bits(prod), bits(O.floyd_warshall(s, a)))
 
 
 def test_plusprod_grid_vs_inverse():

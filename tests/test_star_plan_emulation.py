@@ -52,12 +52,19 @@ GRAPHS = {
     "grid9x9x9": lambda: W.grid((9, 9, 9)),                # an 82-column front: a 64 block and an 18 panel
     "components": lambda: W.disjoint_union([W.grid((10, 10, 9)), W.grid((30, 29)), W.rgg(300, seed=5)],
                                            isolated=3, name="components"),
+    # one 64-wide block whose component rows reach far outside its subtree: the padded K steps of the backward
+    # block GEMM read rows that nothing has written yet (NaN under PlusProd before the fix)
+    "digraph300": lambda: W.random_digraph(300, 0.01, 3),
 }
 
-ALL = [(O.MINPLUS, np.float32), (O.MINPLUS, np.float64), (O.MAXMIN, np.float32), (O.MAXPLUS, np.float64),
-       (O.PLUSPROD, np.float64), (O.ORAND, np.float32)]
-FEW = [(O.MINPLUS, np.float32), (O.MINPLUS, np.float64), (O.PLUSPROD, np.float64)]
-CASES = [(name, s, d) for name in GRAPHS for (s, d) in (ALL if name in ("grid9x9x9", "components") else FEW)]
+# X starts as NaN (-1 for OrAnd) in the replay, so every semiring checks that no value read before it is written
+# reaches a stored result
+ALL = [(O.MINPLUS, np.float32), (O.MINPLUS, np.float64), (O.MAXPLUS, np.float32), (O.MAXPLUS, np.float64),
+       (O.MAXMIN, np.float32), (O.MINMAX, np.float64), (O.PLUSPROD, np.float32), (O.PLUSPROD, np.float64),
+       (O.ORAND, np.float32)]
+FEW = [(O.MINPLUS, np.float32), (O.MINPLUS, np.float64), (O.PLUSPROD, np.float32), (O.PLUSPROD, np.float64)]
+CASES = [(name, s, d) for name in GRAPHS
+         for (s, d) in (ALL if name in ("grid9x9x9", "components", "digraph300") else FEW)]
 
 
 @pytest.mark.parametrize("name,s,fdtype", CASES)
