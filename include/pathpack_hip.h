@@ -12,6 +12,7 @@
  *   sgetre! (many k)      src/CPU/chordal_slu.jl:445-493     -> pp_star_sources   (rows / columns of A*)
  *   lmul!(F, B)           src/CPU/abstract_slu.jl:131-134    -> pp_lmul
  *   rmul!(B, F)           src/CPU/abstract_slu.jl:142-145    -> pp_rmul
+ *   lmul!/rmul! with transpose(F) or F'  (sgetrs!, chordal_slu.jl:337)  -> pp_sgetrs
  *   sgemx!(s, C, A, B)    src/CPU/dense/sgemx.jl:26-60       -> pp_sgemx           (dense kernel, device operands)
  *   front LU + stars      ext/PATHPACKCUDAExt/batched/sgetrf.jl:11-120 -> pp_getrf_star_batched
  *
@@ -159,6 +160,17 @@ pp_status pp_lmul(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int64_t 
 /* rmul!(B, F): B (nrhs x n, column-major, ldb >= nrhs) <- B A*, the least solution of X = X A (+) B.
  * (abstract_slu.jl:142-145) */
 pp_status pp_rmul(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int64_t nrhs, int on_device);
+/* The solves with the factor or its transpose: sgetrs!(F, side, trans, B) (src/CPU/chordal_slu.jl:337-377), which
+ * lmul!(F, B) / rmul!(B, F) call for F, transpose(F) and F' (abstract_slu.jl:131-145, MaybeTransSLU).
+ *   side = PP_SIDE_LEFT:  B (n x nrhs, ldb >= n)    <- op(A)* B, the least solution of X = op(A) X (+) B
+ *   side = PP_SIDE_RIGHT: B (nrhs x n, ldb >= nrhs) <- B op(A)*, the least solution of X = X op(A) (+) B
+ * with op(A) = A (PP_NOTRANS) or A^T (PP_TRANS; for these real semirings F' is transpose(F)).  (A^T)* = (A*)^T, so the
+ * transposed solves run the same sweeps as the plain ones of the other side.  B is a device pointer when
+ * on_device != 0. */
+enum { PP_SIDE_LEFT = 0, PP_SIDE_RIGHT = 1 };
+enum { PP_NOTRANS = 0, PP_TRANS = 1 };
+pp_status pp_sgetrs(pp_ctx *ctx, const pp_fac *fac, int side, int trans, void *B, int64_t ldb, int64_t nrhs,
+                    int on_device);
 
 /* ===== dense kernels (device operands) ===== */
 

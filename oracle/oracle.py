@@ -164,6 +164,21 @@ def lmul(F: Factor, B: np.ndarray) -> np.ndarray:
     return B
 
 
+def lmul_t(F: Factor, B: np.ndarray) -> np.ndarray:
+    """lmul!(transpose(F), B): B (n x nrhs) <- (A^T)* B, the least solution of X = A^T X (+) B.  The reference
+    runs sgetrs!(P, Val(:L), Val(:T), B) (src/CPU/abstract_slu.jl:131-134, chordal_slu.jl:337-377); since
+    (A^T)* = (A*)^T this is rmul!(B^T, F)^T, which the oracle computes with the same triangular sweeps."""
+    B = np.asarray(B)
+    if B.ndim == 1:
+        B = B.reshape(-1, 1)
+    return np.asfortranarray(rmul(F, np.asfortranarray(B.T)).T)
+
+
+def rmul_t(F: Factor, B: np.ndarray) -> np.ndarray:
+    """rmul!(B, transpose(F)): B (nrhs x n) <- B (A^T)* = (A* B^T)^T (sgetrs!(P, Val(:R), Val(:T), B))."""
+    return np.asfortranarray(lmul(F, np.asfortranarray(np.asarray(B).T)).T)
+
+
 def star(F: Factor, rows: tuple[int, int] | None = None, relabel: bool = True, nthreads: int = 0) -> np.ndarray:
     """Matrix(F): the full star in the original labels (n x n, column-major); ``rows`` restricts the computed rows
     of the permuted star (a timing sample), in which case ``relabel=False`` keeps the permuted labels."""

@@ -717,8 +717,8 @@ pp_status pp_star_sources(pp_ctx *ctx, const pp_fac *fac, int which, int64_t nsr
     return PP_OK;
 }
 
-static pp_status solve(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int64_t nrhs, int on_device, bool left) {
-    const char *name = left ? "pp_lmul" : "pp_rmul";
+static pp_status solve(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int64_t nrhs, int on_device, bool left,
+                       bool trans, const char *name) {
     if (!ctx || !fac || (!B && nrhs > 0)) return fail(ctx, PP_EINVAL, std::string(name) + ": null argument");
     const i64 n = fac->sym->S.n;
     if (nrhs < 0) return fail(ctx, PP_EINVAL, std::string(name) + ": nrhs < 0");
@@ -730,7 +730,7 @@ static pp_status solve(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int
     size_t freeb = 0, totalb = 0;
     CHECK_HIP(ctx, mem_free(ctx, &freeb, &totalb));
     const size_t need = (size_t)n * nrhs * es + (on_device ? 0 : bytesB);
-    if (need > freeb) return fail(ctx, PP_ENOMEM, std::string(name) + ": not enough device memory");
+    if (need > freeb) return fail(ctx, PP_ENOMEM, std::string(name) + ": not enough device memory; nothing was launched");
     void *dB = B;
     if (!on_device) {
         CHECK_HIP(ctx, dev_malloc(ctx, &dB, bytesB));
@@ -740,7 +740,7 @@ static pp_status solve(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int
             return fail(ctx, PP_EHIP, std::string(name) + ": upload failed");
         }
     }
-    std::string e = left ? pp::device_lmul(ctx, fac, dB, ldb, nrhs) : pp::device_rmul(ctx, fac, dB, ldb, nrhs);
+    std::string e = pp::device_solve(ctx, fac, dB, ldb, nrhs, left, trans);
     hipError_t se = hipStreamSynchronize(ctx->stream);
     if (e.empty() && se == hipSuccess && !on_device) se = hipMemcpy(B, dB, bytesB, hipMemcpyDeviceToHost);
     if (!on_device) hipFree(dB);
@@ -750,11 +750,18 @@ static pp_status solve(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int
 }
 
 pp_status pp_lmul(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int64_t nrhs, int on_device) {
-    return solve(ctx, fac, B, ldb, nrhs, on_device, true);
+    return solve(ctx, fac, B, ldb, nrhs, on_device, true, false, "pp_lmul");
 }
 
 pp_status pp_rmul(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int64_t nrhs, int on_device) {
-    return solve(ctx, fac, B, ldb, nrhs, on_device, false);
+    return solve(ctx, fac, B, ldb, nrhs, on_device, false, false, "pp_rmul");
+}
+
+pp_status pp_sgetrs(pp_ctx *ctx, const pp_fac *fac, int side, int trans, void *B, int64_t ldb, int64_t nrhs,
+                    int on_device) {
+    if (side != PP_SIDE_LEFT && side != PP_SIDE_RIGHT) return fail(ctx, PP_EINVAL, "pp_sgetrs: side must be PP_SIDE_LEFT or PP_SIDE_RIGHT");
+    if (trans != PP_NOTRANS && trans != PP_TRANS) return fail(ctx, PP_EINVAL, "pp_sgetrs: trans must be PP_NOTRANS or PP_TRANS");
+    return solve(ctx, fac, B, ldb, nrhs, on_device, side == PP_SIDE_LEFT, trans == PP_TRANS, "pp_sgetrs");
 }
 
 // ===== dense kernels =====

@@ -15,7 +15,8 @@ template <class S> std::string packs_impl(pp_ctx *ctx, pp_fac *fac);
 template <class S> std::string star_impl(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc, int host);
 template <class S>
 std::string star_src_impl(pp_ctx *ctx, const pp_fac *fac, const RowSub &R, i64 nsrc, int cols, void *out, i64 ldo);
-template <class S> std::string solve_impl(pp_ctx *ctx, const pp_fac *fac, void *B, i64 ldb, i64 nrhs, bool left);
+template <class S>
+std::string solve_impl(pp_ctx *ctx, const pp_fac *fac, void *B, i64 ldb, i64 nrhs, bool left, bool trans);
 template <class S>
 std::string gemm_impl(pp_ctx *ctx, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B, i64 ldb, void *C, i64 ldc);
 template <class S> std::string getrf_impl(pp_ctx *ctx, i64 nb, i64 batch, void *A, void *TL, void *TU);
@@ -119,12 +120,8 @@ std::string device_star_sources(pp_ctx *ctx, const pp_fac *fac, const RowSub &R,
     PP_DISPATCH(fac->semiring, fac->dtype, star_src_impl<S>(ctx, fac, R, nsrc, cols, out, ldo));
 }
 
-std::string device_rmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs) {
-    PP_DISPATCH(fac->semiring, fac->dtype, solve_impl<S>(ctx, fac, d_B, ldb, nrhs, false));
-}
-
-std::string device_lmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs) {
-    PP_DISPATCH(fac->semiring, fac->dtype, solve_impl<S>(ctx, fac, d_B, ldb, nrhs, true));
+std::string device_solve(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs, bool left, bool trans) {
+    PP_DISPATCH(fac->semiring, fac->dtype, solve_impl<S>(ctx, fac, d_B, ldb, nrhs, left, trans));
 }
 
 std::string device_sgemx(pp_ctx *ctx, int sr, int dt, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B,

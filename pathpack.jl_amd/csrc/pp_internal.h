@@ -261,8 +261,8 @@ std::string device_star(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc, int 
 // Rows (cols = 0: out[k, j] = A*[src_k, j], nsrc x n, leading dimension ldo) or columns (cols = 1: out[i, k] =
 // A*[i, src_k], n x nsrc) of the star for the sources of R (device copies uploaded), into device memory.
 std::string device_star_sources(pp_ctx *ctx, const pp_fac *fac, const RowSub &R, i64 nsrc, int cols, void *out, i64 ldo);
-std::string device_rmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs);
-std::string device_lmul(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs);
+// The solves on B in device memory: left (lmul!, B n x nrhs) or right (rmul!, B nrhs x n), with A or A^T.
+std::string device_solve(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs, bool left, bool trans);
 std::string device_sgemx(pp_ctx *ctx, int sr, int dt, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B,
                          i64 ldb, void *C, i64 ldc);
 std::string device_getrf_star_batched(pp_ctx *ctx, int sr, int dt, i64 nb, i64 batch, void *A, void *TL, void *TU);

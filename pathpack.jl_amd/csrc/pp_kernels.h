@@ -2475,12 +2475,19 @@ template <class S> struct StarSrcRun {
     }
 };
 
+// The solves (chordal_slu.jl:337-377 -> chordal/sgetrs.jl:29-51).  The right-hand sides go into Y (nrhs x n, one
+// row per right-hand side, vertex-major in the elimination order): rmul!'s B (nrhs x n) by a column permutation,
+// lmul!'s B (n x nrhs) transposed.  On Y the sweeps compute either Y <- Y A* (U forward, then L backward; the panel
+// blocks as stored) or Y <- Y (A*)^T (L^T forward, then U^T backward; the blocks transposed):
+//   rmul!(B, F)            Y = B     Y <- Y A*        lmul!(F, B)            Y = B^T   Y <- Y (A*)^T
+//   rmul!(B, transpose(F)) Y = B     Y <- Y (A*)^T    lmul!(transpose(F), B) Y = B^T   Y <- Y A*
+// since (A^T)* = (A*)^T.  For the real semirings here transpose(F) and adjoint(F) are the same.
 template <class S> struct SolveRun {
     pp_ctx *ctx;
     const pp_fac *fac;
     void *B;
     i64 ldb, nrhs;
-    bool left;
+    bool left, trans;
     std::string err;
     void operator()() { err = run(); }
     std::string run() {
@@ -2493,25 +2500,26 @@ template <class S> struct SolveRun {
         std::string pe = poison_fill(ctx, Y, (size_t)(n * nrhs) * sizeof(T));
         if (!pe.empty()) return pe;
         timer_start(ctx, 4);
+        const dim3 g((unsigned)((n + 31) / 32), (unsigned)((nrhs + 31) / 32));
+        auto layout = [&](int dir) {
+            if (left) k_transpose_perm<T><<<g, NT, 0, st>>>((T *)B, ldb, Y, n, nrhs, fac->plan.invp, dir);
+            else k_permute_cols<T><<<(unsigned)std::min<i64>(n, 65536), NT, 0, st>>>((T *)B, ldb, Y, n, nrhs,
+                                                                                      fac->plan.invp, dir);
+        };
+        layout(0);
+        LAUNCHCHK();
         std::string e;
-        if (!left) {
-            // rmul!: B (nrhs x n) <- B A*: U forward, then L backward (chordal/sgetrs.jl:29-51)
-            k_permute_cols<T><<<(unsigned)std::min<i64>(n, 65536), NT, 0, st>>>((T *)B, ldb, Y, n, nrhs, fac->plan.invp, 0);
-            LAUNCHCHK();
+        if (left == trans) {
+            // Y <- Y A*: U forward, then L backward
             e = run_sweeps<S>(ctx, fac, true, 0, Y, nrhs, false, nrhs, fac->Upack);
             if (e.empty()) e = run_sweeps<S>(ctx, fac, false, 0, Y, nrhs, false, nrhs, fac->Lpack);
-            if (!e.empty()) return e;
-            k_permute_cols<T><<<(unsigned)std::min<i64>(n, 65536), NT, 0, st>>>((T *)B, ldb, Y, n, nrhs, fac->plan.invp, 1);
         } else {
-            // lmul!: B (n x nrhs) <- A* B: L forward, then U backward, run on B^T
-            dim3 g((unsigned)((n + 31) / 32), (unsigned)((nrhs + 31) / 32));
-            k_transpose_perm<T><<<g, NT, 0, st>>>((T *)B, ldb, Y, n, nrhs, fac->plan.invp, 0);
-            LAUNCHCHK();
+            // Y <- Y (A*)^T: L^T forward, then U^T backward
             e = run_sweeps<S>(ctx, fac, true, 1, Y, nrhs, false, nrhs, fac->Lpack);
             if (e.empty()) e = run_sweeps<S>(ctx, fac, false, 1, Y, nrhs, false, nrhs, fac->Upack);
-            if (!e.empty()) return e;
-            k_transpose_perm<T><<<g, NT, 0, st>>>((T *)B, ldb, Y, n, nrhs, fac->plan.invp, 1);
         }
+        if (!e.empty()) return e;
+        layout(1);
         LAUNCHCHK();
         timer_stop(ctx, 4);
         HIPCHK(hipFreeAsync(Y, st));
@@ -2586,8 +2594,9 @@ std::string star_src_impl(pp_ctx *ctx, const pp_fac *fac, const RowSub &R, i64 n
     r();
     return r.err;
 }
-template <class S> std::string solve_impl(pp_ctx *ctx, const pp_fac *fac, void *B, i64 ldb, i64 nrhs, bool left) {
-    SolveRun<S> r{ctx, fac, B, ldb, nrhs, left};
+template <class S>
+std::string solve_impl(pp_ctx *ctx, const pp_fac *fac, void *B, i64 ldb, i64 nrhs, bool left, bool trans) {
+    SolveRun<S> r{ctx, fac, B, ldb, nrhs, left, trans};
     r();
     return r.err;
 }

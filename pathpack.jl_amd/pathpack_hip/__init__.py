@@ -30,7 +30,7 @@ from ._lib import (PathpackArgumentError, PathpackDeviceError, PathpackError, Pa
 
 __all__ = [
     "AbstractSemiring", "MinPlus", "MaxPlus", "MaxMin", "MinMax", "PlusProd", "OrAnd",
-    "szero", "sone", "mlu", "lu_", "mstar", "lmul_", "rmul_", "Matrix", "star_rows", "star_cols", "Factorization", "Symbolic", "symbolic",
+    "szero", "sone", "mlu", "lu_", "mstar", "lmul_", "rmul_", "transpose", "adjoint", "Matrix", "star_rows", "star_cols", "Factorization", "Symbolic", "symbolic",
     "Context", "context", "DeviceArray", "PathpackError", "PathpackArgumentError", "PathpackMemoryError",
     "PathpackUnsupportedError", "PathpackDeviceError",
 ]
@@ -523,9 +523,35 @@ def star_cols(F: Factorization, src, device: bool = False):
     return _star_sources(F, src, 1, device)
 
 
-def _solve(F: Factorization, B, left: bool):
+class TransposedFactorization:
+    """transpose(F) (equivalently adjoint(F) for these real semirings): the factorization of A^T that F implies,
+    (A^T)* = (A*)^T, for lmul_ / rmul_ (the reference's MaybeTransSLU, abstract_slu.jl:131-145)."""
+
+    def __init__(self, F: Factorization):
+        self.parent = F
+
+    @property
+    def shape(self):
+        return self.parent.shape
+
+
+def transpose(F):
+    """transpose(F): lmul_(transpose(F), B) solves X = A^T X (+) B, rmul_(B, transpose(F)) solves X = X A^T (+) B."""
+    return F.parent if isinstance(F, TransposedFactorization) else TransposedFactorization(F)
+
+
+adjoint = transpose
+
+
+def _solve(F, B, left: bool):
     name = "lmul_" if left else "rmul_"
-    fn = lib().pp_lmul if left else lib().pp_rmul
+    trans = isinstance(F, TransposedFactorization)
+    if trans:
+        F = F.parent
+
+    def fn(ctxh, fh, ptr, ld, nrhs, on_dev):
+        return lib().pp_sgetrs(ctxh, fh, 0 if left else 1, 1 if trans else 0, ptr, ld, nrhs, on_dev)
+
     if isinstance(B, np.ndarray):
         if B.dtype != F.dtype:
             raise PathpackArgumentError(_lib.PP_EINVAL, f"{name}: B must have the factor's element type {F.dtype}")
@@ -554,11 +580,13 @@ def _solve(F: Factorization, B, left: bool):
     return B
 
 
-def lmul_(F: Factorization, B):
-    """lmul!(F, B): B <- A* B, the least solution of X = A X (+) B (abstract_slu.jl:131-134)."""
+def lmul_(F, B):
+    """lmul!(F, B): B <- A* B, the least solution of X = A X (+) B (abstract_slu.jl:131-134); with
+    F = transpose(F0), B <- (A^T)* B."""
     return _solve(F, B, True)
 
 
-def rmul_(B, F: Factorization):
-    """rmul!(B, F): B <- B A*, the least solution of X = X A (+) B (abstract_slu.jl:142-145)."""
+def rmul_(B, F):
+    """rmul!(B, F): B <- B A*, the least solution of X = X A (+) B (abstract_slu.jl:142-145); with
+    F = transpose(F0), B <- B (A^T)*."""
     return _solve(F, B, False)

@@ -121,6 +121,46 @@ def test_solves_match_oracle(s):
     assert_star_equal(s, R, O.rmul(Fo, np.asfortranarray(B.T)), rtol=1e-12)
 
 
+@pytest.mark.parametrize("s", ALL)
+def test_transposed_solves_match_oracle(s):
+    """lmul!(transpose(F), B) and rmul!(B, transpose(F)) (pp_sgetrs with PP_TRANS; sgetrs!(P, side, Val(:T), B),
+    chordal_slu.jl:337): B <- (A^T)* B and B <- B (A^T)*, against the oracle, with host and device B; the transposed
+    solve of a matrix equals the plain solve of the transposed matrix."""
+    dtype = dtype_for(s, np.float64)
+    g = weighted(W.random_digraph(260, 0.012, 8), s, dtype)
+    print(f"case transposed solves s={s}", flush=True)
+    sym, F, Fo = both(g, s, dtype)
+    rng = np.random.default_rng(4)
+    k = 29
+    B = np.full((g.n, k), O.zero(s, dtype), dtype=dtype, order="F")
+    B[rng.integers(0, g.n, k), np.arange(k)] = O.one(s, dtype)
+    if s == O.ORAND:
+        B[:, -3:] = rng.integers(0, 128, (g.n, 3)).astype(np.int32)
+    elif s == O.PLUSPROD:
+        B[:, -3:] = rng.random((g.n, 3))
+    else:
+        B[:, -3:] = rng.integers(0, 50, (g.n, 3)).astype(dtype)
+    L = P.lmul_(P.transpose(F), B.copy(order="F"))
+    assert_star_equal(s, L, O.lmul_t(Fo, B), rtol=1e-12)
+    Bt = np.asfortranarray(B.T)
+    R = P.rmul_(Bt.copy(order="F"), P.adjoint(F))
+    assert_star_equal(s, R, O.rmul_t(Fo, Bt), rtol=1e-12)
+    dB = P.DeviceArray.from_numpy(B)
+    P.lmul_(P.transpose(F), dB)
+    assert np.array_equal(bits(dB.numpy()), bits(L))
+    # the factor of A^T gives the same solves untransposed
+    gT = W.Graph(g.n, *_transpose_csc(g), g.name + "T")
+    FT = P.mlu(SEMIRINGS[s], gT)
+    assert_star_equal(s, P.lmul_(FT, B.copy(order="F")), L, rtol=1e-12)
+    assert P.transpose(P.transpose(F)) is F
+
+
+def _transpose_csc(g):
+    A = g.scipy().T.tocsc()
+    A.sort_indices()
+    return A.indptr.astype(np.int64), A.indices.astype(np.int64), A.data.astype(g.nzval.dtype)
+
+
 @pytest.mark.parametrize("name", ["paris", "bunny"])
 def test_factor_matches_reference_fixture(name):
     """The HIP factorization with the reference's own ordering and fronts reproduces the reference's factor of the

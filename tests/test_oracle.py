@@ -170,6 +170,10 @@ def test_solves_are_rows_and_columns_of_the_star(s):
     assert_star_equal(s, O.lmul(F, B), semiring_matmul(s, ref, B))
     Bt = np.asfortranarray(dense_rhs(s, dtype, (5, g.n), rng))
     assert_star_equal(s, O.rmul(F, Bt), semiring_matmul(s, Bt, ref))
+    # transposed solves (lmul!/rmul! with transpose(F)): (A^T)* B and B (A^T)*, against the star's transpose
+    refT = np.ascontiguousarray(ref.T)
+    assert_star_equal(s, O.lmul_t(F, B), semiring_matmul(s, refT, B))
+    assert_star_equal(s, O.rmul_t(F, Bt), semiring_matmul(s, Bt, refT))
 
 
 @pytest.mark.parametrize("s", ALL)
