@@ -171,6 +171,13 @@ enum { PP_SIDE_LEFT = 0, PP_SIDE_RIGHT = 1 };
 enum { PP_NOTRANS = 0, PP_TRANS = 1 };
 pp_status pp_sgetrs(pp_ctx *ctx, const pp_fac *fac, int side, int trans, void *B, int64_t ldb, int64_t nrhs,
                     int on_device);
+/* pp_sgetrs with B in device memory and no device allocation at all.  No counterpart in the reference: for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * solve's scratch (the vertex-major copy of B) is a fixed device array of 64 MiB per device, held until the process
+ * ends; requests with n * nrhs * element size above 64 MiB are refused with PP_EINVAL.  The work is queued on the
+ * context's stream and not waited for (pp_synchronize).  Every call on one device shares that device's array:
+ * calls that overlap on one device (two contexts, two threads) race; calls on one context are ordered. */
+pp_status pp_sgetrs_noalloc(pp_ctx *ctx, const pp_fac *fac, int side, int trans, void *B, int64_t ldb, int64_t nrhs);
 
 /* ===== dense kernels (device operands) ===== */
 

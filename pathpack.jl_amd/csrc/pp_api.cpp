@@ -129,6 +129,14 @@ pp_status pp_init(pp_ctx **out, int device) {
             return fail(nullptr, PP_EHIP, "pp_init: creating the memory pool failed");
         }
     }
+    {
+        // the device address of the allocation-free solves' scratch array, taken once per device (device current)
+        const std::string se = pp::noalloc_scratch_setup(device);
+        if (!se.empty()) {
+            pp_destroy(ctx);
+            return fail(nullptr, PP_EHIP, "pp_init: " + se);
+        }
+    }
     if (hipStreamCreateWithFlags(&ctx->aux_stream, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreateWithFlags(&ctx->aux_from, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&ctx->aux_done, hipEventDisableTiming) != hipSuccess) {
@@ -740,7 +748,7 @@ static pp_status solve(pp_ctx *ctx, const pp_fac *fac, void *B, int64_t ldb, int
             return fail(ctx, PP_EHIP, std::string(name) + ": upload failed");
         }
     }
-    std::string e = pp::device_solve(ctx, fac, dB, ldb, nrhs, left, trans);
+    std::string e = pp::device_solve(ctx, fac, dB, ldb, nrhs, left, trans, nullptr);
     hipError_t se = hipStreamSynchronize(ctx->stream);
     if (e.empty() && se == hipSuccess && !on_device) se = hipMemcpy(B, dB, bytesB, hipMemcpyDeviceToHost);
     if (!on_device) hipFree(dB);
@@ -762,6 +770,31 @@ pp_status pp_sgetrs(pp_ctx *ctx, const pp_fac *fac, int side, int trans, void *B
     if (side != PP_SIDE_LEFT && side != PP_SIDE_RIGHT) return fail(ctx, PP_EINVAL, "pp_sgetrs: side must be PP_SIDE_LEFT or PP_SIDE_RIGHT");
     if (trans != PP_NOTRANS && trans != PP_TRANS) return fail(ctx, PP_EINVAL, "pp_sgetrs: trans must be PP_NOTRANS or PP_TRANS");
     return solve(ctx, fac, B, ldb, nrhs, on_device, side == PP_SIDE_LEFT, trans == PP_TRANS, "pp_sgetrs");
+}
+
+pp_status pp_sgetrs_noalloc(pp_ctx *ctx, const pp_fac *fac, int side, int trans, void *B, int64_t ldb, int64_t nrhs) {
+    if (!ctx || !fac || (!B && nrhs > 0)) return fail(ctx, PP_EINVAL, "pp_sgetrs_noalloc: null argument");
+    if (fac->ctx != ctx) return fail(ctx, PP_EINVAL, "pp_sgetrs_noalloc: the factor belongs to another context");
+    if (side != PP_SIDE_LEFT && side != PP_SIDE_RIGHT)
+        return fail(ctx, PP_EINVAL, "pp_sgetrs_noalloc: side must be PP_SIDE_LEFT or PP_SIDE_RIGHT");
+    if (trans != PP_NOTRANS && trans != PP_TRANS)
+        return fail(ctx, PP_EINVAL, "pp_sgetrs_noalloc: trans must be PP_NOTRANS or PP_TRANS");
+    const bool left = side == PP_SIDE_LEFT;
+    const i64 n = fac->sym->S.n;
+    if (nrhs < 0) return fail(ctx, PP_EINVAL, "pp_sgetrs_noalloc: nrhs < 0");
+    if (left ? ldb < n : ldb < nrhs) return fail(ctx, PP_EINVAL, "pp_sgetrs_noalloc: leading dimension too small");
+    if (nrhs == 0 || n == 0) return PP_OK;
+    const size_t bytes = (size_t)n * (size_t)nrhs * (size_t)pp::dtype_size(fac->dtype);
+    if (bytes > pp::NOALLOC_SCRATCH_BYTES)
+        return fail(ctx, PP_EINVAL, "pp_sgetrs_noalloc: n * nrhs * element size = " + std::to_string(bytes) +
+                                        " bytes is more than the fixed scratch of " +
+                                        std::to_string(pp::NOALLOC_SCRATCH_BYTES) + " bytes (use pp_sgetrs)");
+    void *scr = pp::noalloc_scratch(ctx->device);
+    if (!scr) return fail(ctx, PP_EHIP, "pp_sgetrs_noalloc: the scratch of this device is not set up");
+    CHECK_HIP(ctx, hipSetDevice(ctx->device));
+    std::string e = pp::device_solve(ctx, fac, B, ldb, nrhs, left, trans == PP_TRANS, scr);
+    if (!e.empty()) return fail(ctx, PP_EHIP, "pp_sgetrs_noalloc: " + e);
+    return PP_OK;
 }
 
 // ===== dense kernels =====

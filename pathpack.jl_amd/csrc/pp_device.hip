@@ -3,6 +3,7 @@
 // The kernels and drivers are templates (pp_kernels.h); each pair is instantiated in its own translation unit
 // (pp_inst_*.hip) so that they compile in parallel.
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 #include "pp_internal.h"
@@ -16,10 +17,44 @@ template <class S> std::string star_impl(pp_ctx *ctx, const pp_fac *fac, void *o
 template <class S>
 std::string star_src_impl(pp_ctx *ctx, const pp_fac *fac, const RowSub &R, i64 nsrc, int cols, void *out, i64 ldo);
 template <class S>
-std::string solve_impl(pp_ctx *ctx, const pp_fac *fac, void *B, i64 ldb, i64 nrhs, bool left, bool trans);
+std::string solve_impl(pp_ctx *ctx, const pp_fac *fac, void *B, i64 ldb, i64 nrhs, bool left, bool trans,
+                       void *scratch);
 template <class S>
 std::string gemm_impl(pp_ctx *ctx, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B, i64 ldb, void *C, i64 ldc);
 template <class S> std::string getrf_impl(pp_ctx *ctx, i64 nb, i64 batch, void *A, void *TL, void *TU);
+
+// ===== the scratch of the allocation-free solves (pp_sgetrs_noalloc) =====
+//
+// Y, the vertex-major copy of the right-hand sides, lives in this fixed array instead of a pool allocation.  Every
+// device the library runs on holds its own copy until the process ends.  The array's name is a host-side stand-in, not
+// a device address: host code uses only the address hipGetSymbolAddress returns for each device, taken once per
+// device with that device current (pp_init calls noalloc_scratch_setup).  Every call on one device shares that
+// device's array: calls that overlap on one device (two contexts, two threads) race.  Y is written in full by the
+// layout kernel before any sweep reads it, so nothing in the array needs clearing between calls.
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void *scratch_ptr[MAX_DEVICES] = {};
+}  // namespace
+
+std::string noalloc_scratch_setup(int device) {
+    if (device < 0 || device >= MAX_DEVICES) return "device index beyond the scratch table";
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (scratch_ptr[device]) return "";
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return std::string("hipGetSymbolAddress of the solve scratch: ") + hipGetErrorString(e);
+    scratch_ptr[device] = p;
+    return "";
+}
+
+void *noalloc_scratch(int device) {
+    if (device < 0 || device >= MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    return scratch_ptr[device];
+}
 
 // plain copy, 16 bytes per thread per step (the memory-counter calibration kernel)
 __global__ __launch_bounds__(256) void k_copy16(uint4 *__restrict__ dst, const uint4 *__restrict__ src, i64 n16) {
@@ -120,8 +155,9 @@ std::string device_star_sources(pp_ctx *ctx, const pp_fac *fac, const RowSub &R,
     PP_DISPATCH(fac->semiring, fac->dtype, star_src_impl<S>(ctx, fac, R, nsrc, cols, out, ldo));
 }
 
-std::string device_solve(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs, bool left, bool trans) {
-    PP_DISPATCH(fac->semiring, fac->dtype, solve_impl<S>(ctx, fac, d_B, ldb, nrhs, left, trans));
+std::string device_solve(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs, bool left, bool trans,
+                         void *scratch) {
+    PP_DISPATCH(fac->semiring, fac->dtype, solve_impl<S>(ctx, fac, d_B, ldb, nrhs, left, trans, scratch));
 }
 
 std::string device_sgemx(pp_ctx *ctx, int sr, int dt, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B,

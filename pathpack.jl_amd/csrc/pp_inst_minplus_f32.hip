@@ -6,7 +6,7 @@ template std::string factor_impl<MinPlus<float>>(pp_ctx *, pp_fac *, const void 
 template std::string packs_impl<MinPlus<float>>(pp_ctx *, pp_fac *);
 template std::string star_impl<MinPlus<float>>(pp_ctx *, const pp_fac *, void *, i64, int);
 template std::string star_src_impl<MinPlus<float>>(pp_ctx *, const pp_fac *, const RowSub &, i64, int, void *, i64);
-template std::string solve_impl<MinPlus<float>>(pp_ctx *, const pp_fac *, void *, i64, i64, bool, bool);
+template std::string solve_impl<MinPlus<float>>(pp_ctx *, const pp_fac *, void *, i64, i64, bool, bool, void *);
 template std::string gemm_impl<MinPlus<float>>(pp_ctx *, i64, i64, i64, const void *, i64, const void *, i64, void *, i64);
 template std::string getrf_impl<MinPlus<float>>(pp_ctx *, i64, i64, void *, void *, void *);
 }  // namespace pp

@@ -261,8 +261,15 @@ std::string device_star(pp_ctx *ctx, const pp_fac *fac, void *out, i64 ldc, int 
 // Rows (cols = 0: out[k, j] = A*[src_k, j], nsrc x n, leading dimension ldo) or columns (cols = 1: out[i, k] =
 // A*[i, src_k], n x nsrc) of the star for the sources of R (device copies uploaded), into device memory.
 std::string device_star_sources(pp_ctx *ctx, const pp_fac *fac, const RowSub &R, i64 nsrc, int cols, void *out, i64 ldo);
-// The solves on B in device memory: left (lmul!, B n x nrhs) or right (rmul!, B nrhs x n), with A or A^T.
-std::string device_solve(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs, bool left, bool trans);
+// The solves on B in device memory: left (lmul!, B n x nrhs) or right (rmul!, B nrhs x n), with A or A^T; Y in
+// `scratch` (device memory of at least n * nrhs elements) when it is not null, else in a pool allocation.
+std::string device_solve(pp_ctx *ctx, const pp_fac *fac, void *d_B, i64 ldb, i64 nrhs, bool left, bool trans,
+                         void *scratch);
+// The fixed device array of the allocation-free solves: its size, the per-device set-up (hipGetSymbolAddress with
+// the device current; once per device) and the device address it gave (null before the set-up).
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(64) << 20;
+std::string noalloc_scratch_setup(int device);
+void *noalloc_scratch(int device);
 std::string device_sgemx(pp_ctx *ctx, int sr, int dt, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B,
                          i64 ldb, void *C, i64 ldc);
 std::string device_getrf_star_batched(pp_ctx *ctx, int sr, int dt, i64 nb, i64 batch, void *A, void *TL, void *TU);

@@ -2488,6 +2488,7 @@ template <class S> struct SolveRun {
     void *B;
     i64 ldb, nrhs;
     bool left, trans;
+    void *scratch;                   // Y's memory when not null (at least n * nrhs elements), else a pool allocation
     std::string err;
     void operator()() { err = run(); }
     std::string run() {
@@ -2495,8 +2496,8 @@ template <class S> struct SolveRun {
         const i64 n = fac->sym->S.n;
         hipStream_t st = ctx->stream;
         if (n == 0 || nrhs == 0) return "";
-        T *Y = nullptr;
-        HIPCHK(ctx_alloc(ctx, (void **)&Y, n * nrhs * sizeof(T), st));
+        T *Y = (T *)scratch;
+        if (!Y) HIPCHK(ctx_alloc(ctx, (void **)&Y, n * nrhs * sizeof(T), st));
         std::string pe = poison_fill(ctx, Y, (size_t)(n * nrhs) * sizeof(T));
         if (!pe.empty()) return pe;
         timer_start(ctx, 4);
@@ -2522,7 +2523,7 @@ template <class S> struct SolveRun {
         layout(1);
         LAUNCHCHK();
         timer_stop(ctx, 4);
-        HIPCHK(hipFreeAsync(Y, st));
+        if (!scratch) HIPCHK(hipFreeAsync(Y, st));
         return "";
     }
 };
@@ -2595,8 +2596,9 @@ std::string star_src_impl(pp_ctx *ctx, const pp_fac *fac, const RowSub &R, i64 n
     return r.err;
 }
 template <class S>
-std::string solve_impl(pp_ctx *ctx, const pp_fac *fac, void *B, i64 ldb, i64 nrhs, bool left, bool trans) {
-    SolveRun<S> r{ctx, fac, B, ldb, nrhs, left, trans};
+std::string solve_impl(pp_ctx *ctx, const pp_fac *fac, void *B, i64 ldb, i64 nrhs, bool left, bool trans,
+                       void *scratch) {
+    SolveRun<S> r{ctx, fac, B, ldb, nrhs, left, trans, scratch};
     r();
     return r.err;
 }

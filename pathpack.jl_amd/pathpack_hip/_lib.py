@@ -20,7 +20,7 @@ EXPORTS = [
     "pp_factor", "pp_factor_device", "pp_refactor", "pp_fac_export", "pp_fac_destroy",
     "pp_star", "pp_mstar", "pp_star_sources", "pp_lmul", "pp_rmul", "pp_sgemx", "pp_getrf_star_batched",
     "pp_buffer_alloc", "pp_buffer_free", "pp_upload", "pp_download", "pp_copy", "pp_calibrate_valu", "pp_set_timing",
-    "pp_get_timing", "pp_set_debug", "pp_sgetrs",
+    "pp_get_timing", "pp_set_debug", "pp_sgetrs", "pp_sgetrs_noalloc",
 ]
 
 
@@ -107,6 +107,7 @@ def lib() -> ctypes.CDLL:
         L.pp_get_timing.argtypes = [c_vp, ctypes.POINTER(ctypes.c_double)]
         L.pp_set_debug.argtypes = [c_vp, ctypes.c_int]
         L.pp_sgetrs.argtypes = [c_vp, c_vp, ctypes.c_int, ctypes.c_int, c_vp, c_i64, c_i64, ctypes.c_int]
+        L.pp_sgetrs_noalloc.argtypes = [c_vp, c_vp, ctypes.c_int, ctypes.c_int, c_vp, c_i64, c_i64]
         _lib = L
     return _lib
 
