@@ -35,12 +35,41 @@ for sub in ("pathpack.jl_amd", "oracle"):
 import pathpack_hip as P  # noqa: E402
 from pathpack_hip import workloads as W  # noqa: E402
 
-# MI355X published FP32 vector rate: 157.3 TFLOP/s = 78.6e12 lane FMAs/s (256 CU x 4 SIMD x 32 lanes x 2.4 GHz), one
-# full-rate VALU instruction per lane and clock.  A MinPlus / MaxPlus Float32 multiply-add costs 1.5 such instructions
-# (v_add_f32, v_add_f32, v_min3_f32 per two; packed FP32 is not used), so the VALU peak is 52.4e12 madds/s.  The VALU
-# probe (--calibrate-valu) runs the compiled two-madd sequence at 63.8e12 lane instructions/s (81 % of 78.6e12).
-VALU_PEAK_MADD = 78.6e12 / 1.5
+# MI355X's published FP32 vector rate is 157.3 TFLOP/s: 78.65e12 lane FMAs/s (256 CU x 4 SIMD x 32 lanes x 2.4 GHz),
+# one full-rate VALU instruction per lane and clock.  The roofline counts one semiring multiply-add as one FMA (two
+# flops), so its peak is the published 157.3 TFLOP/s.  Beside it the instruction-mix bound: a MinPlus / MaxPlus Float32
+# multiply-add costs 1.5 VALU instructions (v_add_f32, v_add_f32, v_min3_f32 per two; packed FP32 is not used), which
+# caps the min-plus kernels at 52.4e12 madds/s.  The VALU probe (--calibrate-valu) measures the compiled sequence.
+FP32_PEAK_TFLOPS = 157.3
+VALU_PEAK_MADD = FP32_PEAK_TFLOPS * 1e12 / 2          # madds/s at one FMA slot per madd
+INSTR_PER_MADD = 1.5
+INSTR_MIX_PEAK_MADD = VALU_PEAK_MADD / INSTR_PER_MADD
 HBM_PEAK = 8.0e12
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def valu_roofline(kernel: str, madds: float, seconds: float, extra=None) -> dict:
+    """The roofline object of a VALU-bound min/max kernel: achieved and peak in TFLOP/s (one madd = one FMA = two
+    flops, against the published FP32 rate), and the same rate against the 1.5-instruction mix."""
+    rate = madds / seconds
+    r = {"bound": "valu", "kernel": kernel, "achieved": round(2 * rate / 1e12, 3), "peak": FP32_PEAK_TFLOPS,
+         "unit": "TFLOP/s", "frac": round(rate / VALU_PEAK_MADD, 4), "traffic": None,
+         "madds_per_s": round(rate / 1e12, 3),
+         "instr_mix": {"instr_per_madd": INSTR_PER_MADD, "peak_Tmadd_s": round(INSTR_MIX_PEAK_MADD / 1e12, 2),
+                       "frac": round(rate / INSTR_MIX_PEAK_MADD, 4)}}
+    if extra:
+        r.update(extra)
+    return r
 PROFILES = os.path.join(ROOT, "profiles")
 
 
@@ -212,26 +241,50 @@ def bench_mstar(args):
         n = g.n
         lstar_madds = n * st["nnzL_alg"]
         t_l = ph["star_Lstar_s"]
-        ach = lstar_madds / t_l
-        result["roofline"] = {"bound": "valu",
-                              "kernel": "X <- X L* sweep: k_blk<..., false> + k_sweep_bwd + k_sub<..., false>, all launches "
-                                        "of one star",
-                              "achieved": round(ach / 1e12, 4), "peak": round(VALU_PEAK_MADD / 1e12, 2),
-                              "unit": "Tmadd/s", "frac": round(ach / VALU_PEAK_MADD, 4),
-                              "traffic": measured_traffic("lstar_sweep"),
-                              "algorithmic_madds": lstar_madds, "seconds": round(t_l, 6),
-                              "output_floor_GBps": round(4.0 * n * n / T / 1e9, 1)}
+        result["roofline"] = valu_roofline(
+            "X <- X L* sweep: k_blk<..., false> + k_sweep_bwd + k_sub<..., false>, all launches of one star",
+            lstar_madds, t_l,
+            {"traffic": measured_traffic("lstar_sweep"), "algorithmic_madds": lstar_madds, "seconds": round(t_l, 6),
+             "output_floor_GBps": round(4.0 * n * n / T / 1e9, 1)})
+    Th = None
+    if args.host_steps > 0:
+        # mstar as the reference returns it: the n x n star in host memory (the analysis, the device factorization
+        # and star, then the relabelled star copied back through pinned chunks), timed in the same run
+        Th = mstar_to_host(g, args.host_steps)
+        result["mstar_to_host"] = {"ms_per_step": round(Th * 1e3, 2), "semiring_Gops": round(madds / Th / 1e9, 2),
+                                   "step": "symbolic + pp_mstar with the star delivered into a host array (n x n, "
+                                           "original labels)"}
     if not args.no_cpu and cfg == 3:
         cb = cpu_baseline(g, sym, budget_s=args.cpu_budget)
         result["cpu_baseline"] = {"value": round(madds / cb["est_mstar_s"] / 1e9, 3), "unit": "semiring Gop/s",
-                                  "cores": cb["threads"], "kind": "port",
+                                  "cores": cb["threads"], "kind": "port", "cpu_model": cpu_model(),
                                   "sample": f"oracle factorization (single thread, full) + star rows "
                                             f"{cb['rows']} of {g.n} in blocks spread over the rows "
                                             f"({cb['star_sample_s']:.1f} s on {cb['threads']} threads), scaled to "
-                                            f"n rows; symbolic excluded",
+                                            f"n rows; symbolic excluded; star left in host memory",
                                   "est_mstar_s": round(cb["est_mstar_s"], 3), "factor_s": round(cb["factor_s"], 3)}
-        result["speedup_vs_cpu"] = round(cb["est_mstar_s"] / T, 1)
+        # like for like: both stars end in host memory
+        if Th is not None:
+            result["speedup_vs_cpu"] = round(cb["est_mstar_s"] / Th, 1)
+        result["speedup_vs_cpu_star_in_hbm"] = round(cb["est_mstar_s"] / T, 1)
     print(json.dumps(result), flush=True)
+
+
+def mstar_to_host(g, steps):
+    """Mean seconds of mstar(MinPlus(), A) with the star delivered into host memory (symbolic included), after one
+    warm-up call; the host array is allocated and touched once beforehand."""
+    C = np.empty((g.n, g.n), g.nzval.dtype, order="F")
+    C.fill(0)
+    ts = []
+    for i in range(steps + 1):
+        t0 = time.perf_counter()
+        P.mstar(P.MinPlus(), g, out=C)
+        t = time.perf_counter() - t0
+        if i:
+            ts.append(t)
+        log(f"mstar to host {i}: {t * 1e3:.1f} ms")
+    del C
+    return float(np.mean(ts))
 
 
 def timed(fn, ctx, steps, warmup):
@@ -310,9 +363,7 @@ def bench_gemm(args):
                     "semiring Gop/s", T, "f32",
                     "dense MinPlus GEMM C <- min(C, A + B), M=N=K=8192, entries U{0..1000} with 10% +Inf "
                     "(SplitMix64 seeds 0x5EED+2, +12, +22), operands in HBM", {"m": N, "n": N, "k": N})
-    r["roofline"] = {"bound": "valu", "kernel": "k_gemm_tiled<MinPlus<float>, 8, 8>", "achieved": round(madds / T / 1e12, 3),
-                     "peak": round(VALU_PEAK_MADD / 1e12, 2), "unit": "Tmadd/s", "frac": round(madds / T / VALU_PEAK_MADD, 4),
-                     "traffic": None}
+    r["roofline"] = valu_roofline("k_gemm_tiled<MinPlus<float>, 8, 8>", madds, T)
     if not args.no_cpu:
         # the oracle's OpenMP GEMM on a 1024 x 1024 block of C with the full K
         mb = 1024
@@ -320,7 +371,7 @@ def bench_gemm(args):
         O.sgemx(O.MINPLUS, np.asfortranarray(A[:mb, :]), np.asfortranarray(B[:, :mb]), np.asfortranarray(C[:mb, :mb]))
         tc = time.perf_counter() - t0
         r["cpu_baseline"] = {"value": round(float(mb) * mb * N / tc / 1e9, 3), "unit": "semiring Gop/s",
-                             "cores": O.num_threads(), "kind": "port",
+                             "cores": O.num_threads(), "kind": "port", "cpu_model": cpu_model(),
                              "sample": f"oracle sgemx on a {mb}x{mb} block of C with K={N} ({tc:.1f} s)"}
     print(json.dumps(r), flush=True)
 
@@ -354,9 +405,8 @@ def bench_getrf(args):
                     T, "f32", "16384 independent 64x64 MinPlus fronts, entries U{0..1000} with 10% +Inf, diagonal 0 "
                     "(SplitMix64 seed 0x5EED+32); A <- L+U, TL <- L*, TU <- U*; step includes a 268 MB device copy "
                     "restoring A", {"nb": nb, "batch": batch, "madds_per_front": per})
-    r["roofline"] = {"bound": "valu", "kernel": "k_getrf_star<MinPlus<float>>", "achieved": round(madds / T / 1e12, 4),
-                     "peak": round(VALU_PEAK_MADD / 1e12, 2), "unit": "Tmadd/s", "frac": round(madds / T / VALU_PEAK_MADD, 4),
-                     "traffic": None, "hbm_floor_ms": round(4.0 * A.size * 4 / HBM_PEAK * 1e3, 3)}
+    r["roofline"] = valu_roofline("k_getrf_star<MinPlus<float>>", madds, T,
+                                  {"hbm_floor_ms": round(4.0 * A.size * 4 / HBM_PEAK * 1e3, 3)})
     if not args.no_cpu:
         sb = 512
         t0 = time.perf_counter()
@@ -364,7 +414,7 @@ def bench_getrf(args):
         O.getrf_star_batched(O.MINPLUS, flat.reshape(sb, nb, nb))   # front b at [b] (column-major: [b, j, i])
         tc = time.perf_counter() - t0
         r["cpu_baseline"] = {"value": round(per * sb / tc / 1e9, 3), "unit": "semiring Gop/s",
-                             "cores": O.num_threads(), "kind": "port", "sample": f"oracle on {sb} of the fronts"}
+                             "cores": O.num_threads(), "kind": "port", "cpu_model": cpu_model(), "sample": f"oracle on {sb} of the fronts"}
     print(json.dumps(r), flush=True)
 
 
@@ -452,7 +502,7 @@ def bench_solve(args, cfg):
         (O.lmul if left else O.rmul)(Fo, Bs)
         tc = time.perf_counter() - t0
         r["cpu_baseline"] = {"value": round(st["madds_rhs_alg"] * k / tc / 1e9, 3), "unit": "semiring Gop/s",
-                             "cores": O.num_threads(), "kind": "port",
+                             "cores": O.num_threads(), "kind": "port", "cpu_model": cpu_model(),
                              "sample": f"oracle {name} on {k} of the {nrhs} right-hand sides"}
     print(json.dumps(r), flush=True)
 
@@ -471,6 +521,8 @@ def main():
     ap.add_argument("--ordering", default="nd", choices=["nd", "amd"],
                     help="fill-reducing order of the analysis: nested dissection (default) or approximate minimum degree")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--host-steps", type=int, default=2,
+                    help="configurations 1 and 3: timed mstar calls with the star delivered to host memory (0: skip)")
     ap.add_argument("--no-timing", dest="timing", action="store_false")
     ap.add_argument("--calibrate-valu", action="store_true",
                     help="only run the VALU probe (pp_calibrate_valu): v_add_f32 and MinPlus multiply-add rates")
