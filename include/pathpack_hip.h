@@ -111,6 +111,14 @@ pp_status pp_sym_export(const pp_sym *sym, int64_t *perm, int64_t *Rptr, int64_t
  * (fundamental-supernode) structure; the same four of the executed (amalgamated) structure; seconds spent in the
  * ordering and in the whole analysis. */
 pp_status pp_sym_stats(const pp_sym *sym, double *stats);
+/* The strongly connected components (sccs and soffd, src/CPU/chordal_ssymbolic.jl:26-57,212-269): nB components in a
+ * topological order, component c holding the permuted vertices [Bptr[c], Bptr[c+1]) (nB + 1 entries); and N, the nN
+ * arcs between components, by column of the permuted labels (CSC: Nptr, n + 1 entries; Nidx, the permuted row of
+ * each arc, ascending per column; Nsrc, its position in the nzval of the matrix given to pp_symbolic).  Every arc of
+ * N goes from a lower to a higher component.  Any output pointer may be NULL (call with the arrays NULL for the
+ * sizes). */
+pp_status pp_sym_components(const pp_sym *sym, int64_t *nB, int64_t *Bptr, int64_t *nN, int64_t *Nptr, int64_t *Nidx,
+                            int64_t *Nsrc);
 pp_status pp_sym_destroy(pp_sym *sym);
 
 /* ===== numeric factorization (device) ===== */

@@ -40,6 +40,7 @@ def lib():
         if not os.path.exists(LIB):
             build()
         _lib = ctypes.CDLL(LIB)
+        _lib.ppo_offd.restype = ctypes.c_int64
     return _lib
 
 
@@ -94,10 +95,14 @@ def times(s: int, a, b):
 
 class Sym:
     """A symbolic structure in the oracle's terms (0-based): res(f) = [Rptr[f], Rptr[f+1]), sep(f) =
-    Stgt[Sptr[f]:Sptr[f+1]] (sorted), perm[new] = old."""
+    Stgt[Sptr[f]:Sptr[f+1]] (sorted), perm[new] = old.  Bptr (optional): the strongly connected components in a
+    topological order, component c holding the permuted vertices [Bptr[c], Bptr[c+1]); the fronts are then those of
+    the diagonal blocks, and the arcs between components (N) are applied by the blocked algorithms."""
 
-    def __init__(self, n, Rptr, Sptr, Stgt, perm):
+    def __init__(self, n, Rptr, Sptr, Stgt, perm, Bptr=None):
         self.n = int(n)
+        self.Bptr = None if Bptr is None or len(Bptr) <= 2 else np.ascontiguousarray(Bptr, dtype=np.int64)
+        self.nB = 1 if self.Bptr is None else self.Bptr.size - 1
         self.Rptr = np.ascontiguousarray(Rptr, dtype=np.int64)
         self.Sptr = np.ascontiguousarray(Sptr, dtype=np.int64)
         self.Stgt = np.ascontiguousarray(Stgt, dtype=np.int64)
@@ -114,12 +119,17 @@ class Sym:
 
 
 class Factor:
-    def __init__(self, s, sym: Sym, dtype, LD, UD, LL, UL):
+    def __init__(self, s, sym: Sym, dtype, LD, UD, LL, UL, N=None):
         self.s, self.sym, self.dtype = s, sym, np.dtype(dtype)
         self.LD, self.UD, self.LL, self.UL = LD, UD, LL, UL
+        self.N = N   # (Nptr, Nidx, Nval) of a structure with components, else None
 
     def _fargs(self):
         return (_p(self.LD), _p(self.UD), _p(self.LL), _p(self.UL))
+
+    def _nargs(self):
+        Nptr, Nidx, Nval = self.N
+        return (ctypes.c_int64(self.sym.nB), _p(self.sym.Bptr), _p(Nptr), _p(Nidx), _p(Nval))
 
 
 def _check(rc, what):
@@ -141,12 +151,29 @@ def factor(s: int, sym: Sym, colptr, rowval, nzval, scatter_only: bool = False) 
     rc = fn(ctypes.c_int(s), ctypes.c_int(dtype_code(dt)), *sym.args(), _p(colptr), _p(rowval), _p(nzval),
             _p(LD), _p(UD), _p(LL), _p(UL))
     _check(rc, "factor")
-    return Factor(s, sym, dt, LD, UD, LL, UL)
+    N = None
+    if sym.nB > 1:
+        # soffd (chordal_ssymbolic.jl:212-269): the arcs between components, by permuted column
+        Nptr = np.empty(sym.n + 1, np.int64)
+        cap = max(1, int(colptr[-1]))
+        Nidx = np.empty(cap, np.int64)
+        Nval = np.empty(cap, dt)
+        cnt = lib().ppo_offd(ctypes.c_int(s), ctypes.c_int(dtype_code(dt)), *sym.args(), ctypes.c_int64(sym.nB),
+                             _p(sym.Bptr), _p(colptr), _p(rowval), _p(nzval), _p(Nptr), _p(Nidx), _p(Nval))
+        if cnt < 0:
+            raise RuntimeError(f"oracle offd failed with code {cnt}")
+        N = (Nptr, Nidx[:max(1, cnt)].copy(), Nval[:max(1, cnt)].copy())
+    return Factor(s, sym, dt, LD, UD, LL, UL, N)
 
 
 def rmul(F: Factor, B: np.ndarray) -> np.ndarray:
     """B (nrhs x n) <- B A*."""
     B = np.asfortranarray(B, dtype=F.dtype).copy(order="F")
+    if F.N is not None:
+        rc = lib().ppo_rmul_scc(ctypes.c_int(F.s), ctypes.c_int(dtype_code(F.dtype)), *F.sym.args(), *F._fargs(),
+                                *F._nargs(), _p(B), ctypes.c_int64(B.shape[0]))
+        _check(rc, "rmul")
+        return B
     rc = lib().ppo_rmul(ctypes.c_int(F.s), ctypes.c_int(dtype_code(F.dtype)), *F.sym.args(), *F._fargs(), _p(B),
                         ctypes.c_int64(B.shape[0]))
     _check(rc, "rmul")
@@ -158,6 +185,11 @@ def lmul(F: Factor, B: np.ndarray) -> np.ndarray:
     B = np.asfortranarray(B, dtype=F.dtype).copy(order="F")
     if B.ndim == 1:
         B = B.reshape(-1, 1, order="F")
+    if F.N is not None:
+        rc = lib().ppo_lmul_scc(ctypes.c_int(F.s), ctypes.c_int(dtype_code(F.dtype)), *F.sym.args(), *F._fargs(),
+                                *F._nargs(), _p(B), ctypes.c_int64(B.shape[1]))
+        _check(rc, "lmul")
+        return B
     rc = lib().ppo_lmul(ctypes.c_int(F.s), ctypes.c_int(dtype_code(F.dtype)), *F.sym.args(), *F._fargs(), _p(B),
                         ctypes.c_int64(B.shape[1]))
     _check(rc, "lmul")
@@ -185,6 +217,13 @@ def star(F: Factor, rows: tuple[int, int] | None = None, relabel: bool = True, n
     n = F.sym.n
     r0, r1 = rows if rows is not None else (0, n)
     C = np.empty((n, n), dtype=F.dtype, order="F")
+    if F.N is not None:
+        if rows is not None or not relabel:
+            raise ValueError("the star of a structure with components is computed whole and relabelled")
+        rc = lib().ppo_star_scc(ctypes.c_int(F.s), ctypes.c_int(dtype_code(F.dtype)), *F.sym.args(), *F._fargs(),
+                                *F._nargs(), _p(C), ctypes.c_int(nthreads))
+        _check(rc, "star")
+        return C
     rc = lib().ppo_star(ctypes.c_int(F.s), ctypes.c_int(dtype_code(F.dtype)), *F.sym.args(), *F._fargs(), _p(C),
                         ctypes.c_int64(r0), ctypes.c_int64(r1), ctypes.c_int(1 if relabel else 0),
                         ctypes.c_int(nthreads))

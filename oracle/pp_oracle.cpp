@@ -15,6 +15,10 @@
 //                             src/CPU/chordal/strsx.jl (strsx_fwd*/strsx_bwd*)
 //   full star                 src/CPU/chordal/sgetri.jl:13-31, src/CPU/chordal/strtri.jl:171-319,
 //                             src/CPU/chordal/strsx.jl:729-867, src/CPU/utils.jl:261-505 (permuterowscols!)
+//   components                src/CPU/chordal_ssymbolic.jl:212-269 (soffd: the arcs between components, N),
+//                             src/CPU/blocked/sgetri.jl:3-162 (sgetri_offd!: the off-diagonal blocks of the star),
+//                             src/CPU/blocked/sgetrs.jl:80-122 (sgetrs_mt!: the solves over the components),
+//                             src/CPU/sparse/sgemx.jl (sgemx_sparse!: products with N)
 //   dense semiring GEMM       src/CPU/dense/sgemx.jl:606-635 (generic loop)
 //   batched getrf + star      ext/PATHPACKCUDAExt/batched/sgetrf.jl:11-120 (front_diag_kernel!)
 //
@@ -535,6 +539,213 @@ static void star(const Sym &Y, const T *LD, const T *UD, const T *LL, const T *U
     }
 }
 
+// ===== strongly connected components (src/CPU/blocked/*.jl) =====
+//
+// The structure's vertices are grouped by component in a topological order: component c holds the permuted vertices
+// [Bptr[c], Bptr[c+1]) and the fronts [Fptr[c], Fptr[c+1]); the factor is that of the diagonal blocks.  N holds the
+// arcs between components in the permuted labels, by column j (Nptr, Nidx = rows i < Bptr[comp(j)], ascending;
+// Nval = A[i, j]).
+
+// soffd (chordal_ssymbolic.jl:212-269): the entries of column j of the permuted A whose row lies in an earlier
+// component.  Returns their number; with Nidx / Nval null only Nptr is filled.
+template <class T>
+static i64 offd(const Sym &Y, const i64 *Bptr, i64 nB, const i64 *colptr, const i64 *rowval, const T *nzval, i64 *Nptr,
+                i64 *Nidx, T *Nval) {
+    const i64 n = Y.n;
+    std::vector<i64> start(n);
+    for (i64 c = 0; c < nB; c++)
+        for (i64 j = Bptr[c]; j < Bptr[c + 1]; j++) start[j] = Bptr[c];
+    Nptr[0] = 0;
+    std::vector<std::pair<i64, T>> col;
+    for (i64 j = 0; j < n; j++) {
+        const i64 oc = Y.perm[j];
+        col.clear();
+        for (i64 p = colptr[oc]; p < colptr[oc + 1]; p++) {
+            const i64 i = Y.invp[rowval[p]];
+            if (i < start[j]) col.push_back({i, nzval ? nzval[p] : T(0)});
+        }
+        std::sort(col.begin(), col.end(), [](const std::pair<i64, T> &a, const std::pair<i64, T> &b) { return a.first < b.first; });
+        if (Nidx)
+            for (size_t k = 0; k < col.size(); k++) {
+                Nidx[Nptr[j] + k] = col[k].first;
+                Nval[Nptr[j] + k] = col[k].second;
+            }
+        Nptr[j + 1] = Nptr[j] + (i64)col.size();
+    }
+    return Nptr[n];
+}
+
+// The fronts of component c, from the vertex ranges.
+static void comp_fronts(const Sym &Y, const i64 *Bptr, i64 nB, std::vector<i64> &Fptr) {
+    Fptr.assign(nB + 1, Y.nf);
+    for (i64 c = nB - 1; c >= 0; c--) Fptr[c] = Bptr[c] < Bptr[c + 1] ? Y.idx[Bptr[c]] : Fptr[c + 1];
+}
+
+// C[:, cols] with the rows of fronts [f0, f1) <- A_cc* C (lmul! over one component's fronts: L forward, then U
+// backward; chordal/sgetrs.jl:29-51 restricted to fronts fstrt:fstop, as blocked/sgetri.jl:109 calls it); C is
+// n x m column-major (ldc).
+template <class S, class T>
+static void lmul_fronts(const Sym &Y, const T *LD, const T *UD, const T *LL, const T *UL, T *C, i64 ldc, i64 m, i64 f0,
+                        i64 f1) {
+    for (i64 col = 0; col < m; col++) {
+        T *x = C + col * ldc;
+        for (i64 f = f0; f < f1; f++) {
+            const i64 Rp = Y.Rptr[f], nn = Y.Rptr[f + 1] - Rp, s0 = Y.Sptr[f], na = Y.Sptr[f + 1] - s0;
+            const T *D11 = LD + Y.Dptr[f], *L21 = LL + Y.Lptr[f];
+            trsm_left_lower_unit<S>(D11, nn, x + Rp, ldc, nn, 1);
+            for (i64 k = 0; k < na; k++) {
+                T acc = x[Y.Stgt[s0 + k]];
+                for (i64 j = 0; j < nn; j++) acc = S::muladd(L21[k + j * na], x[Rp + j], acc);
+                x[Y.Stgt[s0 + k]] = acc;
+            }
+        }
+        for (i64 f = f1 - 1; f >= f0; f--) {
+            const i64 Rp = Y.Rptr[f], nn = Y.Rptr[f + 1] - Rp, s0 = Y.Sptr[f], na = Y.Sptr[f + 1] - s0;
+            const T *D11 = UD + Y.Dptr[f], *U12 = UL + Y.Lptr[f];
+            for (i64 i = 0; i < nn; i++) {
+                T acc = x[Rp + i];
+                for (i64 k = 0; k < na; k++) acc = S::muladd(U12[i + k * nn], x[Y.Stgt[s0 + k]], acc);
+                x[Rp + i] = acc;
+            }
+            trsm_left_upper_nonunit<S>(D11, nn, x + Rp, ldc, nn, 1);
+        }
+    }
+}
+
+// C (nrhs x n, ldc = nrhs, permuted columns) <- C A_cc* over the fronts [f0, f1) (rmul!: U forward, then L backward)
+template <class S, class T>
+static void rmul_fronts(const Sym &Y, const T *LD, const T *UD, const T *LL, const T *UL, T *C, i64 nrhs, i64 f0, i64 f1) {
+    for (i64 f = f0; f < f1; f++) {
+        const i64 Rp = Y.Rptr[f], nn = Y.Rptr[f + 1] - Rp, s0 = Y.Sptr[f], na = Y.Sptr[f + 1] - s0;
+        const T *D11 = UD + Y.Dptr[f], *U12 = UL + Y.Lptr[f];
+        trsm_right_upper_nonunit<S>(D11, nn, &C[Rp * nrhs], nrhs, nrhs, nn);
+        for (i64 k = 0; k < na; k++) {
+            T *ck = &C[Y.Stgt[s0 + k] * nrhs];
+            for (i64 i = 0; i < nn; i++) {
+                T u = U12[i + k * nn];
+                const T *ci = &C[(Rp + i) * nrhs];
+                for (i64 r = 0; r < nrhs; r++) ck[r] = S::muladd(ci[r], u, ck[r]);
+            }
+        }
+    }
+    for (i64 f = f1 - 1; f >= f0; f--) {
+        const i64 Rp = Y.Rptr[f], nn = Y.Rptr[f + 1] - Rp, s0 = Y.Sptr[f], na = Y.Sptr[f + 1] - s0;
+        const T *D11 = LD + Y.Dptr[f], *L21 = LL + Y.Lptr[f];
+        for (i64 j = 0; j < nn; j++) {
+            T *cj = &C[(Rp + j) * nrhs];
+            for (i64 k = 0; k < na; k++) {
+                T l = L21[k + j * na];
+                const T *ck = &C[Y.Stgt[s0 + k] * nrhs];
+                for (i64 r = 0; r < nrhs; r++) cj[r] = S::muladd(ck[r], l, cj[r]);
+            }
+        }
+        trsm_right_lower_unit<S>(D11, nn, &C[Rp * nrhs], nrhs, nrhs, nn);
+    }
+}
+
+// rmul! over the components (blocked/sgetrs.jl:80-122 with side :R, trans :N: components in increasing order, each
+// first gathering its arcs from earlier components, X[:, j] <- X[:, j] (+) sum_i X[:, i] (x) N[i, j]
+// (sgemx_sparse!), then solving with its own fronts).  B: nrhs x n.
+template <class S, class T>
+static void rmul_scc(const Sym &Y, const T *LD, const T *UD, const T *LL, const T *UL, const i64 *Bptr, i64 nB,
+                     const i64 *Nptr, const i64 *Nidx, const T *Nval, T *B, i64 nrhs) {
+    const i64 n = Y.n;
+    std::vector<i64> Fptr;
+    comp_fronts(Y, Bptr, nB, Fptr);
+    std::vector<T> C(n * nrhs);
+    for (i64 j = 0; j < n; j++) std::memcpy(&C[Y.invp[j] * nrhs], &B[j * nrhs], nrhs * sizeof(T));
+    for (i64 c = 0; c < nB; c++) {
+        for (i64 j = Bptr[c]; j < Bptr[c + 1]; j++) {
+            T *cj = &C[j * nrhs];
+            for (i64 q = Nptr[j]; q < Nptr[j + 1]; q++) {
+                const T *ci = &C[Nidx[q] * nrhs];
+                for (i64 r = 0; r < nrhs; r++) cj[r] = S::muladd(ci[r], Nval[q], cj[r]);
+            }
+        }
+        rmul_fronts<S>(Y, LD, UD, LL, UL, C.data(), nrhs, Fptr[c], Fptr[c + 1]);
+    }
+    for (i64 j = 0; j < n; j++) std::memcpy(&B[Y.perm[j] * nrhs], &C[j * nrhs], nrhs * sizeof(T));
+}
+
+// lmul! over the components (side :L, trans :N: components in decreasing order, each solving with its own fronts,
+// then pushing its rows to the earlier components, X[i, :] <- X[i, :] (+) N[i, j] (x) X[j, :]).  B: n x nrhs.
+template <class S, class T>
+static void lmul_scc(const Sym &Y, const T *LD, const T *UD, const T *LL, const T *UL, const i64 *Bptr, i64 nB,
+                     const i64 *Nptr, const i64 *Nidx, const T *Nval, T *B, i64 nrhs) {
+    const i64 n = Y.n;
+    std::vector<i64> Fptr;
+    comp_fronts(Y, Bptr, nB, Fptr);
+    std::vector<T> C(n * nrhs);
+    for (i64 col = 0; col < nrhs; col++)
+        for (i64 i = 0; i < n; i++) C[Y.invp[i] + col * n] = B[i + col * n];
+    for (i64 c = nB - 1; c >= 0; c--) {
+        lmul_fronts<S>(Y, LD, UD, LL, UL, C.data(), n, nrhs, Fptr[c], Fptr[c + 1]);
+        for (i64 col = 0; col < nrhs; col++) {
+            T *x = &C[col * n];
+            for (i64 j = Bptr[c]; j < Bptr[c + 1]; j++)
+                for (i64 q = Nptr[j]; q < Nptr[j + 1]; q++) x[Nidx[q]] = S::muladd(Nval[q], x[j], x[Nidx[q]]);
+        }
+    }
+    for (i64 col = 0; col < nrhs; col++)
+        for (i64 i = 0; i < n; i++) B[Y.perm[i] + col * n] = C[i + col * n];
+}
+
+// The star over the components (blocked/sgetri.jl:3-162): the diagonal blocks A_cc* by the chordal star (star(),
+// rows of other components stay zero), then for each component d whose columns N reaches, the components with a
+// path into d (sgetri_reach!) in an order that visits every component after all those it has arcs into (decreasing
+// number: every arc goes to a higher one): C[rows of c, cols of d] <- A_cc* C[rows of c, cols of d] (c != d), then
+// C[rows of b, cols of d] <- (+) N[b, c] (x) C[rows of c, cols of d] for the arcs b -> c (sgemx_sparse!).
+template <class S, class T>
+static void star_scc(const Sym &Y, const T *LD, const T *UD, const T *LL, const T *UL, const i64 *Bptr, i64 nB,
+                     const i64 *Nptr, const i64 *Nidx, const T *Nval, T *C, int nthreads) {
+    const i64 n = Y.n;
+    std::vector<T> X((size_t)n * n);
+    star<S>(Y, LD, UD, LL, UL, X.data(), 0, n, 0, nthreads);
+    std::vector<i64> Fptr, comp(n);
+    comp_fronts(Y, Bptr, nB, Fptr);
+    for (i64 c = 0; c < nB; c++)
+        for (i64 j = Bptr[c]; j < Bptr[c + 1]; j++) comp[j] = c;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+    {
+        std::vector<char> anc(nB);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (i64 d = 0; d < nB; d++) {
+            const i64 j0 = Bptr[d], j1 = Bptr[d + 1];
+            if (Nptr[j0] == Nptr[j1]) continue;
+            // the components with a path into d (sgetri_reach!)
+            std::fill(anc.begin(), anc.end(), 0);
+            anc[d] = 1;
+            for (i64 c = d; c >= 0; c--) {
+                if (!anc[c]) continue;
+                for (i64 j = Bptr[c]; j < Bptr[c + 1]; j++)
+                    for (i64 q = Nptr[j]; q < Nptr[j + 1]; q++) anc[comp[Nidx[q]]] = 1;
+            }
+            T *Cd = X.data() + j0 * n;
+            const i64 m = j1 - j0;
+            for (i64 c = d; c >= 0; c--) {
+                if (!anc[c]) continue;
+                if (c != d) lmul_fronts<S>(Y, LD, UD, LL, UL, Cd, n, m, Fptr[c], Fptr[c + 1]);
+                for (i64 j = Bptr[c]; j < Bptr[c + 1]; j++)
+                    for (i64 q = Nptr[j]; q < Nptr[j + 1]; q++)
+                        for (i64 col = 0; col < m; col++) {
+                            T *x = Cd + col * n;
+                            x[Nidx[q]] = S::muladd(Nval[q], x[j], x[Nidx[q]]);
+                        }
+            }
+        }
+    }
+    for (i64 c = 0; c < n; c++) {
+        T *dst = C + Y.perm[c] * n;
+        const T *src = X.data() + c * n;
+        for (i64 r = 0; r < n; r++) dst[Y.perm[r]] = src[r];
+    }
+}
+
 // ===== batched getrf + star of dense fronts (ext/PATHPACKCUDAExt/batched/sgetrf.jl:11-120) =====
 //
 // A (nb x nb, column-major, batch of them back to back) <- L + U;  TU <- U*;  TL <- L* (unit lower).
@@ -655,6 +866,51 @@ int ppo_star(int sr, int dt, i64 n, i64 nf, const i64 *Rptr, const i64 *Sptr, co
     if (e) return e;
     if (row0 < 0 || row1 > n || row0 > row1) return -5;
     PPO_DISPATCH(sr, dt, (star<S, T>(Y, (const T *)LD, (const T *)UD, (const T *)LL, (const T *)UL, (T *)C, row0, row1, relabel, nthreads)));
+}
+
+// N of a structure with components (soffd): Nptr (n + 1) always; Nidx / Nval (capacity nnz) when not null.
+// Returns the number of arcs, or a negative error.
+i64 ppo_offd(int sr, int dt, i64 n, i64 nf, const i64 *Rptr, const i64 *Sptr, const i64 *Stgt, const i64 *perm, i64 nB,
+             const i64 *Bptr, const i64 *colptr, const i64 *rowval, const void *nzval, i64 *Nptr, i64 *Nidx, void *Nval) {
+    Sym Y;
+    int e = build_sym(Y, n, nf, Rptr, Sptr, Stgt, perm);
+    if (e) return e;
+    i64 cnt = -100;
+    if (dt == D_F32) cnt = offd<float>(Y, Bptr, nB, colptr, rowval, (const float *)nzval, Nptr, Nidx, (float *)Nval);
+    else if (dt == D_F64) cnt = offd<double>(Y, Bptr, nB, colptr, rowval, (const double *)nzval, Nptr, Nidx, (double *)Nval);
+    else if (dt == D_I32) cnt = offd<int32_t>(Y, Bptr, nB, colptr, rowval, (const int32_t *)nzval, Nptr, Nidx, (int32_t *)Nval);
+    (void)sr;
+    return cnt;
+}
+
+int ppo_rmul_scc(int sr, int dt, i64 n, i64 nf, const i64 *Rptr, const i64 *Sptr, const i64 *Stgt, const i64 *perm,
+                 const void *LD, const void *UD, const void *LL, const void *UL, i64 nB, const i64 *Bptr, const i64 *Nptr,
+                 const i64 *Nidx, const void *Nval, void *B, i64 nrhs) {
+    Sym Y;
+    int e = build_sym(Y, n, nf, Rptr, Sptr, Stgt, perm);
+    if (e) return e;
+    PPO_DISPATCH(sr, dt, (rmul_scc<S, T>(Y, (const T *)LD, (const T *)UD, (const T *)LL, (const T *)UL, Bptr, nB, Nptr,
+                                         Nidx, (const T *)Nval, (T *)B, nrhs)));
+}
+
+int ppo_lmul_scc(int sr, int dt, i64 n, i64 nf, const i64 *Rptr, const i64 *Sptr, const i64 *Stgt, const i64 *perm,
+                 const void *LD, const void *UD, const void *LL, const void *UL, i64 nB, const i64 *Bptr, const i64 *Nptr,
+                 const i64 *Nidx, const void *Nval, void *B, i64 nrhs) {
+    Sym Y;
+    int e = build_sym(Y, n, nf, Rptr, Sptr, Stgt, perm);
+    if (e) return e;
+    PPO_DISPATCH(sr, dt, (lmul_scc<S, T>(Y, (const T *)LD, (const T *)UD, (const T *)LL, (const T *)UL, Bptr, nB, Nptr,
+                                         Nidx, (const T *)Nval, (T *)B, nrhs)));
+}
+
+int ppo_star_scc(int sr, int dt, i64 n, i64 nf, const i64 *Rptr, const i64 *Sptr, const i64 *Stgt, const i64 *perm,
+                 const void *LD, const void *UD, const void *LL, const void *UL, i64 nB, const i64 *Bptr, const i64 *Nptr,
+                 const i64 *Nidx, const void *Nval, void *C, int nthreads) {
+    Sym Y;
+    int e = build_sym(Y, n, nf, Rptr, Sptr, Stgt, perm);
+    if (e) return e;
+    PPO_DISPATCH(sr, dt, (star_scc<S, T>(Y, (const T *)LD, (const T *)UD, (const T *)LL, (const T *)UL, Bptr, nB, Nptr,
+                                         Nidx, (const T *)Nval, (T *)C, nthreads)));
 }
 
 int ppo_sgemx(int sr, int dt, i64 m, i64 n, i64 k, const void *A, i64 lda, const void *B, i64 ldb, void *C, i64 ldc, int nthreads) {

@@ -282,6 +282,19 @@ pp_status pp_sym_stats(const pp_sym *sym, double *st) {
     return PP_OK;
 }
 
+pp_status pp_sym_components(const pp_sym *sym, int64_t *nB, int64_t *Bptr, int64_t *nN, int64_t *Nptr, int64_t *Nidx,
+                            int64_t *Nsrc) {
+    if (!sym) return fail(nullptr, PP_EINVAL, "pp_sym_components: null symbolic");
+    const pp::Symbolic &S = sym->S;
+    if (nB) *nB = S.nB;
+    if (nN) *nN = S.nN;
+    if (Bptr) std::copy(S.Bptr.begin(), S.Bptr.end(), Bptr);
+    if (Nptr) std::copy(S.Nptr.begin(), S.Nptr.end(), Nptr);
+    if (Nidx) std::copy(S.Nidx.begin(), S.Nidx.end(), Nidx);
+    if (Nsrc) std::copy(S.Nsrc.begin(), S.Nsrc.end(), Nsrc);
+    return PP_OK;
+}
+
 pp_status pp_sym_destroy(pp_sym *sym) {
     delete sym;
     return PP_OK;
@@ -344,7 +357,11 @@ static size_t factor_bytes(const pp::Symbolic &S, const pp::FactorPlan &P, size_
                          sizeof(i64) * (5 * (size_t)z.units + 2 * (size_t)S.n) + 40 * 256;
     const size_t packs = es * (2 * (size_t)z.npack + (size_t)z.ndpack + (size_t)z.nbpack + (size_t)z.nhpack +
                                (size_t)z.nb * 2 * pp::BLK_W * pp::BLK_W);
-    return plan1 + factor + std::max(scratch, plan2 + packs + extra);
+    // N (components coupled by arcs): values and sources by column and by row, pointers, indices, gather lists
+    const size_t ncoup = z.nN ? (2 * es + 2 * sizeof(i64) + 2 * sizeof(int32_t) + 3 * sizeof(int32_t)) * (size_t)z.nN +
+                                    2 * sizeof(i64) * ((size_t)S.n + 1) + 2 * sizeof(int32_t) * (size_t)z.units + 8 * 256
+                              : 0;
+    return plan1 + factor + ncoup + std::max(scratch, plan2 + packs + extra);
 }
 
 // finish: wait for the factorization before returning (pp_factor); pp_mstar queues the star behind it instead, and
@@ -438,8 +455,14 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     u1.add(S.Dptr, &d.Dptr);
     u1.add(S.Lptr, &d.Lptr);
     u1.add(S.Rptr, &d.Rptr);
+    const bool coupled = S.nB > 1 && S.nN > 0;
+    if (coupled) {
+        u1.add(S.Nsrc, &d.Nsrc);
+        u1.add(S.NTsrc, &d.NTsrc);
+    }
     const size_t plan1 = u1.total;
     const size_t oLD = u1.place(nD * es), oLL = u1.place(nL * es), oUL = u1.place(nL * es);
+    const size_t oNv = coupled ? u1.place((size_t)S.nN * es) : 0, oNTv = coupled ? u1.place((size_t)S.nN * es) : 0;
     void *block1 = nullptr;
     std::string e = u1.run(ctx, st, ctx->staging, ctx->staging_bytes, plan1, &block1);
     if (!e.empty()) return failf(PP_ENOMEM, "pp_factor: " + e);
@@ -447,6 +470,10 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     fac->LD = (char *)block1 + oLD;
     fac->LL = (char *)block1 + oLL;
     fac->UL = (char *)block1 + oUL;
+    if (coupled) {
+        fac->Nval = (char *)block1 + oNv;
+        fac->NTval = (char *)block1 + oNTv;
+    }
     const void *dnz = nzval;
     void *tmpnz = nullptr;
     if (!on_device && S.nnz > 0) {
@@ -497,6 +524,17 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     u2.add(S.perm, &d.perm);
     u2.add(S.invp, &d.invp);
     u2.add(invp32, &d.invp32);
+    if (W.coupled) {
+        u2.add(S.Nptr, &d.Nptr);
+        u2.add(S.Nidx, &d.Nidx);
+        u2.add(S.NTptr, &d.NTptr);
+        u2.add(S.NTidx, &d.NTidx);
+        u2.add(W.ccols, &d.ccols);
+        u2.add(W.ccol_lo, &d.ccol_lo);
+        u2.add(W.ccol_hi, &d.ccol_hi);
+        u2.add(W.rowC_lo, &d.p_rowC_lo);
+        u2.add(W.rowC_hi, &d.p_rowC_hi);
+    }
     const size_t plan2 = u2.total;
     const size_t oD = u2.place(W.ndpack * es), oU = u2.place(W.npack * es), oL = u2.place(W.npack * es);
     const size_t oB = u2.place(W.nbpack * es), oH = u2.place(W.nhpack * es);

@@ -133,9 +133,29 @@ struct SweepPlan {
         bool uniB;                   // every panel of the list has the same backward rows [rowB_lo, rowB_hi)
         int32_t rowB_lo, rowB_hi;
         i64 pT[2];                   // block lists: per-block prefix of GEMM tiles for 64 and 128 rows per tile
+        i64 pCu, pC64;               // forward units (tiles x chunks) and backward tiles over the rows [rowC_lo, rowC_hi)
     };
     std::vector<List> fwd, bwd;      // in execution order (panels; the solves)
     std::vector<List> sfwd, sbwd;    // the star's (panels of small fronts and blocks)
+    // Strongly connected components coupled by N (several components and arcs between them): schedules over the
+    // component DAG, one entry per level.  "up" (Y <- Y A*: rmul!, the rows and the off-diagonal blocks of the star):
+    // the components by increasing lev_up; a level first gathers, into each of its columns j, the arcs i -> j from
+    // earlier components (Y[:, j] (+)= Y[:, i] (x) N[i, j], N by column), then runs its panels (U forward, L backward).
+    // "dn" (Y <- Y (A*)^T: lmul!, the columns of the star): by increasing lev_dn, gathering into row i the arcs i -> j
+    // to later components (N by row), then the transposed sweeps.  The solves run every list on all their rows; the
+    // star's second pass runs the "up" lists on each panel's rows [rowC_lo, rowC_hi) = [anc_lo, first row) of its
+    // component, i.e. the rows of the earlier components (the diagonal blocks come from the first pass).
+    bool coupled = false;
+    struct CLevel {
+        i64 cols_off, cols_cnt;      // the level's columns with arcs to gather (in ccols)
+        i64 fwd_off, fwd_cnt;        // its forward panel lists (in cfwd)
+        i64 bwd_off, bwd_cnt;        // its backward panel lists (in cbwd)
+    };
+    std::vector<CLevel> cup, cdn;
+    std::vector<List> cfwd, cbwd;
+    std::vector<int32_t> ccols;      // gather columns of all levels
+    std::vector<int32_t> ccol_lo, ccol_hi;   // per gather column of an "up" level: the rows of the star's second pass
+    std::vector<int32_t> rowC_lo, rowC_hi;   // per unit
     std::vector<int32_t> plist;
     std::vector<int32_t> tiles;      // the prefix sums of all lists
     i64 max_e = 0;
@@ -151,6 +171,7 @@ struct SweepSizes {
     i64 eidx = 0;                    // gather-list entries (with the padding)
     i64 npack = 0, ndpack = 0, nbpack = 0, nhpack = 0;
     i64 prep = 0;                    // block-pack GEMM tiles
+    i64 nN = 0;                      // arcs between strongly connected components
 };
 SweepSizes sweep_sizes(const Symbolic &S);
 
@@ -187,6 +208,10 @@ struct DevPlan {
     i64 *b_boff = nullptr, *b_hoff = nullptr;
     int32_t *b_kp = nullptr, *b_ep = nullptr, *b_bn = nullptr, *prep = nullptr, *sunits = nullptr;
     int32_t *sub_ptr = nullptr, *sub_pan = nullptr, *sub_rows = nullptr, *sub_preF = nullptr, *sub_preB = nullptr;
+    // components coupled by N: N by column and by row, the value sources, the gather columns, per-unit rows
+    i64 *Nptr = nullptr, *NTptr = nullptr, *Nsrc = nullptr, *NTsrc = nullptr;
+    int32_t *Nidx = nullptr, *NTidx = nullptr, *ccols = nullptr, *ccol_lo = nullptr, *ccol_hi = nullptr;
+    int32_t *p_rowC_lo = nullptr, *p_rowC_hi = nullptr;
     // permutation
     i64 *perm = nullptr, *invp = nullptr;
     int32_t *invp32 = nullptr;
@@ -243,6 +268,7 @@ struct pp_fac {
     void *LD = nullptr, *LL = nullptr, *UL = nullptr;     // reference layout
     void *Dpack = nullptr, *Upack = nullptr, *Lpack = nullptr;
     void *Bpack = nullptr, *Hpack = nullptr;             // star blocks
+    void *Nval = nullptr, *NTval = nullptr;              // N's values by column and by row (components coupled)
     ~pp_fac();
 };
 

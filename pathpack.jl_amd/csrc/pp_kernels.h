@@ -49,9 +49,19 @@ template <class T> __global__ void k_fill(T *__restrict__ p, i64 n, T v) {
     for (i64 i = blockIdx.x * (i64)NT + threadIdx.x; i < n; i += (i64)gridDim.x * NT) p[i] = v;
 }
 
+// F[pos[i]] = val[i] for the entries with a position (pos < 0: an arc between components, which N holds)
 template <class T>
 __global__ void k_scatter_entries(T *__restrict__ F, const i64 *__restrict__ pos, const T *__restrict__ val, i64 nnz) {
-    for (i64 i = blockIdx.x * (i64)NT + threadIdx.x; i < nnz; i += (i64)gridDim.x * NT) F[pos[i]] = val[i];
+    for (i64 i = blockIdx.x * (i64)NT + threadIdx.x; i < nnz; i += (i64)gridDim.x * NT) {
+        const i64 q = pos[i];
+        if (q >= 0) F[q] = val[i];
+    }
+}
+
+// dst[q] = src[idx[q]]: the values of N (by column and by row) from A's values
+template <class T>
+__global__ void k_gather(T *__restrict__ dst, const T *__restrict__ src, const i64 *__restrict__ idx, i64 m) {
+    for (i64 q = blockIdx.x * (i64)NT + threadIdx.x; q < m; q += (i64)gridDim.x * NT) dst[q] = src[idx[q]];
 }
 
 // X <- I in the semiring (the start of X <- U*; row i is the unit vector of source rsrc[i], or of i), on the entries
@@ -1863,6 +1873,37 @@ __global__ __launch_bounds__(NT) void k_transpose_perm(T *__restrict__ B, i64 ld
     }
 }
 
+// ===== arcs between strongly connected components (blocked/sgetrs.jl, sparse/sgemx.jl) =====
+//
+// Y[r, t] <- Y[r, t] (+) sum_q Y[r, idx[q]] (x) val[q], q in [ptr[t], ptr[t + 1]), for the gather columns t =
+// cols[blockIdx.x] of one level of the component DAG: with N by column (idx = rows i of the arcs i -> t, from earlier
+// components) or by row (idx = columns j of the arcs t -> j, to later components).  Rows [rlo[b], rhi[b]) (the star's
+// second pass), or [0, nrows).  The sources lie in components of earlier levels, so no block writes what another
+// reads; every row is one lane, the arc lists are wave-uniform (scalar loads), the columns coalesced.
+template <class S>
+__global__ __launch_bounds__(NT) void k_spmm_pull(typename S::value_type *__restrict__ Y, i64 ld,
+                                                  const int32_t *__restrict__ cols, const int32_t *__restrict__ rlo,
+                                                  const int32_t *__restrict__ rhi, i64 nrows, const i64 *__restrict__ ptr,
+                                                  const int32_t *__restrict__ idx,
+                                                  const typename S::value_type *__restrict__ val) {
+    typedef typename S::value_type T;
+    const int b = blockIdx.x;
+    const i64 t = cols[b];
+    const i64 lo = rlo ? rlo[b] : 0, hi = rhi ? rhi[b] : nrows;
+    const i64 q0 = ptr[t], q1 = ptr[t + 1];
+    for (i64 r = lo + (i64)blockIdx.y * NT + threadIdx.x; r < hi; r += (i64)gridDim.y * NT) {
+        T acc = Y[r + t * ld];
+        for (i64 q = q0; q < q1; q++) acc = S::muladd(Y[r + (i64)idx[q] * ld], val[q], acc);
+        Y[r + t * ld] = acc;
+    }
+}
+
+// Y[k, js[k]] = one for the m rows of the source-row buffer (its other entries are zero)
+template <class S>
+__global__ void k_set_units(typename S::value_type *__restrict__ Y, i64 m, const int32_t *__restrict__ js) {
+    for (i64 k = blockIdx.x * (i64)NT + threadIdx.x; k < m; k += (i64)gridDim.x * NT) Y[k + (i64)js[k] * m] = S::one();
+}
+
 // ===== batched getrf + star of dense fronts (nb <= 64), one workgroup per front =====
 
 template <class S>
@@ -1960,6 +2001,13 @@ template <class S> struct FactorRun {
         if (fac->sym->S.nnz > 0)
             k_scatter_entries<T><<<grid1(fac->sym->S.nnz), NT, 0, st>>>(F, d.entry_pos, (const T *)nz, fac->sym->S.nnz);
         LAUNCHCHK();
+        if (fac->Nval) {
+            // the arcs between strongly connected components: N's values by column and by row
+            const i64 nN = fac->sym->S.nN;
+            k_gather<T><<<grid1(nN), NT, 0, st>>>((T *)fac->Nval, (const T *)nz, d.Nsrc, nN);
+            k_gather<T><<<grid1(nN), NT, 0, st>>>((T *)fac->NTval, (const T *)nz, d.NTsrc, nN);
+            LAUNCHCHK();
+        }
         for (const auto &L : P.levels) {
             if (L.asm_cnt)
                 k_assemble<S><<<(unsigned)L.asm_cnt, NT, 0, st>>>(F, d.Foff, d.nn, d.na, d.nj, d.Sptr, d.relpos, d.chptr,
@@ -2041,22 +2089,28 @@ static void launch_bwd(unsigned grid, int dmode, typename S::value_type *X, i64 
     }
 }
 
+// Rows of the sweeps: ROWS_ALL, every list on rows [0, nrows) (the solves); ROWS_STAR, each unit its star rows
+// (rowA forward, rowB backward); ROWS_OFFD, each unit the rows [rowC_lo, rowC_hi) of the star's second pass.
+enum { ROWS_ALL = 0, ROWS_STAR = 1, ROWS_OFFD = 2 };
+
 template <class S, int W>
 static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type *X, i64 ld, const SweepArgs &base,
-                        const SweepPlan &Wp, const SweepPlan::List &li, bool star_rows, i64 nrows, const void *Dpack,
+                        const SweepPlan &Wp, const SweepPlan::List &li, int rows_mode, i64 nrows, const void *Dpack,
                         const void *pack, hipStream_t st, const RowSub *rs) {
     typedef typename S::value_type T;
     const T *D = (const T *)Dpack, *Pk = (const T *)pack;
     const int32_t *tiles = base.pre;   // device copy of the prefix arrays
     const std::vector<int32_t> &HT = rs ? rs->tiles : Wp.tiles;
+    const bool star_rows = rows_mode == ROWS_STAR;
     SweepArgs a = base;
     if (fwd) {
         // one launch per list: the panels' own columns solved and scattered, per (64-row tile, target chunk)
         unsigned grid;
         a.cpre = tiles + li.pC;
-        if (star_rows) {
-            a.pre = tiles + li.pAu;
-            grid = (unsigned)HT[li.pAu + li.cnt];
+        if (rows_mode != ROWS_ALL) {
+            const i64 pu = rows_mode == ROWS_OFFD ? li.pCu : li.pAu;
+            a.pre = tiles + pu;
+            grid = (unsigned)HT[pu + li.cnt];
         } else {
             a.pre = nullptr;
             grid = (unsigned)(((nrows + TILE_ROWS - 1) / TILE_ROWS) * HT[li.pC + li.cnt]);
@@ -2073,9 +2127,10 @@ static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type
     } else {
         unsigned grid;
         i64 ntile = 0;
-        if (star_rows && !li.uniB) {
-            a.pre = tiles + li.pB64;
-            grid = (unsigned)HT[li.pB64 + li.cnt];
+        if (rows_mode == ROWS_OFFD || (star_rows && !li.uniB)) {
+            const i64 pb = rows_mode == ROWS_OFFD ? li.pC64 : li.pB64;
+            a.pre = tiles + pb;
+            grid = (unsigned)HT[pb + li.cnt];
             ntile = grid / std::max<i64>(1, li.cnt);
         } else {
             a.pre = nullptr;
@@ -2157,6 +2212,21 @@ static void launch_blocks(pp_ctx *ctx, const pp_fac *fac, bool fwd, typename S::
     else launch_blk<S, 4, 4>(ctx, fwd, X, ld, a, fac->Hpack, fac->Bpack);
 }
 
+// One panel list, dispatched on its width class.
+template <class S>
+static void launch_panels(bool fwd, int dmode, bool atomic, typename S::value_type *X, i64 ld, const SweepArgs &a,
+                          const SweepPlan &Wp, const SweepPlan::List &li, int rows_mode, i64 nrows, const void *Dpack,
+                          const void *pack, hipStream_t st, const RowSub *rs) {
+    switch (li.cls) {
+    case 0: launch_list<S, 1>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
+    case 1: launch_list<S, 2>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
+    case 2: launch_list<S, 4>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
+    case 3: launch_list<S, 8>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
+    case 4: launch_list<S, 16>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
+    default: launch_list<S, 32>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
+    }
+}
+
 // star_rows: each unit's own rows (those of the plan, or of the source subset rs); otherwise rows [0, nrows) for
 // every panel (the solves; atomic forward scatter).  star_lists: the star's units (blocks for the large fronts, the
 // small subtrees first forward and last backward; dmode 0 only) rather than panels only.
@@ -2232,19 +2302,79 @@ static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmod
         a.init_lo = star_rows ? rAlo : nullptr;
         a.init_hi = star_rows ? rAhi : nullptr;
         const bool atomic = !star_rows;
-        switch (li.cls) {
-        case 0: launch_list<S, 1>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st, rs); break;
-        case 1: launch_list<S, 2>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st, rs); break;
-        case 2: launch_list<S, 4>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st, rs); break;
-        case 3: launch_list<S, 8>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st, rs); break;
-        case 4: launch_list<S, 16>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st, rs); break;
-        default: launch_list<S, 32>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows, nrows, fac->Dpack, pack, st, rs); break;
-        }
+        launch_panels<S>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows ? ROWS_STAR : ROWS_ALL, nrows, fac->Dpack, pack,
+                         st, rs);
         LAUNCHCHK();
     }
     if (sl && !fwd) {
         subtrees();
         LAUNCHCHK();
+    }
+    return "";
+}
+
+// The sweeps over the component DAG when components are coupled by N (blocked/sgetrs.jl:80-122,
+// blocked/sgetri.jl:44-121).  up: Y <- Y A*, the levels of lev_up, each gathering N by column into its columns and
+// then running its panels (U forward, L backward); !up: Y <- Y (A*)^T, the levels of lev_dn, gathering N by row, then
+// the transposed sweeps (L^T forward, U^T backward).  offd: the star's second pass, each gather column and panel on
+// the rows of the earlier components of its own component ([anc_lo, first row)); else every row [0, nrows).  The
+// forward scatter is atomic: the rows of the panels of one level overlap.
+template <class S>
+static std::string run_coupled(pp_ctx *ctx, const pp_fac *fac, bool up, bool offd, typename S::value_type *Y, i64 ld,
+                               i64 nrows) {
+    typedef typename S::value_type T;
+    const SweepPlan &Wp = *fac->sym->splan;
+    const DevPlan &d = fac->plan;
+    hipStream_t st = ctx->stream;
+    if (nrows == 0) return "";
+    const int dmode = up ? 0 : 1;
+    const void *fpack = up ? fac->Upack : fac->Lpack, *bpack = up ? fac->Lpack : fac->Upack;
+    SweepArgs a;
+    a.pre = d.tiles;
+    a.cpre = nullptr;
+    a.nrows = (int32_t)nrows;
+    a.row_base = 0;
+    a.p_c0 = d.p_c0;
+    a.p_w = d.p_w;
+    a.p_e = d.p_e;
+    a.p_chunks = d.p_chunks;
+    a.row_lo = offd ? d.p_rowC_lo : nullptr;
+    a.row_hi = offd ? d.p_rowC_hi : nullptr;
+    a.p_eoff = d.p_eoff;
+    a.p_poff = d.p_poff;
+    a.p_doff = d.p_doff;
+    a.Eidx = d.Eidx;
+    a.init_lo = a.init_hi = nullptr;   // every row of a panel holds its forward values
+    const int rows_mode = offd ? ROWS_OFFD : ROWS_ALL;
+    i64 maxrows = nrows;
+    if (offd) {
+        maxrows = 0;
+        for (size_t k = 0; k < Wp.ccols.size(); k++) maxrows = std::max<i64>(maxrows, Wp.ccol_hi[k] - Wp.ccol_lo[k]);
+    }
+    const unsigned gy = (unsigned)std::max<i64>(1, std::min<i64>(64, (maxrows + NT - 1) / NT));
+    for (const auto &cl : up ? Wp.cup : Wp.cdn) {
+        if (cl.cols_cnt)
+            k_spmm_pull<S><<<dim3((unsigned)cl.cols_cnt, gy), NT, 0, st>>>(
+                Y, ld, d.ccols + cl.cols_off, offd ? d.ccol_lo + cl.cols_off : nullptr,
+                offd ? d.ccol_hi + cl.cols_off : nullptr, nrows, up ? d.Nptr : d.NTptr, up ? d.Nidx : d.NTidx,
+                (const T *)(up ? fac->Nval : fac->NTval));
+        LAUNCHCHK();
+        for (i64 k = 0; k < cl.fwd_cnt; k++) {
+            const auto &li = Wp.cfwd[cl.fwd_off + k];
+            SweepArgs b = a;
+            b.plist = d.plist + li.off;
+            b.np = (int32_t)li.cnt;
+            launch_panels<S>(true, dmode, true, Y, ld, b, Wp, li, rows_mode, nrows, fac->Dpack, fpack, st, nullptr);
+            LAUNCHCHK();
+        }
+        for (i64 k = 0; k < cl.bwd_cnt; k++) {
+            const auto &li = Wp.cbwd[cl.bwd_off + k];
+            SweepArgs b = a;
+            b.plist = d.plist + li.off;
+            b.np = (int32_t)li.cnt;
+            launch_panels<S>(false, dmode, true, Y, ld, b, Wp, li, rows_mode, nrows, fac->Dpack, bpack, st, nullptr);
+            LAUNCHCHK();
+        }
     }
     return "";
 }
@@ -2292,6 +2422,12 @@ template <class S> struct StarRun {
         e = run_sweeps<S>(ctx, fac, false, 0, X, n, true, n, fac->Lpack);
         if (!e.empty()) return e;
         timer_stop(ctx, 2);
+        if (fac->sym->splan->coupled) {
+            // the off-diagonal blocks between strongly connected components (the first pass left A_cc* on the
+            // diagonal blocks and zero elsewhere)
+            e = run_coupled<S>(ctx, fac, true, true, X, n, n);
+            if (!e.empty()) return e;
+        }
         timer_start(ctx, 3);
         if (!host) {
             relabel(X, n, (T *)out, ldc, 0, n);
@@ -2442,23 +2578,28 @@ template <class S> struct StarSrcRun {
         std::string pe = poison_fill(ctx, Y, (size_t)(m * n) * sizeof(T));
         if (!pe.empty()) return pe;
         timer_start(ctx, 4);
-        if (!cols) {
+        std::string e;
+        if (Wp.coupled) {
+            // components coupled by N: the rows (columns) of A* as the solve of unit rows, Y <- Y A* (Y (A*)^T)
+            k_fill<T><<<grid1(m * n), NT, 0, st>>>(Y, m * n, S::zero());
+            k_set_units<S><<<grid1(m), NT, 0, st>>>(Y, m, R->d_js);
+            LAUNCHCHK();
+            e = run_coupled<S>(ctx, fac, !cols, false, Y, m, m);
+        } else if (!cols) {
             const i64 nsu = (i64)Wp.sunits.size();
             if (nsu > 0)
                 k_identity_panels<S><<<dim3((unsigned)nsu, PANEL_W), NT, 0, st>>>(Y, m, d.sunits, R->d_js, n, d.p_c0, d.p_w,
                                                                                 R->d_rowA_lo, R->d_rowA_hi, R->d_rowB_lo,
                                                                                 R->d_rowB_hi);
-        } else if (Wp.np > 0) {
-            k_identity_panels<S><<<dim3((unsigned)Wp.np, PANEL_W), NT, 0, st>>>(Y, m, nullptr, R->d_js, n, d.p_c0, d.p_w,
-                                                                              R->d_rowA_lo, R->d_rowA_hi, R->d_rowB_lo,
-                                                                              R->d_rowB_hi);
-        }
-        LAUNCHCHK();
-        std::string e;
-        if (!cols) {
+            LAUNCHCHK();
             e = run_sweeps<S>(ctx, fac, true, 0, Y, m, true, m, fac->Upack, R, 1);
             if (e.empty()) e = run_sweeps<S>(ctx, fac, false, 0, Y, m, true, m, fac->Lpack, R, 1);
         } else {
+            if (Wp.np > 0)
+                k_identity_panels<S><<<dim3((unsigned)Wp.np, PANEL_W), NT, 0, st>>>(Y, m, nullptr, R->d_js, n, d.p_c0,
+                                                                                  d.p_w, R->d_rowA_lo, R->d_rowA_hi,
+                                                                                  R->d_rowB_lo, R->d_rowB_hi);
+            LAUNCHCHK();
             e = run_sweeps<S>(ctx, fac, true, 1, Y, m, true, m, fac->Lpack, R, 0);
             if (e.empty()) e = run_sweeps<S>(ctx, fac, false, 1, Y, m, true, m, fac->Upack, R, 0);
         }
@@ -2510,7 +2651,10 @@ template <class S> struct SolveRun {
         layout(0);
         LAUNCHCHK();
         std::string e;
-        if (left == trans) {
+        if (fac->sym->splan->coupled) {
+            // components coupled by N: level by level over the component DAG
+            e = run_coupled<S>(ctx, fac, left == trans, false, Y, nrhs, nrhs);
+        } else if (left == trans) {
             // Y <- Y A*: U forward, then L backward
             e = run_sweeps<S>(ctx, fac, true, 0, Y, nrhs, false, nrhs, fac->Upack);
             if (e.empty()) e = run_sweeps<S>(ctx, fac, false, 0, Y, nrhs, false, nrhs, fac->Lpack);

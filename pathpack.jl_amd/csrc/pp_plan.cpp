@@ -68,10 +68,11 @@ std::string build_factor_plan(const Symbolic &S, FactorPlan &P) {
             if (S.parent[f] >= 0) P.chidx[pos[S.parent[f]]++] = (int32_t)f;
     }
     // entries of A
+    // (an arc between two strongly connected components belongs to N, not to a front: position -1, skipped)
     P.entry_pos.resize(S.nnz);
     for (i64 p = 0; p < S.nnz; p++) {
-        i64 f = S.entry_front[p];
-        P.entry_pos[p] = P.Foff[f] + S.entry_row[p] + (i64)S.entry_col[p] * P.nj[f];
+        const i64 f = S.entry_front[p];
+        P.entry_pos[p] = f < 0 ? -1 : P.Foff[f] + S.entry_row[p] + (i64)S.entry_col[p] * P.nj[f];
     }
     // heights
     std::vector<i64> h(nf, 0);
@@ -321,37 +322,43 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
     for (i64 f = 0; f < nf; f++) P.sunits.insert(P.sunits.end(), su[f].begin(), su[f].end());
     P.sunits.insert(P.sunits.end(), P.sub_pan.begin(), P.sub_pan.end());
     auto rowtiles = [](i64 lo, i64 hi, i64 bm) { return hi > lo ? (hi - lo / bm * bm + bm - 1) / bm : 0; };
-    auto make_lists = [&](const std::vector<i64> &lv, bool fwd, std::vector<SweepPlan::List> &out) {
-        i64 L = 0;
-        for (i64 p = 0; p < nu; p++) L = std::max(L, lv[p] + 1);
-        constexpr int NC = BLK_CLS + 2;
-        std::vector<std::vector<int32_t>> buckets(L * NC);
-        for (i64 p = 0; p < nu; p++)
-            if (lv[p] >= 0) {
-                const int cls = p < P.np ? width_class(P.w[p]) : P.b_bn[p - P.np] == BLK_W ? BLK_CLS : BLK_CLS + 1;
-                buckets[lv[p] * NC + cls].push_back((int32_t)p);
-            }
-        for (i64 b = 0; b < (i64)buckets.size(); b++) {
-            if (buckets[b].empty()) continue;
+    auto unit_class = [&](i64 p) {
+        return p < P.np ? width_class(P.w[p]) : P.b_bn[p - P.np] == BLK_W ? BLK_CLS : BLK_CLS + 1;
+    };
+    // the rows of the star's second pass (components coupled by N): those of the earlier components with a path in
+    P.coupled = S.nB > 1 && S.nN > 0;
+    P.rowC_lo.assign(nu, 0);
+    P.rowC_hi.assign(nu, 0);
+    if (P.coupled)
+        for (i64 p = 0; p < nu; p++) {
+            const i64 c = S.comp[P.c0[p]];
+            P.rowC_lo[p] = (int32_t)S.anc_lo[c];
+            P.rowC_hi[p] = (int32_t)S.Bptr[c];
+        }
+    // one list of units of one level and width class, with the prefix arrays of its launches
+    auto emit = [&](int cls, const std::vector<int32_t> &bucket, bool fwd, std::vector<SweepPlan::List> &out) {
+        {
             SweepPlan::List li;
-            li.cls = (int)(b % NC);
+            li.cls = cls;
             li.off = (i64)P.plist.size();
-            li.cnt = (i64)buckets[b].size();
-            P.plist.insert(P.plist.end(), buckets[b].begin(), buckets[b].end());
+            li.cnt = (i64)bucket.size();
+            P.plist.insert(P.plist.end(), bucket.begin(), bucket.end());
             auto prefix = [&](auto units) {
                 const i64 off = (i64)P.tiles.size();
                 int64_t acc = 0;
                 P.tiles.push_back(0);
-                for (int32_t p : buckets[b]) {
+                for (int32_t p : bucket) {
                     acc += units(p);
                     P.tiles.push_back((int32_t)acc);
                 }
                 return off;
             };
-            auto tiles_of = [&](i64 lo, i64 hi, i64 rows) { return (hi - lo + rows - 1) / rows; };
+            auto tiles_of = [&](i64 lo, i64 hi, i64 rows) { return hi > lo ? (hi - lo + rows - 1) / rows : 0; };
             li.pAu = prefix([&](int32_t p) { return tiles_of(P.rowA_lo[p], P.rowA_hi[p], TILE_ROWS) * P.chunks[p]; });
             li.pB64 = prefix([&](int32_t p) { return tiles_of(P.rowB_lo[p], P.rowB_hi[p], TILE_ROWS); });
             li.pC = prefix([&](int32_t p) { return (i64)P.chunks[p]; });
+            li.pCu = prefix([&](int32_t p) { return tiles_of(P.rowC_lo[p], P.rowC_hi[p], TILE_ROWS) * P.chunks[p]; });
+            li.pC64 = prefix([&](int32_t p) { return tiles_of(P.rowC_lo[p], P.rowC_hi[p], TILE_ROWS); });
             li.pT[0] = li.pT[1] = 0;
             if (li.cls >= BLK_CLS)
                 for (int q = 0; q < 2; q++) {
@@ -362,13 +369,40 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
                     });
                 }
             li.esum = 0;
-            for (int32_t p : buckets[b]) li.esum += P.e[p];
+            for (int32_t p : bucket) li.esum += P.e[p];
             li.uniB = true;
-            li.rowB_lo = P.rowB_lo[buckets[b][0]];
-            li.rowB_hi = P.rowB_hi[buckets[b][0]];
-            for (int32_t p : buckets[b])
+            li.rowB_lo = P.rowB_lo[bucket[0]];
+            li.rowB_hi = P.rowB_hi[bucket[0]];
+            for (int32_t p : bucket)
                 if (P.rowB_lo[p] != li.rowB_lo || P.rowB_hi[p] != li.rowB_hi) li.uniB = false;
             out.push_back(li);
+        }
+    };
+    // the lists of the units with lv >= 0: by level (increasing), then width class
+    auto make_lists = [&](const std::vector<i64> &lv, bool fwd, std::vector<SweepPlan::List> &out) {
+        i64 L = 0;
+        for (i64 p = 0; p < nu; p++) L = std::max(L, lv[p] + 1);
+        constexpr int NC = BLK_CLS + 2;
+        std::vector<std::vector<int32_t>> buckets(L * NC);
+        for (i64 p = 0; p < nu; p++)
+            if (lv[p] >= 0) buckets[lv[p] * NC + unit_class(p)].push_back((int32_t)p);
+        for (i64 b = 0; b < (i64)buckets.size(); b++)
+            if (!buckets[b].empty()) emit((int)(b % NC), buckets[b], fwd, out);
+    };
+    // the same for a subset of the units
+    auto make_lists_of = [&](const std::vector<int32_t> &units, const std::vector<i64> &lv, bool fwd,
+                             std::vector<SweepPlan::List> &out) {
+        std::vector<std::pair<i64, int32_t>> key;   // (level * classes + class, unit)
+        constexpr int NC = BLK_CLS + 2;
+        for (int32_t p : units) key.push_back({lv[p] * NC + unit_class(p), p});
+        std::sort(key.begin(), key.end());
+        std::vector<int32_t> bucket;
+        for (size_t k = 0; k < key.size(); k++) {
+            bucket.push_back(key[k].second);
+            if (k + 1 == key.size() || key[k + 1].first != key[k].first) {
+                emit((int)(key[k].first % NC), bucket, fwd, out);
+                bucket.clear();
+            }
         }
     };
     P.plist.clear();
@@ -381,6 +415,50 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
     make_lists(lvB, false, P.bwd);
     make_lists(slvA, true, P.sfwd);
     make_lists(slvB, false, P.sbwd);
+    // the schedules over the component DAG (panels only, as the solves)
+    P.cup.clear();
+    P.cdn.clear();
+    P.cfwd.clear();
+    P.cbwd.clear();
+    P.ccols.clear();
+    P.ccol_lo.clear();
+    P.ccol_hi.clear();
+    if (P.coupled) {
+        std::vector<std::vector<int32_t>> cpan(S.nB);   // panels of each component
+        for (i64 p = 0; p < P.np; p++) cpan[S.comp[P.c0[p]]].push_back((int32_t)p);
+        auto schedule = [&](const std::vector<i32> &lev, bool up, std::vector<SweepPlan::CLevel> &out) {
+            i64 L = 0;
+            for (i64 c = 0; c < S.nB; c++) L = std::max<i64>(L, lev[c] + 1);
+            std::vector<std::vector<int32_t>> bylev(L);
+            for (i64 c = 0; c < S.nB; c++) bylev[lev[c]].push_back((int32_t)c);
+            std::vector<int32_t> units;
+            for (i64 l = 0; l < L; l++) {
+                SweepPlan::CLevel cl;
+                cl.cols_off = (i64)P.ccols.size();
+                units.clear();
+                for (int32_t c : bylev[l]) {
+                    for (i64 j = S.Bptr[c]; j < S.Bptr[c + 1]; j++) {
+                        const bool any = up ? S.Nptr[j + 1] > S.Nptr[j] : S.NTptr[j + 1] > S.NTptr[j];
+                        if (!any) continue;
+                        P.ccols.push_back((int32_t)j);
+                        P.ccol_lo.push_back((int32_t)S.anc_lo[c]);
+                        P.ccol_hi.push_back((int32_t)S.Bptr[c]);
+                    }
+                    units.insert(units.end(), cpan[c].begin(), cpan[c].end());
+                }
+                cl.cols_cnt = (i64)P.ccols.size() - cl.cols_off;
+                cl.fwd_off = (i64)P.cfwd.size();
+                make_lists_of(units, lvA, true, P.cfwd);
+                cl.fwd_cnt = (i64)P.cfwd.size() - cl.fwd_off;
+                cl.bwd_off = (i64)P.cbwd.size();
+                make_lists_of(units, lvB, false, P.cbwd);
+                cl.bwd_cnt = (i64)P.cbwd.size() - cl.bwd_off;
+                out.push_back(cl);
+            }
+        };
+        schedule(S.lev_up, true, P.cup);
+        schedule(S.lev_dn, false, P.cdn);
+    }
     return "";
 }
 
@@ -409,6 +487,7 @@ SweepSizes sweep_sizes(const Symbolic &S) {
         }
     }
     z.eidx += EIDX_PAD;
+    z.nN = S.nB > 1 ? S.nN : 0;
     return z;
 }
 

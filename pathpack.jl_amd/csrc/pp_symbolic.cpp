@@ -144,8 +144,8 @@ template <class Fn> void parallel_for(i64 count, int threads, Fn fn) {
     pool_run(threads, [&](int t) { fn(count * t / threads, count * (t + 1) / threads); });
 }
 
-// Symmetric pattern of A without the diagonal, neighbours sorted.
-std::string symmetrize(i64 n, const i64 *colptr, const i64 *rowval, Adj &G) {
+// The CSC arrays of an n x n pattern: "" when they are well formed.
+std::string check_csc(i64 n, const i64 *colptr, const i64 *rowval) {
     if (n < 0 || n > (i64)0x7fffffff) return "n out of range";
     if (colptr[0] != 0) return "colptr[0] must be 0";
     for (i64 j = 0; j < n; j++) {
@@ -155,6 +155,12 @@ std::string symmetrize(i64 n, const i64 *colptr, const i64 *rowval, Adj &G) {
             if (p > colptr[j] && rowval[p] <= rowval[p - 1]) return "row indices must be sorted and unique in each column";
         }
     }
+    return "";
+}
+
+// Symmetric pattern of A without the diagonal, neighbours sorted; with `comp`, only the pairs inside one component
+// (the pattern of the diagonal blocks).  The CSC arrays must have passed check_csc.
+std::string symmetrize(i64 n, const i64 *colptr, const i64 *rowval, Adj &G, const std::vector<i32> *comp = nullptr) {
     // A^T by a counting sort over the columns of A: the entries of each of its columns come out in increasing order
     const i64 nnz = colptr[n];
     std::vector<i64> tptr(n + 1, 0);
@@ -183,13 +189,73 @@ std::string symmetrize(i64 n, const i64 *colptr, const i64 *rowval, Adj &G) {
             } else {
                 x = tidx[b++];
             }
-            if (x != v) G.adj[w++] = (i32)x;
+            if (x != v && (!comp || (*comp)[x] == (*comp)[v])) G.adj[w++] = (i32)x;
         }
     }
     nx[n] = w;
     G.xadj = nx;
     G.adj.resize(w);
     return "";
+}
+
+// ===== strongly connected components (Tarjan 1972, iterative) =====
+//
+// The digraph has the arc i -> j for every stored A[i, j], i != j.  The search walks the arcs backwards, from
+// column j to its rows i, so a component is completed only after every component with an arc into it; numbering the
+// components in the order of completion therefore puts every arc between two components from a lower to a higher
+// number.  The reference's sccs! (utils.jl:18-70) walks the same column lists from the same roots.
+i64 strong_components(i64 n, const i64 *colptr, const i64 *rowval, std::vector<i32> &comp) {
+    comp.assign(n, -1);
+    std::vector<i32> index(n, -1), low(n, 0), stack, call;
+    std::vector<i64> edge(n, 0);
+    std::vector<char> on(n, 0);
+    stack.reserve(n);
+    i32 counter = 0, nc = 0;
+    for (i64 s0 = 0; s0 < n; s0++) {
+        if (index[s0] >= 0) continue;
+        auto enter = [&](i64 v) {
+            index[v] = low[v] = counter++;
+            edge[v] = colptr[v];
+            stack.push_back((i32)v);
+            on[v] = 1;
+            call.push_back((i32)v);
+        };
+        enter(s0);
+        while (!call.empty()) {
+            const i64 v = call.back();
+            if (edge[v] < colptr[v + 1]) {
+                const i64 w = rowval[edge[v]++];
+                if (index[w] < 0) enter(w);
+                else if (on[w]) low[v] = std::min(low[v], index[w]);
+                continue;
+            }
+            call.pop_back();
+            if (!call.empty()) low[call.back()] = std::min(low[call.back()], low[v]);
+            if (low[v] == index[v]) {
+                while (true) {
+                    const i64 w = stack.back();
+                    stack.pop_back();
+                    on[w] = 0;
+                    comp[w] = nc;
+                    if (w == v) break;
+                }
+                nc++;
+            }
+        }
+    }
+    return nc;
+}
+
+// perm (perm[new] = old) with the vertices of each component moved together, the components in increasing number,
+// and the vertices of one component in their order in perm (a stable counting sort).  The fill of each component's
+// own order is unchanged: no pattern entry joins two components.
+void group_by_component(std::vector<i64> &perm, const std::vector<i32> &comp, i64 nc) {
+    const i64 n = (i64)perm.size();
+    std::vector<i64> ptr(nc + 1, 0), out(n);
+    for (i64 k = 0; k < n; k++) ptr[comp[perm[k]] + 1]++;
+    for (i64 c = 0; c < nc; c++) ptr[c + 1] += ptr[c];
+    for (i64 k = 0; k < n; k++) out[ptr[comp[perm[k]]]++] = perm[k];
+    perm.swap(out);
 }
 
 // ===== nested dissection on level structures =====
@@ -942,8 +1008,100 @@ void work_counts(i64 n, const std::vector<i64> &Rptr, const std::vector<i64> &Sp
     }
 }
 
+// The component structure of out (perm, Rptr, invp set) from the components of the old labels: Bptr, Fptr, comp,
+// N by column and by row, the two level orders and the earliest ancestor rows.  "" or an error when the order does
+// not keep each component's vertices together in increasing component number.
+std::string components(i64 n, const i64 *colptr, const i64 *rowval, const std::vector<i32> &comp_old, i64 nB,
+                       Symbolic &out) {
+    const i64 nf = out.nf;
+    out.nB = nB;
+    out.comp.resize(n);
+    for (i64 k = 0; k < n; k++) out.comp[k] = comp_old[out.perm[k]];
+    for (i64 k = 1; k < n; k++)
+        if (out.comp[k] < out.comp[k - 1]) return "the order does not group the strongly connected components";
+    out.Bptr.assign(nB + 1, 0);
+    for (i64 k = 0; k < n; k++) out.Bptr[out.comp[k] + 1]++;
+    for (i64 c = 0; c < nB; c++) out.Bptr[c + 1] += out.Bptr[c];
+    out.Fptr.assign(nB + 1, nf);
+    for (i64 f = nf - 1; f >= 0; f--) out.Fptr[out.comp[out.Rptr[f]]] = f;
+    for (i64 f = 0; f < nf; f++)
+        if (out.comp[out.Rptr[f]] != out.comp[out.Rptr[f + 1] - 1]) return "a front spans two components";
+    for (i64 c = nB - 1; c >= 0; c--)
+        if (out.Fptr[c] > out.Fptr[c + 1]) out.Fptr[c] = out.Fptr[c + 1];
+    // N by column (new labels), rows ascending, then by row
+    out.Nptr.assign(n + 1, 0);
+    for (i64 c = 0; c < n; c++) {
+        const i64 j = out.invp[c];
+        for (i64 p = colptr[c]; p < colptr[c + 1]; p++) {
+            const i64 i = out.invp[rowval[p]];
+            if (out.comp[i] == out.comp[j]) continue;
+            if (out.comp[i] > out.comp[j]) return "internal error: an arc against the component order";
+            out.Nptr[j + 1]++;
+        }
+    }
+    for (i64 j = 0; j < n; j++) out.Nptr[j + 1] += out.Nptr[j];
+    out.nN = out.Nptr[n];
+    out.Nidx.resize(out.nN);
+    out.Nsrc.resize(out.nN);
+    {
+        std::vector<i64> pos(out.Nptr.begin(), out.Nptr.end() - 1);
+        for (i64 c = 0; c < n; c++) {
+            const i64 j = out.invp[c];
+            for (i64 p = colptr[c]; p < colptr[c + 1]; p++) {
+                const i64 i = out.invp[rowval[p]];
+                if (out.comp[i] == out.comp[j]) continue;
+                out.Nidx[pos[j]] = (i32)i;
+                out.Nsrc[pos[j]++] = p;
+            }
+        }
+        std::vector<std::pair<i32, i64>> tmp;
+        for (i64 j = 0; j < n; j++) {
+            tmp.clear();
+            for (i64 q = out.Nptr[j]; q < out.Nptr[j + 1]; q++) tmp.push_back({out.Nidx[q], out.Nsrc[q]});
+            std::sort(tmp.begin(), tmp.end());
+            for (i64 q = out.Nptr[j]; q < out.Nptr[j + 1]; q++) {
+                out.Nidx[q] = tmp[q - out.Nptr[j]].first;
+                out.Nsrc[q] = tmp[q - out.Nptr[j]].second;
+            }
+        }
+    }
+    // by row: a counting sort over the columns keeps each row's columns ascending
+    out.NTptr.assign(n + 1, 0);
+    for (i64 q = 0; q < out.nN; q++) out.NTptr[out.Nidx[q] + 1]++;
+    for (i64 i = 0; i < n; i++) out.NTptr[i + 1] += out.NTptr[i];
+    out.NTidx.resize(out.nN);
+    out.NTsrc.resize(out.nN);
+    {
+        std::vector<i64> pos(out.NTptr.begin(), out.NTptr.end() - 1);
+        for (i64 j = 0; j < n; j++)
+            for (i64 q = out.Nptr[j]; q < out.Nptr[j + 1]; q++) {
+                const i64 i = out.Nidx[q];
+                out.NTidx[pos[i]] = (i32)j;
+                out.NTsrc[pos[i]++] = out.Nsrc[q];
+            }
+    }
+    out.lev_up.assign(nB, 0);
+    out.lev_dn.assign(nB, 0);
+    out.anc_lo.resize(nB);
+    for (i64 c = 0; c < nB; c++) {
+        out.anc_lo[c] = out.Bptr[c];
+        for (i64 j = out.Bptr[c]; j < out.Bptr[c + 1]; j++)
+            for (i64 q = out.Nptr[j]; q < out.Nptr[j + 1]; q++) {
+                const i64 b = out.comp[out.Nidx[q]];
+                out.lev_up[c] = std::max(out.lev_up[c], out.lev_up[b] + 1);
+                out.anc_lo[c] = std::min(out.anc_lo[c], out.anc_lo[b]);
+            }
+    }
+    for (i64 c = nB - 1; c >= 0; c--)
+        for (i64 i = out.Bptr[c]; i < out.Bptr[c + 1]; i++)
+            for (i64 q = out.NTptr[i]; q < out.NTptr[i + 1]; q++)
+                out.lev_dn[c] = std::max(out.lev_dn[c], out.lev_dn[out.comp[out.NTidx[q]]] + 1);
+    return "";
+}
+
 std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, std::vector<i64> perm,
-                   std::vector<i64> Rptr, Symbolic &out, const std::vector<i64> *tree = nullptr) {
+                   std::vector<i64> Rptr, Symbolic &out, const std::vector<i64> *tree = nullptr,
+                   const std::vector<i32> *comp_old = nullptr, i64 nB = 1) {
     std::vector<i64> Sptr, parent;
     std::vector<i32> Stgt;
     double ts = now();
@@ -972,9 +1130,25 @@ std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, st
         out.Dptr[f + 1] = out.Dptr[f] + nn * nn;
         out.Lptr[f + 1] = out.Lptr[f] + nn * na;
     }
+    out.nB = 1;
+    out.nN = 0;
+    out.Bptr = {0, n};
+    out.Fptr = {0, nf};
+    out.comp.clear();
+    out.Nptr.assign(n + 1, 0);
+    out.NTptr.assign(n + 1, 0);
+    out.Nidx.clear(); out.Nsrc.clear(); out.NTidx.clear(); out.NTsrc.clear();
+    out.lev_up.assign(1, 0);
+    out.lev_dn.assign(1, 0);
+    out.anc_lo.assign(1, 0);
+    if (comp_old && nB > 1) {
+        err = components(n, colptr, rowval, *comp_old, nB, out);
+        if (!err.empty()) return err;
+    }
     // where each stored entry (i, j) lands (new labels): the front f of min(i, j), at the local positions of i and j
-    // in bag(f) = res(f) then sep(f).  Entries are grouped by front (counting sort), and each front's bag positions
-    // are scattered into a per-thread map over the vertices that its entries then read; in parallel over fronts.
+    // in bag(f) = res(f) then sep(f); an arc between two components is in N instead (entry_front = -1).  Entries are
+    // grouped by front (counting sort), and each front's bag positions are scattered into a per-thread map over the
+    // vertices that its entries then read; in parallel over fronts.
     stage("  structure copies", ts);
     out.nnz = colptr[n];
     const i64 nnz = out.nnz;
@@ -987,10 +1161,16 @@ std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, st
         for (i64 v = out.Rptr[f]; v < out.Rptr[f + 1]; v++) fof[v] = (i32)f;
     std::vector<i64> eptr(nf + 1, 0);
     std::vector<i32> eidx(nnz);
+    const bool split = out.nB > 1;
     for (i64 c = 0; c < n; c++) {
         const i64 j = out.invp[c];
         for (i64 p = colptr[c]; p < colptr[c + 1]; p++) {
-            const i64 f = fof[std::min<i64>(out.invp[rowval[p]], j)];
+            const i64 i = out.invp[rowval[p]];
+            if (split && out.comp[i] != out.comp[j]) {
+                out.entry_front[p] = -1;
+                continue;
+            }
+            const i64 f = fof[std::min<i64>(i, j)];
             out.entry_front[p] = f;
             eptr[f + 1]++;
         }
@@ -999,7 +1179,8 @@ std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, st
     for (i64 f = 0; f < nf; f++) eptr[f + 1] += eptr[f];
     {
         std::vector<i64> pos(eptr.begin(), eptr.end() - 1);
-        for (i64 p = 0; p < nnz; p++) eidx[pos[out.entry_front[p]]++] = (i32)p;
+        for (i64 p = 0; p < nnz; p++)
+            if (out.entry_front[p] >= 0) eidx[pos[out.entry_front[p]]++] = (i32)p;
     }
     std::vector<i64> colof(nnz);   // column of A of each entry
     for (i64 c = 0; c < n; c++)
@@ -1043,8 +1224,7 @@ std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, st
 std::string analyze_given(i64 n, const i64 *colptr, const i64 *rowval, const i64 *perm, i64 nf, const i64 *Rptr,
                           Symbolic &out) {
     double t0 = now();
-    Adj G;
-    std::string err = symmetrize(n, colptr, rowval, G);
+    std::string err = check_csc(n, colptr, rowval);
     if (!err.empty()) return err;
     std::vector<i64> p(perm, perm + n), R(Rptr, Rptr + nf + 1);
     std::vector<char> seen(n, 0);
@@ -1055,7 +1235,24 @@ std::string analyze_given(i64 n, const i64 *colptr, const i64 *rowval, const i64
     if (R[0] != 0 || R[nf] != n) return "Rptr must run from 0 to n";
     for (i64 f = 0; f < nf; f++)
         if (R[f + 1] <= R[f]) return "fronts must be nonempty";
-    err = finish(G, n, colptr, rowval, p, R, out);
+    // the strongly connected components, renumbered in the order the given permutation visits them (any topological
+    // order of the components is the reference's; components() checks that they come out grouped)
+    std::vector<i32> comp;
+    i64 nB = strong_components(n, colptr, rowval, comp);
+    if (nB > 1) {
+        std::vector<i32> ren(nB, -1);
+        i32 next = 0;
+        for (i64 k = 0; k < n; k++)
+            if (ren[comp[p[k]]] < 0) ren[comp[p[k]]] = next++;
+        for (i64 v = 0; v < n; v++) comp[v] = ren[comp[v]];
+        for (i64 j = 0; j < n; j++)
+            for (i64 q = colptr[j]; q < colptr[j + 1]; q++)
+                if (comp[rowval[q]] > comp[j]) return "the given order puts a strongly connected component before one with an arc into it";
+    }
+    Adj G;
+    err = symmetrize(n, colptr, rowval, G, nB > 1 ? &comp : nullptr);
+    if (!err.empty()) return err;
+    err = finish(G, n, colptr, rowval, p, R, out, nullptr, nB > 1 ? &comp : nullptr, nB);
     if (!err.empty()) return err;
     out.madds_factor_alg = out.madds_factor;
     out.madds_star_alg = out.madds_star;
@@ -1068,8 +1265,15 @@ std::string analyze_given(i64 n, const i64 *colptr, const i64 *rowval, const i64
 std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOptions &opts, const i64 *given_perm,
                     Symbolic &out) {
     double t0 = now();
+    std::string err = check_csc(n, colptr, rowval);
+    if (!err.empty()) return err;
+    // 0. strongly connected components in a topological order (sccs, chordal_ssymbolic.jl:26-57): the pattern that is
+    //    ordered and factorized is that of the diagonal blocks; every order below is regrouped by component
+    std::vector<i32> comp;
+    const i64 nB = strong_components(n, colptr, rowval, comp);
+    const std::vector<i32> *cp = nB > 1 ? &comp : nullptr;
     Adj G;
-    std::string err = symmetrize(n, colptr, rowval, G);
+    err = symmetrize(n, colptr, rowval, G, cp);
     if (!err.empty()) return err;
     {
         double tt = t0;
@@ -1087,6 +1291,10 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
         nd.run(analysis_threads(n));
         tamd.join();
         std::vector<i64> p1[2], pc[2], cc[2];
+        if (cp) {
+            group_by_component(nd.order, comp, nB);
+            group_by_component(pa, comp, nB);
+        }
         const std::vector<i64> *cand[2] = {&nd.order, &pa};
         std::thread t1([&] {
             etree_postorder(G, *cand[1], p1[1], pc[1]);
@@ -1120,6 +1328,7 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
             perm0[k] = given_perm[k];
         }
     }
+    if (cp && opts.ordering != 4) group_by_component(perm0, comp, nB);
     out.seconds_order = now() - t0;
     double ts = t0;
     stage("symmetrize + order", ts);
@@ -1161,7 +1370,7 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
         out.nnzL_alg = l;
     }
     if (!opts.amalgamate) {
-        err = finish(G, n, colptr, rowval, perm1, R1, out, &par1);
+        err = finish(G, n, colptr, rowval, perm1, R1, out, &par1, cp, nB);
         out.seconds_total = now() - t0;
         return err;
     }
@@ -1266,7 +1475,7 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
             if (par1[top] >= 0) tree2[fid[s]] = fid[root[par1[top]]];
         }
     stage("amalgamation", ts);
-    err = finish(G, n, colptr, rowval, perm2, R2, out, &tree2);
+    err = finish(G, n, colptr, rowval, perm2, R2, out, &tree2, cp, nB);
     stage("final structure + entries", ts);
     out.seconds_total = now() - t0;
     return err;

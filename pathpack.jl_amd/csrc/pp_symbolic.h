@@ -10,9 +10,12 @@
 //     fronts);
 //   * separators are computed by the supernodal symbolic factorization, so a structure given from outside (a
 //     permutation plus a partition into fronts, e.g. the reference's own) yields the same separators.
-// Unlike the reference, strongly connected components are not split into separate blocks: the whole pattern is
-// one block, and the block triangular structure is absorbed into the fronts (same star, more fill on DAG-like
-// inputs).
+// Strongly connected components are split as the reference does (sccs, chordal_ssymbolic.jl:26-57; utils.jl:3-70):
+// the components are numbered in a topological order of the graph (every arc between two components goes from a
+// lower to a higher number), each component's vertices get consecutive labels in that order, and only arcs inside a
+// component enter the symmetrized pattern.  So the pattern is block upper triangular, the fronts are per component
+// (one elimination tree each), and the arcs between components are kept apart as the sparse matrix N (soffd,
+// chordal_ssymbolic.jl:212-269), applied by the coupled sweeps.
 #pragma once
 #include <cstdint>
 #include <functional>
@@ -43,9 +46,24 @@ struct Symbolic {
     std::vector<i64> parent;            // parent front, -1 for roots
     std::vector<i64> fdsc;              // first descendant front of each front
     std::vector<i64> Dptr, Lptr;        // running sums of nn^2 and nn*na
+    // strongly connected components (in a topological order; nB == 1: one block, nothing below is used)
+    i64 nB = 1;
+    std::vector<i64> Bptr;              // vertices of component c: [Bptr[c], Bptr[c+1]) (new labels)
+    std::vector<i64> Fptr;              // fronts of component c: [Fptr[c], Fptr[c+1])
+    std::vector<i32> comp;              // component of each vertex (new labels)
+    // N: the arcs between components, A[i, j] with comp(i) < comp(j), in the new labels.  By column (CSC: rows i of
+    // column j ascending) and by row (CSR: columns j of row i ascending); *src is the position in A's nzval.
+    i64 nN = 0;
+    std::vector<i64> Nptr, Nsrc, NTptr, NTsrc;
+    std::vector<i32> Nidx, NTidx;
+    // per component: level in the arcs' direction (1 + the largest level of a component with an arc into it), level
+    // against it (1 + the largest level of a component it has an arc into), and the first vertex of the earliest
+    // component with a path into it (its own first vertex if none)
+    std::vector<i32> lev_up, lev_dn;
+    std::vector<i64> anc_lo;
     // the input pattern: where each stored entry of A lands in the frontal matrices
     i64 nnz = 0;
-    std::vector<i64> entry_front;       // front owning entry p (the front of min(new row, new col))
+    std::vector<i64> entry_front;       // front owning entry p (the front of min(new row, new col)); -1: an arc of N
     std::vector<i32> entry_row, entry_col;   // local row / column of entry p in that front's bag (res then sep)
     // work counts (semiring multiply-adds) of the exact structure, before amalgamation, and of the executed one
     double madds_factor_alg = 0, madds_star_alg = 0, madds_rhs_alg = 0, nnzL_alg = 0;

@@ -274,6 +274,19 @@ class Symbolic:
             self._export = {"perm": perm, "Rptr": R, "Sptr": S, "Stgt": T[:self.nstgt], "parent": P[:self.nf]}
         return self._export
 
+    def components(self) -> dict:
+        """The strongly connected components in a topological order (sccs, soffd; chordal_ssymbolic.jl:26-57,
+        212-269): nB, Bptr (component c holds the permuted vertices [Bptr[c], Bptr[c+1])), and N, the arcs between
+        components by permuted column: Nptr (n + 1), Nidx (permuted rows), Nsrc (positions in the analysed nzval)."""
+        nB, nN = ctypes.c_int64(), ctypes.c_int64()
+        check(lib().pp_sym_components(self.handle, ctypes.byref(nB), None, ctypes.byref(nN), None, None, None))
+        B = np.empty(nB.value + 1, np.int64)
+        Np = np.empty(self.n + 1, np.int64)
+        Ni = np.empty(max(1, nN.value), np.int64)
+        Ns = np.empty(max(1, nN.value), np.int64)
+        check(lib().pp_sym_components(self.handle, None, _p(B), None, _p(Np), _p(Ni), _p(Ns)))
+        return {"nB": nB.value, "Bptr": B, "Nptr": Np, "Nidx": Ni[:nN.value], "Nsrc": Ns[:nN.value]}
+
     def check_pattern(self, n: int, colptr, rowval):
         """PathpackArgumentError unless (n, colptr, rowval) is the analysed pattern."""
         same = n == self.n and len(rowval) == self.nnz

@@ -20,7 +20,7 @@ EXPORTS = [
     "pp_factor", "pp_factor_device", "pp_refactor", "pp_fac_export", "pp_fac_destroy",
     "pp_star", "pp_mstar", "pp_star_sources", "pp_lmul", "pp_rmul", "pp_sgemx", "pp_getrf_star_batched",
     "pp_buffer_alloc", "pp_buffer_free", "pp_upload", "pp_download", "pp_copy", "pp_calibrate_valu", "pp_set_timing",
-    "pp_get_timing", "pp_set_debug", "pp_sgetrs", "pp_sgetrs_noalloc",
+    "pp_get_timing", "pp_set_debug", "pp_sgetrs", "pp_sgetrs_noalloc", "pp_sym_components",
 ]
 
 
@@ -82,6 +82,7 @@ def lib() -> ctypes.CDLL:
         L.pp_sym_export.argtypes = [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]
         L.pp_sym_stats.argtypes = [c_vp, ctypes.POINTER(ctypes.c_double)]
         L.pp_sym_destroy.argtypes = [c_vp]
+        L.pp_sym_components.argtypes = [c_vp, c_i64p, c_vp, c_i64p, c_vp, c_vp, c_vp]
         L.pp_factor.argtypes = [c_vp, c_vp, ctypes.c_int, ctypes.c_int, c_vp, ctypes.POINTER(c_vp)]
         L.pp_factor_device.argtypes = [c_vp, c_vp, ctypes.c_int, ctypes.c_int, c_vp, ctypes.POINTER(c_vp)]
         L.pp_refactor.argtypes = [c_vp, c_vp, c_vp, ctypes.c_int]

@@ -199,6 +199,40 @@ def random_digraph(n: int, p: float, seed: int, lo: int = 1, hi: int = 100, dtyp
     return from_arcs(n, src, dst, w, "min", f"digraph{n}")
 
 
+def layered_digraph(layers: int, dims: tuple[int, ...], fwd: float = 0.3, seed: int = SEED_BASE, lo: int = 1,
+                    hi: int = 100, dtype=np.float64) -> Graph:
+    """A DAG of strongly connected layers: ``layers`` copies of the lattice ``dims`` with arcs both ways between
+    neighbours (each layer one strongly connected component), plus arcs from layer k to layer k + 1 only: vertex v of
+    layer k to the same vertex of layer k + 1, and each further pair (v in k, u in k + 1) with probability ``fwd``
+    divided by the layer size.  The condensation is a chain of ``layers`` components; vertex labels are shuffled."""
+    m = int(np.prod(dims))
+    n = layers * m
+    s0, d0 = _grid_arcs(dims)
+    src = [s0 + k * m for k in range(layers)]
+    dst = [d0 + k * m for k in range(layers)]
+    for k in range(layers - 1):
+        src.append(np.arange(m) + k * m)
+        dst.append(np.arange(m) + (k + 1) * m)
+        u = uniform_float(seed + 31 + k, m * m).reshape(m, m)
+        a, b = np.nonzero(u < fwd / m)
+        src.append(a + k * m)
+        dst.append(b + (k + 1) * m)
+    src, dst = np.concatenate(src), np.concatenate(dst)
+    lab = np.argsort(uniform_float(seed + 17, n), kind="stable")
+    w = uniform_int(seed + 7, src.size, lo, hi).astype(dtype)
+    return from_arcs(n, lab[src], lab[dst], w, "min", f"layered{layers}x{m}")
+
+
+def random_dag(n: int, p: float, seed: int, lo: int = 1, hi: int = 100, dtype=np.float64) -> Graph:
+    """A random DAG: arc i -> j with probability p for i < j in a seeded random order of the vertices (every vertex is
+    its own strongly connected component)."""
+    u = uniform_float(seed, n * n).reshape(n, n)
+    src, dst = np.nonzero((u < p) & np.triu(np.ones((n, n), dtype=bool), 1))
+    lab = np.argsort(uniform_float(seed + 3, n), kind="stable")
+    w = uniform_int(seed + 7, src.size, lo, hi).astype(dtype)
+    return from_arcs(n, lab[src], lab[dst], w, "min", f"dag{n}")
+
+
 def disjoint_union(parts: list[Graph], isolated: int = 0, seed: int = SEED_BASE, name: str = "") -> Graph:
     """The disjoint union of ``parts`` plus ``isolated`` vertices without arcs, with the vertices relabelled by a
     seeded permutation so that the components interleave."""

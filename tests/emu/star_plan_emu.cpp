@@ -34,6 +34,9 @@ int ppo_factor(int sr, int dt, i64 n, i64 nf, const i64 *Rptr, const i64 *Sptr, 
 int ppo_star(int sr, int dt, i64 n, i64 nf, const i64 *Rptr, const i64 *Sptr, const i64 *Stgt, const i64 *perm,
              const void *LD, const void *UD, const void *LL, const void *UL, void *C, i64 row0, i64 row1, int relabel,
              int nthreads);
+int ppo_star_scc(int sr, int dt, i64 n, i64 nf, const i64 *Rptr, const i64 *Sptr, const i64 *Stgt, const i64 *perm,
+                 const void *LD, const void *UD, const void *LL, const void *UL, i64 nB, const i64 *Bptr, const i64 *Nptr,
+                 const i64 *Nidx, const void *Nval, void *C, int nthreads);
 }
 
 static long nerr = 0;
@@ -87,7 +90,7 @@ template <class S> struct Emu {
     std::vector<T> LD, LL, UL;                 // device layout
     std::vector<T> Bpack, Hpack, stars;
     std::vector<T> X, X0;                      // X0: snapshot before a launch
-    std::vector<int32_t> wtask;                // writer task of the current launch, -1
+    std::vector<int32_t> wtask;                // writer task of the current launch, -1 (ATOMIC_W: atomic updates)
     std::vector<char> init;                    // element initialised
     int phase = 0;                             // 1: collect writes, 2: compute + check reads
     bool live = false;                         // reads see this launch's own writes (subtree launches)
@@ -112,6 +115,7 @@ template <class S> struct Emu {
     }
 
     // X access with launch semantics
+    static constexpr int32_t ATOMIC_W = -2;
     T rd(i64 r, i64 c, bool used) {
         if (r < 0 || r >= m || c < 0 || c >= n) {
             FAIL("OOB X read (%lld, %lld)", (long long)r, (long long)c);
@@ -119,10 +123,27 @@ template <class S> struct Emu {
         }
         i64 idx = r + c * m;
         if (phase == 2 && used) {
+            if (wtask[idx] == ATOMIC_W) FAIL("race: task %d reads (%lld,%lld), which the launch updates atomically", cur, (long long)r, (long long)c);
             if (wtask[idx] >= 0 && wtask[idx] != cur) FAIL("race: task %d reads (%lld,%lld) written by task %d", cur, (long long)r, (long long)c, wtask[idx]);
             if (!init[idx]) FAIL("read of uninitialised X(%lld, %lld) by task %d", (long long)r, (long long)c, cur);
         }
         return live ? X[idx] : X0[idx];
+    }
+    // an atomic X[r, c] (+)= v of the forward scatter: any number of tasks may do it; no task of the launch may read
+    // the element or write it plainly
+    void wr_atomic(i64 r, i64 c, T v) {
+        if (r < 0 || r >= m || c < 0 || c >= n) {
+            FAIL("OOB X atomic (%lld, %lld)", (long long)r, (long long)c);
+            return;
+        }
+        const i64 idx = r + c * m;
+        if (phase == 1) {
+            if (wtask[idx] >= 0) FAIL("race: atomic and plain writers of (%lld,%lld)", (long long)r, (long long)c);
+            wtask[idx] = ATOMIC_W;
+        } else {
+            if (!init[idx]) FAIL("atomic update of uninitialised X(%lld, %lld)", (long long)r, (long long)c);
+            X[idx] = S::plus(X[idx], v);
+        }
     }
     void wr(i64 r, i64 c, T v) {
         if (r < 0 || r >= m || c < 0 || c >= n) {
@@ -131,6 +152,7 @@ template <class S> struct Emu {
         }
         i64 idx = r + c * m;
         if (phase == 1) {
+            if (wtask[idx] == ATOMIC_W) FAIL("race: plain and atomic writers of (%lld,%lld)", (long long)r, (long long)c);
             if (wtask[idx] >= 0 && wtask[idx] != cur) FAIL("race: two writers of (%lld,%lld): %d, %d", (long long)r, (long long)c, wtask[idx], cur);
             wtask[idx] = cur;
         } else {
@@ -432,6 +454,99 @@ template <class S> struct Emu {
         live = false;
     }
 
+    // ---- the second pass over coupled components (run_coupled with up, offd) ----
+    std::vector<i64> Nptr, Nidx;             // N by column (permuted labels)
+    std::vector<T> Nval;
+    // k_spmm_pull: gather columns t of a level, rows [ccol_lo, ccol_hi), one task per (column, 256-row tile)
+    void spmm(const SweepPlan::CLevel &cl) {
+        X0 = X;
+        std::fill(wtask.begin(), wtask.end(), -1);
+        for (phase = 1; phase <= 2; phase++) {
+            for (i64 b = 0; b < cl.cols_cnt; b++) {
+                const i64 t = P.ccols[cl.cols_off + b];
+                const i64 lo = P.ccol_lo[cl.cols_off + b], hi = P.ccol_hi[cl.cols_off + b];
+                if (hi != Sy.Bptr[Sy.comp[t]] || lo != Sy.anc_lo[Sy.comp[t]]) FAIL("gather column %lld: wrong rows", (long long)t);
+                for (i64 r = lo; r < hi; r++) {
+                    cur = (int)(b * 100000 + (r - lo) / 256);
+                    T acc = rd(r, t, true);
+                    for (i64 q = Nptr[t]; q < Nptr[t + 1]; q++) acc = S::muladd(rd(r, Nidx[q], true), Nval[q], acc);
+                    wr(r, t, acc);
+                }
+            }
+        }
+        phase = 0;
+    }
+    // k_fwd with ATOMIC and per-panel rows [rowC_lo, rowC_hi): solve the panel's columns (not stored), then
+    // X[r, E_t] (+)= sum_j x_j (x) U(j, t) atomically
+    void panel_fwd_offd(int p, int task0) {
+        int f = P.front[p], w = P.w[p], e = P.e[p], c0 = P.c0[p], lj0 = c0 - (int)Sy.Rptr[f], lo = P.lo_ext[p];
+        i64 eo = P.eoff[p];
+        for (i64 r = P.rowC_lo[p]; r < P.rowC_hi[p]; r++) {
+            cur = task0 + (int)((r - P.rowC_lo[p]) / 64);
+            std::vector<T> x(w);
+            for (int j = 0; j < w; j++) x[j] = rd(r, c0 + j, true);
+            for (int j = 0; j < w; j++) {
+                T acc = x[j];
+                for (int i = 0; i < j; i++) acc = S::muladd(x[i], D(f, lj0 + i, lj0 + j), acc);
+                if (!S::integral) acc = S::prod(acc, S::star(D(f, lj0 + j, lj0 + j)));
+                x[j] = acc;
+            }
+            for (int t = 0; t < e; t++) {
+                T v = S::zero();
+                for (int j = 0; j < w; j++) v = S::muladd(x[j], Uext(f, lj0, lo, j, t), v);
+                wr_atomic(r, P.Eidx[eo + t], v);
+            }
+        }
+    }
+    // k_sweep_bwd on the rows [rowC_lo, rowC_hi), every row holding the panel's forward values
+    void panel_bwd_offd(int p, int task0) {
+        int f = P.front[p], w = P.w[p], e = P.e[p], c0 = P.c0[p], lj0 = c0 - (int)Sy.Rptr[f], lo = P.lo_ext[p];
+        i64 eo = P.eoff[p];
+        for (i64 r = P.rowC_lo[p]; r < P.rowC_hi[p]; r++) {
+            cur = task0 + (int)((r - P.rowC_lo[p]) / 64);
+            std::vector<T> acc(w);
+            for (int j = 0; j < w; j++) acc[j] = rd(r, c0 + j, true);
+            for (int j = 0; j < w; j++) {
+                T sv = acc[j];
+                for (int i = 0; i < j; i++) sv = S::muladd(acc[i], D(f, lj0 + i, lj0 + j), sv);
+                if (!S::integral) sv = S::prod(sv, S::star(D(f, lj0 + j, lj0 + j)));
+                acc[j] = sv;
+            }
+            for (int t = 0; t < e; t++) {
+                T v = rd(r, P.Eidx[eo + t], true);
+                for (int j = 0; j < w; j++) acc[j] = S::muladd(v, Lext(f, lj0, lo, t, j), acc[j]);
+            }
+            for (int j = w - 1; j >= 0; j--) {
+                T sv = acc[j];
+                for (int i = j + 1; i < w; i++) sv = S::muladd(acc[i], D(f, lj0 + i, lj0 + j), sv);
+                acc[j] = sv;
+            }
+            for (int j = 0; j < w; j++) wr(r, c0 + j, acc[j]);
+        }
+    }
+    void run_list_offd(const SweepPlan::List &li, bool fwd) {
+        X0 = X;
+        std::fill(wtask.begin(), wtask.end(), -1);
+        if (li.cls >= BLK_CLS) FAIL("a block in a list of the second pass");
+        for (phase = 1; phase <= 2; phase++) {
+            int task0 = 0;
+            for (i64 k = 0; k < li.cnt; k++) {
+                int p = P.plist[li.off + k];
+                if (fwd) panel_fwd_offd(p, task0);
+                else panel_bwd_offd(p, task0);
+                task0 += 100000;
+            }
+        }
+        phase = 0;
+    }
+    void second_pass() {
+        for (const auto &cl : P.cup) {
+            if (cl.cols_cnt) spmm(cl);
+            for (i64 k = 0; k < cl.fwd_cnt; k++) run_list_offd(P.cfwd[cl.fwd_off + k], true);
+            for (i64 k = 0; k < cl.bwd_cnt; k++) run_list_offd(P.cbwd[cl.bwd_off + k], false);
+        }
+    }
+
     void run_list(const SweepPlan::List &li, bool fwd) {
         // phase 1 writes, phase 2 values
         X0 = X;
@@ -517,12 +632,29 @@ template <class S> int run(const char *path, int sr, int dt, int ncu, long mod) 
     for (auto &li : E.P.sfwd) E.run_list(li, true);
     for (auto &li : E.P.sbwd) E.run_list(li, false);
     E.subtrees(false);
+    // the off-diagonal blocks between components coupled by N (the rows of a source subset take the solve path
+    // instead, which this replay does not cover)
+    const bool coupled = E.P.coupled && mod <= 0;
+    std::vector<i64> Bptr(Sy.Bptr.begin(), Sy.Bptr.end());
+    if (coupled) {
+        E.Nptr.assign(Sy.Nptr.begin(), Sy.Nptr.end());
+        E.Nidx.assign(Sy.Nidx.begin(), Sy.Nidx.end());
+        E.Nval.resize(Sy.nN);
+        for (i64 q = 0; q < Sy.nN; q++) E.Nval[q] = nzval[Sy.Nsrc[q]];
+        printf("components %lld, arcs between them %lld, levels %zu\n", (long long)Sy.nB, (long long)Sy.nN, E.P.cup.size());
+        E.second_pass();
+    }
     std::vector<T> C(n * n), Co(n * n);
     if (mod <= 0)
         for (i64 j = 0; j < n; j++)
             for (i64 i = 0; i < n; i++) C[i + j * n] = E.X[Sy.invp[i] + Sy.invp[j] * n];
-    rc = ppo_star(sr, dt, n, Sy.nf, Sy.Rptr.data(), Sy.Sptr.data(), Sy.Stgt.data(), Sy.perm.data(), LDo.data(), UDo.data(),
-                  LLo.data(), ULo.data(), Co.data(), 0, n, 1, 8);
+    if (coupled)
+        rc = ppo_star_scc(sr, dt, n, Sy.nf, Sy.Rptr.data(), Sy.Sptr.data(), Sy.Stgt.data(), Sy.perm.data(), LDo.data(),
+                          UDo.data(), LLo.data(), ULo.data(), Sy.nB, Bptr.data(), E.Nptr.data(), E.Nidx.data(),
+                          E.Nval.data(), Co.data(), 8);
+    else
+        rc = ppo_star(sr, dt, n, Sy.nf, Sy.Rptr.data(), Sy.Sptr.data(), Sy.Stgt.data(), Sy.perm.data(), LDo.data(),
+                      UDo.data(), LLo.data(), ULo.data(), Co.data(), 0, n, 1, 8);
     if (rc) { fprintf(stderr, "oracle star %d\n", rc); return 4; }
     // the entries compared: all of the star, or the rows of the sources (row k of X is source js[k])
     std::vector<i64> qs;

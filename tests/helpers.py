@@ -12,7 +12,7 @@ SEMIRINGS = {O.MINPLUS: P.MinPlus(), O.MAXPLUS: P.MaxPlus(), O.MAXMIN: P.MaxMin(
 
 def oracle_sym(sym: P.Symbolic) -> O.Sym:
     e = sym.export()
-    return O.Sym(sym.n, e["Rptr"], e["Sptr"], e["Stgt"], e["perm"])
+    return O.Sym(sym.n, e["Rptr"], e["Sptr"], e["Stgt"], e["perm"], sym.components()["Bptr"])
 
 
 def weighted(g: W.Graph, s: int, dtype, seed: int = 11) -> W.Graph:
@@ -44,6 +44,9 @@ def assert_star_equal(s: int, C, D, rtol=1e-12):
         floor = np.finfo(np.result_type(np.asarray(C).dtype, np.asarray(D).dtype)).tiny
         C = np.asarray(C, np.float64)
         D = np.asarray(D, np.float64)
+        assert C.shape == D.shape, f"shapes {C.shape} and {D.shape}"
+        if C.size == 0:
+            return
         scale = np.maximum(np.abs(D), floor)
         err = np.abs(C - D) / scale
         err[(C == 0) & (D == 0)] = 0

@@ -486,7 +486,8 @@ def test_oversized_requests_are_refused_before_launch():
 
     n = 300_000
     src = np.arange(n - 1)
-    g = W.from_arcs(n, src, src + 1, np.ones(n - 1, np.float32))
+    # a path with arcs both ways (one strongly connected component)
+    g = W.from_arcs(n, np.concatenate([src, src + 1]), np.concatenate([src + 1, src]), np.ones(2 * (n - 1), np.float32))
     sym = P.symbolic(g)
     ctx = P.context(0)
     out = np.zeros(16, np.float32)
@@ -502,6 +503,61 @@ def test_oversized_requests_are_refused_before_launch():
     ctx.synchronize()
     # the context and the factor still work: rows of the star of the path graph are distances along it
     R = P.star_rows(F, [0, n - 1])
-    assert R[0, 0] == 0 and R[0, n - 1] == n - 1 and R[1, 0] == np.inf
+    assert R[0, 0] == 0 and R[0, n - 1] == n - 1 and R[1, 0] == n - 1 and R[1, n - 1] == 0
     small = weighted(W.random_digraph(90, 0.05, 12), O.MINPLUS, np.float32)
     assert np.array_equal(P.mstar(P.MinPlus(), small), O.floyd_warshall(O.MINPLUS, small.dense(np.float32(np.inf))))
+
+
+DAG_GRAPHS = {
+    "layered": lambda: W.layered_digraph(6, (8, 6), fwd=0.5, seed=3),      # a chain of 6 strongly connected layers
+    "layered3d": lambda: W.layered_digraph(5, (6, 5, 4), seed=4),          # 5 layers of 120 vertices
+    "dag": lambda: W.random_dag(150, 0.04, 9),                             # 150 one-vertex components, 12 levels
+    "digraph300": lambda: W.random_digraph(300, 0.01, 3),                  # 30 components, 88 arcs between them
+}
+
+
+@pytest.mark.parametrize("name", list(DAG_GRAPHS))
+@pytest.mark.parametrize("s,fdtype", [(O.MINPLUS, np.float32), (O.MAXPLUS, np.float64), (O.MAXMIN, np.float32),
+                                      (O.MINMAX, np.float64), (O.PLUSPROD, np.float64), (O.PLUSPROD, np.float32),
+                                      (O.ORAND, np.float32)])
+def test_coupled_components_match_oracle(name, s, fdtype):
+    """Strongly connected components coupled by arcs between them (the block triangular level: sccs and soffd,
+    chordal_ssymbolic.jl:26-57,212-269; blocked/sgetri.jl, blocked/sgetrs.jl): the factor of the diagonal blocks,
+    the full star (the first pass on the diagonal blocks, then the pass over the component DAG), mstar, lmul!/rmul!
+    plain and transposed, and rows / columns for sources, all against the oracle's blocked algorithms; the star also
+    against Floyd-Warshall (or (I - A)^-1), and under poisoned buffers."""
+    dtype = dtype_for(s, fdtype)
+    g = weighted(DAG_GRAPHS[name](), s, dtype)
+    print(f"case coupled {name} s={s} dtype={np.dtype(dtype)}", flush=True)
+    sym, F, Fo = both(g, s, dtype)
+    cm = sym.components()
+    assert cm["nB"] > 1 and cm["Nptr"][-1] > 0
+    compare_factor(s, F, Fo, dtype)
+    rtol = rtol_for(s, dtype)
+    Co = O.star(Fo)
+    ref = O.plusprod_inverse(g.dense(0.0)) if s == O.PLUSPROD else O.floyd_warshall(s, g.dense(O.zero(s, dtype)))
+    assert_star_equal(s, Co, ref, rtol=max(rtol, 1e-12))
+    ctx = P.context(0)
+    ctx.set_poison(True)
+    try:
+        assert_star_equal(s, P.Matrix(F), Co, rtol=rtol)
+        assert_star_equal(s, P.mstar(SEMIRINGS[s], g, sym=sym), Co, rtol=rtol)
+        rng = np.random.default_rng(2)
+        B = np.full((g.n, 9), O.zero(s, dtype), dtype=dtype, order="F")
+        B[rng.integers(0, g.n, 9), np.arange(9)] = O.one(s, dtype)
+        if s == O.ORAND:
+            B[:, -2:] = rng.integers(0, 128, (g.n, 2)).astype(np.int32)
+        elif s == O.PLUSPROD:
+            B[:, -2:] = rng.random((g.n, 2))
+        else:
+            B[:, -2:] = rng.integers(0, 50, (g.n, 2)).astype(dtype)
+        Bt = np.asfortranarray(B.T)
+        assert_star_equal(s, P.lmul_(F, B.copy(order="F")), O.lmul(Fo, B), rtol=rtol)
+        assert_star_equal(s, P.rmul_(Bt.copy(order="F"), F), O.rmul(Fo, Bt), rtol=rtol)
+        assert_star_equal(s, P.lmul_(P.transpose(F), B.copy(order="F")), O.lmul_t(Fo, B), rtol=rtol)
+        assert_star_equal(s, P.rmul_(Bt.copy(order="F"), P.transpose(F)), O.rmul_t(Fo, Bt), rtol=rtol)
+        src = np.concatenate([[0, g.n - 1], rng.choice(g.n, size=20, replace=False), [5, 5]])
+        assert_star_equal(s, P.star_rows(F, src), Co[src, :], rtol=rtol)
+        assert_star_equal(s, P.star_cols(F, src), Co[:, src], rtol=rtol)
+    finally:
+        ctx.set_poison(False)

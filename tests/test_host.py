@@ -40,9 +40,18 @@ def test_separators_match_the_reference(name):
     assert np.array_equal(e["Stgt"], fx["Stgt"])
 
 
+def scipy_sccs(g: W.Graph) -> np.ndarray:
+    """Strongly connected component labels of the digraph i -> j (A[i, j] != 0) by scipy (an independent check)."""
+    from scipy.sparse.csgraph import connected_components
+
+    return connected_components(g.scipy().T, directed=True, connection="strong")[1]
+
+
 def check_structure(g: W.Graph, sym: P.Symbolic):
     """perm is a permutation; fronts partition 0..n-1 in postorder; every separator is sorted, lies after its front
-    and inside its parent's bag; every arc of A lies inside a front's bag."""
+    and inside its parent's bag; every arc of A inside a strongly connected component lies inside a front's bag; the
+    components are scipy's, each holds consecutive permuted labels, and the arcs between them are exactly N, each from
+    a lower to a higher component (the block upper triangular form of chordal_ssymbolic.jl:26-57)."""
     e = sym.export()
     n = g.n
     perm, R, S, T, par = e["perm"], e["Rptr"], e["Sptr"], e["Stgt"], e["parent"]
@@ -63,7 +72,27 @@ def check_structure(g: W.Graph, sym: P.Symbolic):
             assert par[f] == -1
     cols = np.repeat(np.arange(n), np.diff(g.colptr))
     i, j = invp[g.rowval], invp[cols]
-    lo, hi = np.minimum(i, j), np.maximum(i, j)
+    # components: scipy's partition, consecutive permuted labels, fronts inside one component each
+    cm = sym.components()
+    B = cm["Bptr"]
+    comp = np.repeat(np.arange(cm["nB"]), np.diff(B))        # component of each permuted label
+    ref = scipy_sccs(g)[perm]
+    assert cm["nB"] == ref.max() + 1
+    assert np.all(np.diff(comp) >= 0)
+    pairs = set(zip(comp.tolist(), ref.tolist()))
+    assert len(pairs) == cm["nB"] and len({a for a, _ in pairs}) == len({b for _, b in pairs})
+    assert np.all(comp[R[:-1]] == comp[R[1:] - 1])
+    cross = comp[i] != comp[j]
+    assert np.all(comp[i][cross] < comp[j][cross])
+    # N: exactly the crossing arcs, by permuted column, rows ascending, with their nzval positions
+    Np, Ni, Ns = cm["Nptr"], cm["Nidx"], cm["Nsrc"]
+    assert Np[-1] == cross.sum()
+    ncol = np.repeat(np.arange(n), np.diff(Np))
+    assert np.array_equal(np.sort(Ns), np.flatnonzero(cross))
+    assert np.array_equal(Ni, i[Ns]) and np.array_equal(ncol, j[Ns])
+    for c in range(n):
+        assert np.all(np.diff(Ni[Np[c]:Np[c + 1]]) > 0)
+    lo, hi = np.minimum(i, j)[~cross], np.maximum(i, j)[~cross]
     f = idx[lo]
     inres = hi < R[f + 1]
     for a, b, ff in zip(lo[~inres], hi[~inres], f[~inres]):
@@ -109,6 +138,24 @@ def test_automatic_order_keeps_the_smaller_factor(maker):
     fills = {alg: P.symbolic(g, alg=alg).stats()["nnzL_alg"] for alg in ("nd", "amd", "auto")}
     assert fills["auto"] == min(fills["nd"], fills["amd"])
     check_structure(g, P.symbolic(g, alg="auto"))
+
+
+@pytest.mark.parametrize("maker", [lambda: W.layered_digraph(6, (8, 6), fwd=0.5, seed=3),
+                                   lambda: W.random_dag(150, 0.04, 9), lambda: W.layered_digraph(5, (6, 5, 4), seed=4)])
+def test_dag_like_structure_is_valid_and_smaller(maker):
+    """On DAG-like graphs the strongly connected components split the pattern into blocks (one elimination tree each;
+    N between them), and the factor has fewer entries than the single block of the symmetrized pattern (the same
+    graph with every arc made two-way)."""
+    g = maker()
+    sym = P.symbolic(g)
+    check_structure(g, sym)
+    cols = np.repeat(np.arange(g.n), np.diff(g.colptr))
+    gs = W.from_arcs(g.n, np.concatenate([g.rowval, cols]), np.concatenate([cols, g.rowval]),
+                     np.concatenate([g.nzval, g.nzval]))
+    assert P.symbolic(gs).components()["nB"] < sym.components()["nB"]
+    assert sym.stats()["nnzL_alg"] < P.symbolic(gs).stats()["nnzL_alg"]
+    for alg in ("amd", "auto", "natural"):
+        check_structure(g, P.symbolic(g, alg=alg))
 
 
 def test_natural_and_given_orderings():

@@ -68,6 +68,32 @@ def test_oracle_star_vs_floyd_warshall(n, p, seed, s):
         assert_star_equal(s, C, ref)
 
 
+DAG_LIKE = {
+    "layered": lambda: W.layered_digraph(6, (8, 6), fwd=0.5, seed=3),   # a chain of six strongly connected layers
+    "dag": lambda: W.random_dag(150, 0.04, 9),                          # 150 components of one vertex
+}
+
+
+@pytest.mark.parametrize("name", list(DAG_LIKE))
+@pytest.mark.parametrize("s", [O.MINPLUS, O.MAXPLUS, O.MAXMIN, O.MINMAX, O.ORAND, O.PLUSPROD])
+def test_oracle_star_of_dag_like_graphs(name, s):
+    """Graphs whose strongly connected components form a chain or a deep DAG: the blocked star and solves over the
+    components (blocked/sgetri.jl, blocked/sgetrs.jl; N applied between them) against Floyd-Warshall / (I - A)^-1,
+    with the amalgamated and the fundamental structure."""
+    dtype = dtype_for(s)
+    g = weighted(DAG_LIKE[name](), s, dtype)
+    ref = O.plusprod_inverse(g.dense(0.0)) if s == O.PLUSPROD else O.floyd_warshall(s, g.dense(O.zero(s, dtype)))
+    for amalg in (True, False):
+        sym = P.symbolic(g, amalgamate=amalg)
+        assert sym.components()["nB"] > 5 and sym.components()["Nptr"][-1] > 0
+        F = O.factor(s, oracle_sym(sym), g.colptr, g.rowval, g.nzval)
+        assert_star_equal(s, O.star(F), ref)
+        I = np.full((g.n, g.n), O.zero(s, dtype), dtype=dtype)
+        np.fill_diagonal(I, O.one(s, dtype))
+        assert_star_equal(s, O.rmul(F, I), ref)
+        assert_star_equal(s, O.lmul(F, I), ref)
+
+
 @pytest.mark.parametrize("s", [O.MINPLUS, O.MAXMIN, O.ORAND, O.PLUSPROD])
 def test_oracle_star_of_disconnected_graph(s):
     """Eleven components (grids, a random digraph, a geometric graph, isolated vertices) with interleaved labels:

@@ -1,5 +1,6 @@
 """CPU replay of the star's device schedule (tests/emu/star_plan_emu.cpp): the real plan and block packs, the device
-kernels' index arithmetic launch by launch, bounds / race / initialisation checks, and the result against the oracle.
+kernels' index arithmetic launch by launch, bounds / race / initialisation checks, and the result against the oracle
+(its blocked star when strongly connected components are coupled by arcs between them).
 
 The replay is built with hipcc as host code (it includes the plan headers) and linked with the oracle library; it is
 skipped where hipcc is absent.  Graphs are chosen so that large fronts cut into 128- and 64-column blocks, blocks are
@@ -53,8 +54,13 @@ GRAPHS = {
     "components": lambda: W.disjoint_union([W.grid((10, 10, 9)), W.grid((30, 29)), W.rgg(300, seed=5)],
                                            isolated=3, name="components"),
     # one 64-wide block whose component rows reach far outside its subtree: the padded K steps of the backward
-    # block GEMM read rows that nothing has written yet (NaN under PlusProd before the fix)
+    # block GEMM read rows that nothing has written yet (NaN under PlusProd before the fix); also 30 strongly
+    # connected components with 88 arcs between them (the coupled second pass)
     "digraph300": lambda: W.random_digraph(300, 0.01, 3),
+    # strongly connected layers in a chain, and a DAG of 150 one-vertex components: the second pass over the
+    # component DAG (the gathers of N, then the panel lists on the rows of the earlier components, atomic forward)
+    "layered": lambda: W.layered_digraph(6, (8, 6), fwd=0.5, seed=3),
+    "dag": lambda: W.random_dag(150, 0.04, 9),
 }
 
 # X starts as NaN (-1 for OrAnd) in the replay, so every semiring checks that no value read before it is written
@@ -64,7 +70,7 @@ ALL = [(O.MINPLUS, np.float32), (O.MINPLUS, np.float64), (O.MAXPLUS, np.float32)
        (O.ORAND, np.float32)]
 FEW = [(O.MINPLUS, np.float32), (O.MINPLUS, np.float64), (O.PLUSPROD, np.float32), (O.PLUSPROD, np.float64)]
 CASES = [(name, s, d) for name in GRAPHS
-         for (s, d) in (ALL if name in ("grid9x9x9", "components", "digraph300") else FEW)]
+         for (s, d) in (ALL if name in ("grid9x9x9", "components", "digraph300", "layered", "dag") else FEW)]
 
 
 @pytest.mark.parametrize("name,s,fdtype", CASES)
