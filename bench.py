@@ -13,6 +13,7 @@ Other configurations of the benchmark suite (one JSON line each, same keys):
     --config 2b   batched front LU + stars, 16384 fronts of 64 x 64, Float32 (pp_getrf_star_batched)
     --config 4    MaxMin lmul! of 1024 unit columns on a random geometric graph, n = 65536, Float32
     --config 5    PlusProd rmul! of 512 unit rows on the directed 256 x 256 grid, Float64
+    --config dag  MinPlus mstar of a chain of 16 strongly connected layers (components coupled by arcs), n = 16384
 The default is the headline configuration 3.
 """
 
@@ -507,12 +508,52 @@ def bench_solve(args, cfg):
     print(json.dumps(r), flush=True)
 
 
+def bench_dag(args):
+    """Strongly connected components coupled by arcs: MinPlus mstar of a chain of 16 strongly connected layers (each
+    a 16 x 16 x 4 grid with arcs both ways; arcs from layer k to k + 1 only), n = 16384, Float32, star left in HBM.
+    Beside it, the same graph with every arc made two-way (one strongly connected block: the fill a symmetrized
+    pattern pays)."""
+    import ctypes
+
+    g = W.layered_digraph(16, (16, 16, 4), seed=W.SEED_BASE + 6, dtype=np.float32)
+    cols = np.repeat(np.arange(g.n), np.diff(g.colptr))
+    gs = W.from_arcs(g.n, np.concatenate([g.rowval, cols]), np.concatenate([cols, g.rowval]),
+                     np.concatenate([g.nzval, g.nzval]))
+    ctx = P.context(0)
+    out = P.DeviceArray((g.n, g.n), np.float32)
+    res = {}
+    for label, gg in (("components", g), ("one_block", gs)):
+        dnz = P.DeviceArray.from_numpy(np.ascontiguousarray(gg.nzval).reshape(-1, 1))
+
+        def step():
+            sym = P.symbolic(gg)
+            h = ctypes.c_void_p()
+            ctx.check(P.lib().pp_mstar(ctx.handle, sym.handle, 0, 0, ctypes.c_void_p(dnz.ptr), 1, ctypes.c_void_p(out.ptr),
+                                       gg.n, 1, None))
+            return sym
+
+        T = timed(step, ctx, args.steps, args.warmup)
+        sym = P.symbolic(gg)
+        st, cm = sym.stats(), sym.components()
+        res[label] = {"ms_per_step": round(T * 1e3, 3), "components": cm["nB"], "arcs_between": int(cm["Nptr"][-1]),
+                      "nnzL_alg": st["nnzL_alg"], "madds_alg": st["madds_factor_alg"] + st["madds_star_alg"]}
+        log(f"{label}: {res[label]}")
+    T = res["components"]["ms_per_step"] * 1e-3
+    r = base_result(args, "mstar sec + semiring Gop/s, MinPlus chain of 16 strongly connected 16x16x4 layers, n=16384",
+                    res["components"]["madds_alg"] / T / 1e9, "semiring Gop/s", T, "f32",
+                    "MinPlus mstar of layered_digraph(16, (16, 16, 4)) (arcs both ways inside a layer, forward between "
+                    "layers), weights U{1..100} Float32 (seed 0x5EED+6); star left in HBM", {"n": g.n})
+    r["components"] = res["components"]
+    r["one_block_two_way_arcs"] = res["one_block"]
+    print(json.dumps(r), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", default="3", choices=["1", "2a", "2b", "3", "4", "5"])
+    ap.add_argument("--config", default="3", choices=["1", "2a", "2b", "3", "4", "5", "dag"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-plan", dest="plan", action="store_false",
                     help="configurations 1 and 3: skip the repeated-weights (pp_refactor + pp_star) timing")
@@ -564,6 +605,8 @@ def main():
         bench_gemm(args)
     elif args.config == "2b":
         bench_getrf(args)
+    elif args.config == "dag":
+        bench_dag(args)
     else:
         bench_solve(args, int(args.config))
 

@@ -1216,6 +1216,20 @@ std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, st
     if (outside) return "an entry of A falls outside the structure";
     stage("  entries", ts);
     work_counts(n, out.Rptr, out.Sptr, out.parent, out.madds_factor, out.madds_star, out.madds_rhs, out.nnzL);
+    out.madds_star_offd = 0;
+    if (out.nB > 1 && out.nN > 0) {
+        for (i64 c = 0; c < out.nB; c++) {
+            const double rows = (double)(out.Bptr[c] - out.anc_lo[c]);
+            if (rows <= 0) continue;
+            double per = (double)(out.Nptr[out.Bptr[c + 1]] - out.Nptr[out.Bptr[c]]);
+            for (i64 f = out.Fptr[c]; f < out.Fptr[c + 1]; f++) {
+                const double nn = (double)(out.Rptr[f + 1] - out.Rptr[f]), na = (double)(out.Sptr[f + 1] - out.Sptr[f]);
+                per += 2 * nn * (na + (nn - 1) / 2);
+            }
+            out.madds_star_offd += rows * per;
+        }
+        out.madds_star += out.madds_star_offd;
+    }
     return "";
 }
 
@@ -1371,6 +1385,7 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
     }
     if (!opts.amalgamate) {
         err = finish(G, n, colptr, rowval, perm1, R1, out, &par1, cp, nB);
+        out.madds_star_alg += out.madds_star_offd;
         out.seconds_total = now() - t0;
         return err;
     }
@@ -1476,6 +1491,7 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
         }
     stage("amalgamation", ts);
     err = finish(G, n, colptr, rowval, perm2, R2, out, &tree2, cp, nB);
+    out.madds_star_alg += out.madds_star_offd;
     stage("final structure + entries", ts);
     out.seconds_total = now() - t0;
     return err;

@@ -68,6 +68,9 @@ struct Symbolic {
     // work counts (semiring multiply-adds) of the exact structure, before amalgamation, and of the executed one
     double madds_factor_alg = 0, madds_star_alg = 0, madds_rhs_alg = 0, nnzL_alg = 0;
     double madds_factor = 0, madds_star = 0, madds_rhs = 0, nnzL = 0;
+    // the star's pass over coupled components (included in both star counts): for each component, the rows of the
+    // earlier components with a path into it times its per-row solve and its arcs in N
+    double madds_star_offd = 0;
     double seconds_order = 0, seconds_total = 0;
 };
 
