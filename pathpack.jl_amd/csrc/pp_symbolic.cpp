@@ -5,6 +5,7 @@
 #include "pp_symbolic.h"
 
 #include <algorithm>
+#include <climits>
 #include <atomic>
 #include <chrono>
 #include <condition_variable>
@@ -24,8 +25,19 @@ int max_threads();
 }
 
 // A pool of worker threads kept for the life of the process (created at the first parallel call, again in a
-// forked child): starting and joining 15 threads costs about a millisecond, several times per analysis.
+// forked child): starting and joining 15 threads costs about a millisecond, several times per analysis.  A job is
+// published as one atomic word, (generation << 8) | workers, so a worker never pairs one job's worker count with
+// another's generation.  Idle workers spin on that word for about 50 microseconds before they sleep on a condition
+// variable: the analysis runs a dozen short parallel steps with short serial steps between them, and waking a
+// sleeping thread costs tens of microseconds; a longer spin would take the cores from the serial steps and from the
+// thread that launches the GPU work after the analysis.
 namespace {
+inline void cpu_relax() {
+#if defined(__x86_64__)
+    __builtin_ia32_pause();
+#endif
+}
+
 class ThreadPool {
   public:
     explicit ThreadPool(int n) {
@@ -34,7 +46,7 @@ class ThreadPool {
     ~ThreadPool() {
         {
             std::lock_guard<std::mutex> lk(mu_);
-            stop_ = true;
+            stop_.store(true);
         }
         cv_.notify_all();
         for (auto &t : th_) t.join();
@@ -42,45 +54,59 @@ class ThreadPool {
     int size() const { return (int)th_.size() + 1; }
     void run(int n, const std::function<void(int)> &fn) {
         std::lock_guard<std::mutex> one(run_mu_);   // one job at a time
+        job_ = &fn;
+        pending_.store(n - 1, std::memory_order_relaxed);
+        bool wake;
         {
             std::lock_guard<std::mutex> lk(mu_);
-            job_ = &fn;
-            active_ = n;
-            pending_ = n - 1;
-            gen_++;
+            const uint64_t g = (word_.load(std::memory_order_relaxed) >> 8) + 1;
+            word_.store(g << 8 | (uint64_t)n, std::memory_order_release);
+            wake = sleepers_ > 0;
         }
-        cv_.notify_all();
+        if (wake) cv_.notify_all();
         fn(0);
-        std::unique_lock<std::mutex> lk(mu_);
-        done_.wait(lk, [&] { return pending_ == 0; });
-        job_ = nullptr;
+        for (unsigned spins = 0; pending_.load(std::memory_order_acquire) != 0; spins++) {
+            if (spins < 4096) cpu_relax();
+            else std::this_thread::yield();
+        }
     }
 
   private:
     void loop(int i) {
-        unsigned long seen = 0;
+        uint64_t seen = 0;   // the word before the first job: a job published before this thread starts still runs
         while (true) {
-            const std::function<void(int)> *job;
-            {
-                std::unique_lock<std::mutex> lk(mu_);
-                cv_.wait(lk, [&] { return stop_ || gen_ != seen; });
-                if (stop_) return;
-                seen = gen_;
-                if (i >= active_) continue;
-                job = job_;
+            uint64_t w = word_.load(std::memory_order_acquire);
+            if (w == seen) {
+                const double t0 = now_s();
+                for (unsigned spins = 1; (w = word_.load(std::memory_order_acquire)) == seen; spins++) {
+                    if (stop_.load(std::memory_order_relaxed)) return;
+                    cpu_relax();
+                    if ((spins & 255) == 0 && now_s() - t0 > 5e-5) {
+                        std::unique_lock<std::mutex> lk(mu_);
+                        sleepers_++;
+                        cv_.wait(lk, [&] { return stop_.load() || word_.load() != seen; });
+                        sleepers_--;
+                        if (stop_.load()) return;
+                    }
+                }
             }
-            (*job)(i);
-            std::lock_guard<std::mutex> lk(mu_);
-            if (--pending_ == 0) done_.notify_one();
+            seen = w;
+            if (i >= (int)(w & 0xff)) continue;
+            (*job_)(i);
+            pending_.fetch_sub(1, std::memory_order_acq_rel);
         }
+    }
+    static double now_s() {
+        return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
     }
     std::vector<std::thread> th_;
     std::mutex mu_, run_mu_;
-    std::condition_variable cv_, done_;
+    std::condition_variable cv_;
     const std::function<void(int)> *job_ = nullptr;
-    int active_ = 0, pending_ = 0;
-    unsigned long gen_ = 0;
-    bool stop_ = false;
+    std::atomic<uint64_t> word_{0};
+    std::atomic<int> pending_{0};
+    std::atomic<bool> stop_{false};
+    int sleepers_ = 0;
 };
 }  // namespace
 
@@ -128,10 +154,10 @@ struct Adj {
 // Threads for the host analysis: up to 16 (PP_SYMBOLIC_THREADS overrides), one for small graphs.
 int max_threads() {
     int threads = (int)std::min<unsigned>(16, std::max(1u, std::thread::hardware_concurrency()));
-    if (const char *e = std::getenv("PP_SYMBOLIC_THREADS")) threads = std::max(1, std::atoi(e));
+    if (const char *e = std::getenv("PP_SYMBOLIC_THREADS")) threads = std::max(1, std::min(64, std::atoi(e)));
     return threads;
 }
-int analysis_threads(i64 n) { return n < 20000 ? 1 : max_threads(); }
+int analysis_threads(i64 n) { return n < 4096 ? 1 : max_threads(); }
 
 // fn(lo, hi) over [0, count) in contiguous blocks on `threads` threads of the pool (the caller's thread takes the
 // first block)
@@ -144,18 +170,114 @@ template <class Fn> void parallel_for(i64 count, int threads, Fn fn) {
     pool_run(threads, [&](int t) { fn(count * t / threads, count * (t + 1) / threads); });
 }
 
-// The CSC arrays of an n x n pattern: "" when they are well formed.
-std::string check_csc(i64 n, const i64 *colptr, const i64 *rowval) {
+// The CSC arrays of an n x n pattern: "" when they are well formed (the message names the first bad column's fault).
+std::string check_csc(i64 n, const i64 *colptr, const i64 *rowval, int threads = 1) {
     if (n < 0 || n > (i64)0x7fffffff) return "n out of range";
     if (colptr[0] != 0) return "colptr[0] must be 0";
-    for (i64 j = 0; j < n; j++) {
+    for (i64 j = 0; j < n; j++)
         if (colptr[j + 1] < colptr[j]) return "colptr must be nondecreasing";
+    std::atomic<i64> bad(n);   // first column with a bad row list
+    parallel_for(n, threads, [&](i64 a, i64 b) {
+        for (i64 j = a; j < b && j < bad.load(std::memory_order_relaxed); j++)
+            for (i64 p = colptr[j]; p < colptr[j + 1]; p++)
+                if (rowval[p] < 0 || rowval[p] >= n || (p > colptr[j] && rowval[p] <= rowval[p - 1])) {
+                    i64 cur = bad.load();
+                    while (j < cur && !bad.compare_exchange_weak(cur, j)) {}
+                    break;
+                }
+    });
+    if (bad.load() < n) {
+        const i64 j = bad.load();
         for (i64 p = colptr[j]; p < colptr[j + 1]; p++) {
             if (rowval[p] < 0 || rowval[p] >= n) return "row index out of range";
             if (p > colptr[j] && rowval[p] <= rowval[p - 1]) return "row indices must be sorted and unique in each column";
         }
     }
     return "";
+}
+
+// Whether the pattern is symmetric (A[i, j] stored iff A[j, i] stored): each off-diagonal entry's mirror is looked up
+// in its column (binary search; the rows are sorted).  Then the symmetrized pattern is A without its diagonal.
+bool pattern_symmetric(i64 n, const i64 *colptr, const i64 *rowval, int threads) {
+    std::atomic<bool> ok(true);
+    parallel_for(n, threads, [&](i64 a, i64 b) {
+        for (i64 j = a; j < b && ok.load(std::memory_order_relaxed); j++)
+            for (i64 p = colptr[j]; p < colptr[j + 1]; p++) {
+                const i64 i = rowval[p];
+                if (i != j && !std::binary_search(rowval + colptr[i], rowval + colptr[i + 1], j)) {
+                    ok = false;
+                    break;
+                }
+            }
+    });
+    return ok.load();
+}
+
+// The symmetrized pattern of a symmetric A: its columns without the diagonal, in parallel.
+void offdiagonal(i64 n, const i64 *colptr, const i64 *rowval, Adj &G, int threads) {
+    G.n = n;
+    G.xadj.assign(n + 1, 0);
+    parallel_for(n, threads, [&](i64 a, i64 b) {
+        for (i64 j = a; j < b; j++) {
+            i64 c = colptr[j + 1] - colptr[j];
+            if (c > 0 && std::binary_search(rowval + colptr[j], rowval + colptr[j + 1], j)) c--;
+            G.xadj[j + 1] = c;
+        }
+    });
+    for (i64 j = 0; j < n; j++) G.xadj[j + 1] += G.xadj[j];
+    G.adj.resize(G.xadj[n]);
+    parallel_for(n, threads, [&](i64 a, i64 b) {
+        for (i64 j = a; j < b; j++) {
+            i64 w = G.xadj[j];
+            for (i64 p = colptr[j]; p < colptr[j + 1]; p++)
+                if (rowval[p] != j) G.adj[w++] = (i32)rowval[p];
+        }
+    });
+}
+
+// Connected components of G (a symmetric pattern: they are its strongly connected components), numbered in the order
+// of their smallest vertex -- the numbering strong_components gives a symmetric pattern.  A lock-free disjoint-set
+// forest over the edges in parallel, a root always linked under a smaller one, so each set's root ends at its smallest
+// vertex whatever the threads' interleaving.
+i64 connected_components(const Adj &G, std::vector<i32> &comp, int threads) {
+    const i64 n = G.n;
+    std::vector<i32> up(n);
+    parallel_for(n, threads, [&](i64 a, i64 b) {
+        for (i64 v = a; v < b; v++) up[v] = (i32)v;
+    });
+    auto find = [&](i32 x) {
+        while (true) {
+            const i32 p = std::atomic_ref<i32>(up[x]).load(std::memory_order_relaxed);
+            if (p == x) return x;
+            const i32 g = std::atomic_ref<i32>(up[p]).load(std::memory_order_relaxed);
+            if (g != p) {   // path halving
+                i32 e = p;
+                std::atomic_ref<i32>(up[x]).compare_exchange_weak(e, g, std::memory_order_relaxed);
+            }
+            x = p;
+        }
+    };
+    parallel_for(n, threads, [&](i64 a, i64 b) {
+        for (i64 v = a; v < b; v++)
+            for (i64 q = G.xadj[v]; q < G.xadj[v + 1]; q++) {
+                const i32 u = G.adj[q];
+                if (u >= v) continue;   // each edge once
+                while (true) {
+                    i32 ru = find(u), rv = find((i32)v);
+                    if (ru == rv) break;
+                    if (ru < rv) std::swap(ru, rv);   // link the larger root under the smaller
+                    i32 expect = ru;
+                    if (std::atomic_ref<i32>(up[ru]).compare_exchange_strong(expect, rv)) break;
+                }
+            }
+    });
+    comp.assign(n, -1);
+    i32 nc = 0;
+    for (i64 v = 0; v < n; v++) {
+        const i32 r = find((i32)v);
+        comp[v] = r == v ? nc++ : comp[r];
+    }
+    return nc;
 }
 
 // Symmetric pattern of A without the diagonal, neighbours sorted; with `comp`, only the pairs inside one component
@@ -246,141 +368,220 @@ i64 strong_components(i64 n, const i64 *colptr, const i64 *rowval, std::vector<i
     return nc;
 }
 
+// Columns [a, b) of an order whose lower neighbours all lie in [lo, b), filled at depth `level` of a nested
+// dissection (INT_MAX: a whole subtree of it).  Ranges of a deeper level never depend on shallower ones, and ranges of
+// one level are independent of each other.
+struct NDRange {
+    int level;
+    i64 lo, a, b;
+};
+
 // perm (perm[new] = old) with the vertices of each component moved together, the components in increasing number,
 // and the vertices of one component in their order in perm (a stable counting sort).  The fill of each component's
 // own order is unchanged: no pattern entry joins two components.
-void group_by_component(std::vector<i64> &perm, const std::vector<i32> &comp, i64 nc) {
+// With `sub`, each range of positions in it is moved along; a range that the regrouping does not keep in one piece is
+// dropped.
+void group_by_component(std::vector<i64> &perm, const std::vector<i32> &comp, i64 nc,
+                        std::vector<NDRange> *sub = nullptr) {
     const i64 n = (i64)perm.size();
-    std::vector<i64> ptr(nc + 1, 0), out(n);
+    std::vector<i64> ptr(nc + 1, 0), out(n), newpos(sub ? n : 0);
     for (i64 k = 0; k < n; k++) ptr[comp[perm[k]] + 1]++;
     for (i64 c = 0; c < nc; c++) ptr[c + 1] += ptr[c];
-    for (i64 k = 0; k < n; k++) out[ptr[comp[perm[k]]]++] = perm[k];
+    for (i64 k = 0; k < n; k++) {
+        const i64 q = ptr[comp[perm[k]]]++;
+        out[q] = perm[k];
+        if (sub) newpos[k] = q;
+    }
     perm.swap(out);
+    if (sub) {
+        std::vector<NDRange> moved;
+        for (auto &r : *sub)
+            if (r.b > r.lo && newpos[r.b - 1] - newpos[r.lo] == r.b - 1 - r.lo) {
+                const i64 lo = newpos[r.lo];
+                moved.push_back(NDRange{r.level, lo, lo + (r.a - r.lo), lo + (r.b - r.lo)});
+            }
+        sub->swap(moved);
+    }
 }
 
 // ===== nested dissection on level structures =====
 //
-// A work item is a vertex subset (all vertices v with part[v] == id) that owns the output positions
-// [hi - size, hi).  A connected item is split by one level of a breadth-first level structure rooted at a
+// A work item is a vertex subset, held as the subgraph it induces, that owns the output positions [hi - size, hi).
+// Each item carries its own compact adjacency, so a search reads only the item's edges and the workers share no
+// per-vertex arrays.  A connected item is split by one level of a breadth-first level structure rooted at a
 // pseudo-peripheral vertex (George & Liu, "Computer Solution of Large Sparse Positive Definite Systems", 1981):
 // the level with the fewest vertices among those leaving at least 35% of the item on each side.  The separator
 // takes the last positions; the two sides recurse.  Small items are ordered by minimum degree.
 
 struct ND {
+    // A work item: the subgraph induced by its vertices in a local numbering (local vertex v is G's glob[v]; its
+    // neighbours inside the item are adj[xadj[v] .. xadj[v + 1]), in the order of G's lists).  The whole graph is
+    // the first item and is read from G itself.
+    struct Item {
+        std::vector<i64> xadj_s;
+        std::vector<i32> adj_s, glob_s;
+        bool whole = false;
+        i64 m = 0, hi = 0;
+    };
+    // per worker, indexed by local vertex: BFS queue and levels (-1 outside a search), side / component of each
+    // vertex and its index in the item it goes to
+    struct Scratch {
+        std::vector<i32> queue, level, side, cid;
+        std::vector<i64> lptr, lptr2;
+        explicit Scratch(i64 n) : queue(n + 1), level(n, -1), side(n), cid(n) {}   // queue: one slot past the end
+    };
     const Adj &G;
     int leaf;
-    std::vector<i32> part;    // item id of every vertex (items own disjoint vertex sets)
-    std::vector<i32> level;   // BFS level, -1 outside a BFS (per vertex, so items can run concurrently)
     std::vector<i64> order;   // order[k] = vertex eliminated k-th
-    std::atomic<i32> next_id{1};
-    struct Item { std::vector<i32> V; i64 hi; };
+    // Where each position was ordered: columns [a, b) of `order`, whose lower neighbours all lie in [lo, b), were
+    // filled at depth `level` of the dissection (one entry per item split at the top, its separator), or hold a whole
+    // subtree of it (level INT_MAX).  Entries of a deeper level never depend on shallower ones.
+    using Range = NDRange;
+    std::vector<Range> ranges;
 
-    ND(const Adj &g, int leaf_) : G(g), leaf(std::max(2, std::min(leaf_, 64))), part(g.n, 0), level(g.n, -1),
-                                   order(g.n, -1) {}
+    ND(const Adj &g, int leaf_) : G(g), leaf(std::max(2, std::min(leaf_, 64))), order(g.n, -1) {}
 
-    // BFS inside item id from root; returns the number of levels; fills queue[0..cnt) and level[]
-    int bfs(std::vector<i32> &queue, i32 id, i32 root, i64 &cnt, std::vector<i64> &lptr) {
+    const i64 *X(const Item &it) const { return it.whole ? G.xadj.data() : it.xadj_s.data(); }
+    const i32 *A(const Item &it) const { return it.whole ? G.adj.data() : it.adj_s.data(); }
+    i64 glob(const Item &it, i32 v) const { return it.whole ? (i64)v : (i64)it.glob_s[v]; }
+
+    // BFS inside the item from root; returns the number of levels; fills queue[0..cnt), level[] and the level
+    // pointers (a BFS visits the levels in order)
+    int bfs(const Item &it, Scratch &s, i32 root, i64 &cnt, std::vector<i64> &lptr) const {
+        const i64 *xa = X(it);
+        const i32 *ad = A(it);
+        i32 *queue = s.queue.data(), *level = s.level.data();
         lptr.clear();
+        lptr.push_back(0);
         cnt = 0;
         queue[cnt++] = root;
         level[root] = 0;
         i64 head = 0;
-        int nlev;
-        lptr.push_back(0);
+        i32 cur = 0;
         while (head < cnt) {
-            i32 v = queue[head++];
-            for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) {
-                i32 u = G.adj[p];
-                if (part[u] != id || level[u] >= 0) continue;
-                level[u] = level[v] + 1;
-                queue[cnt++] = u;
+            const i32 v = queue[head];
+            if (level[v] != cur) {
+                lptr.push_back(head);
+                cur = level[v];
+            }
+            head++;
+            const i32 lv = cur + 1;
+            // branch-free: every neighbour is written at the queue's end, and the end moves past it only when it was
+            // not visited yet (a neighbour list has no repeats)
+            for (i64 p = xa[v]; p < xa[v + 1]; p++) {
+                const i32 u = ad[p];
+                const i32 lu = level[u];
+                const bool fresh = lu < 0;
+                queue[cnt] = u;
+                level[u] = fresh ? lv : lu;
+                cnt += fresh;
             }
         }
-        // level pointers (BFS visits levels in order)
-        for (i64 k = 1; k < cnt; k++)
-            if (level[queue[k]] != level[queue[k - 1]]) lptr.push_back(k);
         lptr.push_back(cnt);
-        nlev = (int)lptr.size() - 1;
-        return nlev;
+        return (int)lptr.size() - 1;
     }
 
-    void clear_levels(const std::vector<i32> &queue, i64 cnt) {
-        for (i64 k = 0; k < cnt; k++) level[queue[k]] = -1;
+    static void clear_levels(Scratch &s, i64 cnt) {
+        for (i64 k = 0; k < cnt; k++) s.level[s.queue[k]] = -1;
     }
 
-    i64 degree_in(i32 v, i32 id) const {
-        i64 d = 0;
-        for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) d += part[G.adj[p]] == id;
-        return d;
-    }
-
-    // minimum degree on a small item (at most 64 vertices): explicit elimination graph in bit masks
-    void md_leaf(const std::vector<i32> &V, i64 lo) {
-        const int m = (int)V.size();
-        std::vector<uint64_t> mask(m, 0);
-        // local index lookup through level[] (free at this point)
-        for (int a = 0; a < m; a++) level[V[a]] = a;
-        i32 id = part[V[0]];
-        for (int a = 0; a < m; a++)
-            for (i64 p = G.xadj[V[a]]; p < G.xadj[V[a] + 1]; p++) {
-                i32 u = G.adj[p];
-                if (part[u] == id) mask[a] |= uint64_t(1) << level[u];
-            }
-        for (int a = 0; a < m; a++) level[V[a]] = -1;
+    // minimum degree on a small item (at most 64 vertices): explicit elimination graph in bit masks; ties go to the
+    // vertex listed first
+    void md_leaf(const Item &it, i64 lo) {
+        const int m = (int)it.m;
+        const i64 *xa = X(it);
+        const i32 *ad = A(it);
+        uint64_t mask[64];
+        for (int a = 0; a < m; a++) {
+            mask[a] = 0;
+            for (i64 p = xa[a]; p < xa[a + 1]; p++) mask[a] |= uint64_t(1) << ad[p];
+        }
         uint64_t alive = m == 64 ? ~uint64_t(0) : ((uint64_t(1) << m) - 1);
         for (int k = 0; k < m; k++) {
             int best = -1, bd = 1 << 30;
-            for (int a = 0; a < m; a++)
-                if (alive >> a & 1) {
-                    int d = __builtin_popcountll(mask[a] & alive);
-                    if (d < bd) { bd = d; best = a; }
-                }
-            uint64_t nb = mask[best] & alive & ~(uint64_t(1) << best);
-            for (int a = 0; a < m; a++)
-                if (nb >> a & 1) mask[a] |= nb & ~(uint64_t(1) << a);
+            for (uint64_t rest = alive; rest; rest &= rest - 1) {   // alive vertices in increasing index
+                const int a = __builtin_ctzll(rest);
+                const int d = __builtin_popcountll(mask[a] & alive);
+                if (d < bd) { bd = d; best = a; }
+            }
+            const uint64_t nb = mask[best] & alive & ~(uint64_t(1) << best);
+            for (uint64_t rest = nb; rest; rest &= rest - 1) {
+                const int a = __builtin_ctzll(rest);
+                mask[a] |= nb & ~(uint64_t(1) << a);
+            }
             alive &= ~(uint64_t(1) << best);
-            order[lo + k] = V[best];
+            order[lo + k] = glob(it, best);
         }
     }
 
-    // One item: split it (components, or sides + separator) or order it (leaf); new items go to `out`.
-    void process(Item &it, std::vector<i32> &queue, std::vector<i64> &lptr, std::vector<Item> &out) {
-        const i64 sz = (i64)it.V.size();
-        if (sz == 0) return;
-        const i32 id = next_id.fetch_add(1);
-        for (i32 v : it.V) part[v] = id;
+    // the item of the vertices `list` (in that order) of `it`: those with side[v] == code, local index cid[v]
+    Item extract(const Item &it, const Scratch &s, const std::vector<i32> &list, i32 code, i64 hi) const {
+        const i64 *xa = X(it);
+        const i32 *ad = A(it);
+        Item c;
+        c.m = (i64)list.size();
+        c.hi = hi;
+        c.glob_s.resize(c.m);
+        c.xadj_s.resize(c.m + 1);
+        i64 deg = 0;
+        for (i32 v : list) deg += xa[v + 1] - xa[v];
+        c.adj_s.resize(deg);
+        i64 w = 0;
+        c.xadj_s[0] = 0;
+        for (i64 k = 0; k < c.m; k++) {
+            const i32 v = list[k];
+            c.glob_s[k] = (i32)glob(it, v);
+            for (i64 p = xa[v]; p < xa[v + 1]; p++) {
+                const i32 u = ad[p];
+                if (s.side[u] == code) c.adj_s[w++] = s.cid[u];
+            }
+            c.xadj_s[k + 1] = w;
+        }
+        c.adj_s.resize(w);
+        return c;
+    }
+
+    // One item: split it (components, or sides + separator) or order it (leaf); new items go to `out`.  Returns
+    // the positions of `order` filled by this item itself (its separator, or all of it).
+    std::pair<i64, i64> process(const Item &it, Scratch &s, std::vector<Item> &out) {
+        const i64 sz = it.m;
+        if (sz == 0) return {it.hi, it.hi};
         const i64 lo = it.hi - sz;
         if (sz <= leaf) {
-            md_leaf(it.V, lo);
-            return;
+            md_leaf(it, lo);
+            return {lo, it.hi};
         }
-        // connected components of the item
-        // the first breadth-first search starts at the item's first vertex; the pseudo-peripheral search below moves
-        // the root to the far end
+        const i64 *xa = X(it);
+        const i32 *ad = A(it);
+        std::vector<i64> &lptr = s.lptr;
+        // connected components of the item; the first breadth-first search starts at the item's first vertex and
+        // the pseudo-peripheral search below moves the root to the far end
         i64 cnt;
-        i32 root = it.V[0];
-        int nlev = bfs(queue, id, root, cnt, lptr);
+        i32 root = 0;
+        int nlev = bfs(it, s, root, cnt, lptr);
         if (cnt < sz) {
-            // disconnected: every component becomes an item of its own
-            clear_levels(queue, cnt);
+            // disconnected: every component becomes an item of its own, the first one found taking the last
+            // positions; a component lists its vertices in the order its search visits them
             std::vector<std::vector<i32>> comps;
-            std::vector<i64> lp2;
-            for (i32 v : it.V) {
-                if (part[v] != id) continue;
+            comps.emplace_back(s.queue.begin(), s.queue.begin() + cnt);
+            for (i32 v = 0; v < (i32)sz; v++) {
+                if (s.level[v] >= 0) continue;
                 i64 c2;
-                bfs(queue, id, v, c2, lp2);
-                comps.emplace_back(queue.begin(), queue.begin() + c2);
-                clear_levels(queue, c2);
-                for (i32 u : comps.back()) part[u] = -id;
+                bfs(it, s, v, c2, s.lptr2);
+                comps.emplace_back(s.queue.begin(), s.queue.begin() + c2);
             }
+            for (i32 v = 0; v < (i32)sz; v++) s.level[v] = -1;
+            for (i32 c = 0; c < (i32)comps.size(); c++)
+                for (i64 k = 0; k < (i64)comps[c].size(); k++) {
+                    s.side[comps[c][k]] = c;
+                    s.cid[comps[c][k]] = (i32)k;
+                }
             i64 hi = it.hi;
-            for (auto &c : comps) {
-                for (i32 u : c) part[u] = id;
-                i64 csz = (i64)c.size();
-                out.push_back({std::move(c), hi});
-                hi -= csz;
+            for (i32 c = 0; c < (i32)comps.size(); c++) {
+                out.push_back(extract(it, s, comps[c], c, hi));
+                hi -= (i64)comps[c].size();
             }
-            return;
+            return {it.hi, it.hi};
         }
         // pseudo-peripheral root: restart from a vertex of minimum degree in the last level while the level
         // structure gets deeper; a structure as deep as the current one is kept as it is
@@ -388,133 +589,151 @@ struct ND {
             i32 best = -1;
             i64 bd = 1LL << 60;
             for (i64 k = lptr[nlev - 1]; k < lptr[nlev]; k++) {
-                i32 v = queue[k];
-                i64 d = degree_in(v, id);
+                const i32 v = s.queue[k];
+                const i64 d = xa[v + 1] - xa[v];
                 if (d < bd) { bd = d; best = v; }
             }
-            clear_levels(queue, cnt);
-            std::vector<i64> lptr2;
+            clear_levels(s, cnt);
             i64 cnt2;
-            int nlev2 = bfs(queue, id, best, cnt2, lptr2);
+            const int nlev2 = bfs(it, s, best, cnt2, s.lptr2);
             if (nlev2 >= nlev) {
                 const bool deeper = nlev2 > nlev;
                 nlev = nlev2;
-                lptr = lptr2;
+                lptr.swap(s.lptr2);
                 cnt = cnt2;
                 root = best;
                 if (!deeper) break;
             } else {
-                clear_levels(queue, cnt2);
-                nlev = bfs(queue, id, root, cnt, lptr);
+                clear_levels(s, cnt2);
+                nlev = bfs(it, s, root, cnt, lptr);
                 break;
             }
         }
         if (nlev < 3) {
             // too shallow to dissect: minimum degree would be too slow on a large item; natural order
-            for (i64 k = 0; k < cnt; k++) order[lo + k] = queue[k];
-            clear_levels(queue, cnt);
-            return;
+            for (i64 k = 0; k < cnt; k++) order[lo + k] = glob(it, s.queue[k]);
+            clear_levels(s, cnt);
+            return {lo, it.hi};
         }
         // the separator level
         int sl = -1;
         i64 ssz = 1LL << 60, sbal = 1LL << 60;
         const i64 minside = (i64)(0.35 * (double)sz);
         for (int k = 1; k + 1 < nlev; k++) {
-            i64 a = lptr[k], s = lptr[k + 1] - lptr[k], b = sz - a - s;
+            i64 a = lptr[k], sn = lptr[k + 1] - lptr[k], b = sz - a - sn;
             if (a < minside || b < minside) continue;
             i64 bal = a > b ? a - b : b - a;
-            if (s < ssz || (s == ssz && bal < sbal)) { ssz = s; sbal = bal; sl = k; }
+            if (sn < ssz || (sn == ssz && bal < sbal)) { ssz = sn; sbal = bal; sl = k; }
         }
         if (sl < 0) {
             for (int k = 1; k + 1 < nlev; k++)
                 if (lptr[k + 1] * 2 >= sz) { sl = k; break; }
             if (sl < 0) sl = nlev / 2;
         }
-        // sides: A = levels < sl, B = levels > sl, S = level sl; then drop separator vertices that touch only
-        // one side (a minimal separator)
-        const i32 idA = next_id.fetch_add(3), idB = idA + 1, idS = idA + 2;
+        // sides: A (0) = levels < sl, B (1) = levels > sl, S (2) = level sl; then separator vertices that touch
+        // only one side move to it, one after another (a minimal separator)
         for (i64 k = 0; k < cnt; k++) {
-            i32 v = queue[k];
-            part[v] = level[v] < sl ? idA : (level[v] > sl ? idB : idS);
+            const i32 v = s.queue[k];
+            s.side[v] = s.level[v] < sl ? 0 : (s.level[v] > sl ? 1 : 2);
         }
-        clear_levels(queue, cnt);
-        std::vector<i32> S;
-        for (i64 k = lptr[sl]; k < lptr[sl + 1]; k++) S.push_back(queue[k]);
+        clear_levels(s, cnt);
         std::vector<i32> keep;
-        for (i32 v : S) {
+        for (i64 k = lptr[sl]; k < lptr[sl + 1]; k++) {
+            const i32 v = s.queue[k];
             bool ta = false, tb = false;
-            for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) {
-                i32 u = G.adj[p];
-                ta |= part[u] == idA;
-                tb |= part[u] == idB;
+            for (i64 p = xa[v]; p < xa[v + 1]; p++) {
+                const i32 sd = s.side[ad[p]];
+                ta |= sd == 0;
+                tb |= sd == 1;
             }
-            if (!tb) part[v] = idA;
-            else if (!ta) part[v] = idB;
+            if (!tb) s.side[v] = 0;
+            else if (!ta) s.side[v] = 1;
             else keep.push_back(v);
         }
-        std::vector<i32> A, B;
-        for (i32 v : it.V) {
-            if (part[v] == idA) A.push_back(v);
-            else if (part[v] == idB) B.push_back(v);
+        std::vector<i32> Av, Bv;
+        for (i32 v = 0; v < (i32)sz; v++) {
+            if (s.side[v] == 0) {
+                s.cid[v] = (i32)Av.size();
+                Av.push_back(v);
+            } else if (s.side[v] == 1) {
+                s.cid[v] = (i32)Bv.size();
+                Bv.push_back(v);
+            }
         }
         const i64 ns = (i64)keep.size();
-        for (i64 k = 0; k < ns; k++) order[it.hi - ns + k] = keep[k];
-        const i64 na = (i64)A.size();
-        out.push_back({std::move(B), it.hi - ns});
-        out.push_back({std::move(A), lo + na});
+        for (i64 k = 0; k < ns; k++) order[it.hi - ns + k] = glob(it, keep[k]);
+        const i64 na = (i64)Av.size();
+        out.push_back(extract(it, s, Bv, 1, it.hi - ns));
+        out.push_back(extract(it, s, Av, 0, lo + na));
+        return {it.hi - ns, it.hi};
     }
 
-    // Items run on a pool of threads; a worker keeps splitting small items itself (depth first) and shares the
-    // large ones.
+    // The top of the dissection runs level by level, the large items of one level in parallel (an item is large when
+    // it holds more than a quarter of a thread's share of the vertices), until none is large; then the threads take
+    // the remaining items largest first and order each one's whole subtree themselves (depth first).  Every item writes its own positions of `order`, so the result does not
+    // depend on the threads.
     void run(int nthreads) {
-        std::vector<Item> stack;
+        std::vector<Item> level;
         {
             Item all;
-            all.V.resize(G.n);
-            std::iota(all.V.begin(), all.V.end(), 0);
+            all.whole = true;
+            all.m = G.n;
             all.hi = G.n;
-            stack.push_back(std::move(all));
+            level.push_back(std::move(all));
         }
-        std::mutex mu;
-        std::condition_variable cv;
-        int active = 0;
-        const i64 share = 2048;   // items at least this large go back to the shared stack
-        auto work = [&]() {
-            std::vector<i32> queue(G.n);
-            std::vector<i64> lptr;
-            std::vector<Item> out, local;
-            while (true) {
-                Item it;
-                {
-                    std::unique_lock<std::mutex> lk(mu);
-                    cv.wait(lk, [&] { return !stack.empty() || active == 0; });
-                    if (stack.empty()) return;
-                    it = std::move(stack.back());
-                    stack.pop_back();
-                    active++;
+        const i64 big = std::max<i64>(2048, G.n / (4 * (i64)std::max(1, nthreads)));
+        std::vector<Scratch *> scratch(std::max(1, nthreads), nullptr);
+        auto scr = [&](int t) -> Scratch & {
+            if (!scratch[t]) scratch[t] = new Scratch(G.n);
+            return *scratch[t];
+        };
+        double tl = now();
+        for (int depth = 0; nthreads > 1; depth++) {
+            bool any = false;
+            for (auto &it : level) any |= it.m >= big;
+            if (!any) break;
+            std::vector<std::vector<Item>> outs(level.size());
+            std::vector<Range> own(level.size(), Range{depth, 0, 0, 0});
+            std::atomic<size_t> next(0);
+            pool_run((int)std::min<size_t>(nthreads, level.size()), [&](int t) {
+                for (size_t k; (k = next.fetch_add(1)) < level.size();) {
+                    if (level[k].m >= big) {
+                        const auto ab = process(level[k], scr(t), outs[k]);
+                        own[k] = Range{depth, level[k].hi - level[k].m, ab.first, ab.second};
+                    } else {
+                        outs[k].push_back(std::move(level[k]));
+                    }
                 }
+            });
+            for (auto &r : own)
+                if (r.b > r.a) ranges.push_back(r);
+            stage("      dissection depth", tl);
+            std::vector<Item> nl;
+            for (auto &o : outs)
+                for (auto &it : o) nl.push_back(std::move(it));
+            level.swap(nl);
+        }
+        std::sort(level.begin(), level.end(), [](const Item &a, const Item &b) { return a.m > b.m; });
+        for (auto &it : level)
+            if (it.m > 0) ranges.push_back(Range{INT_MAX, it.hi - it.m, it.hi - it.m, it.hi});
+        std::atomic<size_t> next(0);
+        pool_run(std::max(1, (int)std::min<size_t>(nthreads, level.size())), [&](int t) {
+            Scratch &s = scr(t);
+            std::vector<Item> out, local;
+            for (size_t k; (k = next.fetch_add(1)) < level.size();) {
                 local.clear();
-                local.push_back(std::move(it));
-                std::vector<Item> shared;
+                local.push_back(std::move(level[k]));
                 while (!local.empty()) {
                     Item cur = std::move(local.back());
                     local.pop_back();
                     out.clear();
-                    process(cur, queue, lptr, out);
-                    for (auto &o : out) {
-                        if ((i64)o.V.size() >= share && nthreads > 1) shared.push_back(std::move(o));
-                        else local.push_back(std::move(o));
-                    }
+                    process(cur, s, out);
+                    for (auto &o : out) local.push_back(std::move(o));
                 }
-                {
-                    std::lock_guard<std::mutex> lk(mu);
-                    for (auto &o : shared) stack.push_back(std::move(o));
-                    active--;
-                }
-                cv.notify_all();
             }
-        };
-        pool_run(nthreads, [&](int) { work(); });
+        });
+        stage("      dissection subtrees", tl);
+        for (Scratch *p : scratch) delete p;
     }
 };
 
@@ -706,64 +925,116 @@ std::vector<i64> amd_order(const Adj &G) {
 }
 
 // ===== elimination tree and postorder (Liu 1986, path compression) =====
+//
+// The columns of a nested-dissection item (a range of positions holding a whole subtree of the dissection) have
+// their lower neighbours inside the item: the vertices ordered before it lie in other items, which only the later
+// separators touch.  So Liu's algorithm runs on the whole subtrees at the bottom in parallel, then on the separators
+// of the items above them, one depth of the dissection at a time (deepest first, the items of one depth in
+// parallel); each item writes only its own nodes, and every column still sees the columns before it in its item, so
+// the tree is the one a single pass over all columns gives.
 
 // post_perm: a postorder of the elimination tree of perm (the children of a node in increasing order);
-// post_parent: the elimination tree in the postorder's labels.
+// post_parent: the elimination tree in the postorder's labels.  sub: the nested dissection's ranges of perm, or null.
 void etree_postorder(const Adj &G, const std::vector<i64> &perm, std::vector<i64> &post_perm,
-                     std::vector<i64> &post_parent) {
+                     std::vector<i64> &post_parent, const std::vector<NDRange> *sub = nullptr, int threads = 1) {
     const i64 n = G.n;
     double ts = now();
     std::vector<i64> invp(n);
-    for (i64 k = 0; k < n; k++) invp[perm[k]] = k;
+    parallel_for(n, threads, [&](i64 a, i64 b) {
+        for (i64 k = a; k < b; k++) invp[perm[k]] = k;
+    });
     std::vector<i64> parent(n, -1), anc(n, -1);
-    for (i64 j = 0; j < n; j++) {
-        i64 v = perm[j];
-        for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) {
-            i64 i = invp[G.adj[p]];
-            if (i >= j) continue;
-            i64 r = i;
-            while (anc[r] != -1 && anc[r] != j) {
-                i64 t = anc[r];
-                anc[r] = j;
-                r = t;
-            }
-            if (anc[r] == -1) {
-                anc[r] = j;
-                parent[r] = j;
+    // Liu's algorithm on the columns [j0, j1); false when a lower neighbour lies below lo
+    auto cols = [&](i64 j0, i64 j1, i64 lo) {
+        for (i64 j = j0; j < j1; j++) {
+            const i64 v = perm[j];
+            for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) {
+                const i64 i = invp[G.adj[p]];
+                if (i >= j) continue;
+                if (i < lo) return false;
+                i64 r = i;
+                while (anc[r] != -1 && anc[r] != j) {
+                    const i64 t = anc[r];
+                    anc[r] = j;
+                    r = t;
+                }
+                if (anc[r] == -1) {
+                    anc[r] = j;
+                    parent[r] = j;
+                }
             }
         }
-    }
-    stage("    etree", ts);
-    // children lists in increasing order, then an iterative DFS from the roots
-    std::vector<i64> head(n, -1), next(n, -1);
-    for (i64 j = n - 1; j >= 0; j--)
-        if (parent[j] >= 0) {
-            next[j] = head[parent[j]];
-            head[parent[j]] = j;
+        return true;
+    };
+    bool done = false;
+    if (sub && threads > 1 && sub->size() > 1) {
+        // the ranges must cover every column once
+        std::vector<NDRange> rs(*sub);
+        std::sort(rs.begin(), rs.end(), [](const NDRange &x, const NDRange &y) { return x.a < y.a; });
+        bool ok = true;
+        i64 at = 0;
+        for (auto &r : rs) {
+            ok &= r.a == at && r.b > r.a && r.lo >= 0 && r.lo <= r.a;
+            at = r.b;
         }
-    post_perm.clear();
-    post_perm.reserve(n);
-    std::vector<i64> post(n);   // postorder label of each label of perm
-    std::vector<i64> stack;
-    for (i64 r = 0; r < n; r++) {
-        if (parent[r] != -1) continue;
-        stack.push_back(r);
-        while (!stack.empty()) {
-            i64 v = stack.back();
-            if (head[v] >= 0) {
-                i64 c = head[v];
-                head[v] = next[c];
-                stack.push_back(c);
+        ok &= at == n;
+        if (ok) {
+            // deepest level first; the ranges of one level in parallel
+            std::stable_sort(rs.begin(), rs.end(), [](const NDRange &x, const NDRange &y) { return x.level > y.level; });
+            std::atomic<bool> bad(false);
+            stage("      etree setup", ts);
+            for (size_t g0 = 0; g0 < rs.size() && !bad;) {
+                size_t g1 = g0;
+                while (g1 < rs.size() && rs[g1].level == rs[g0].level) g1++;
+                std::atomic<size_t> next(g0);
+                pool_run((int)std::min<size_t>(threads, g1 - g0), [&](int) {
+                    for (size_t k; (k = next.fetch_add(1)) < g1;)
+                        if (!cols(rs[k].a, rs[k].b, rs[k].lo)) bad = true;
+                });
+                stage(rs[g0].level == INT_MAX ? "      etree subtrees" : "      etree depth", ts);
+                g0 = g1;
+            }
+            if (!bad) {
+                done = true;
             } else {
-                stack.pop_back();
-                post[v] = (i64)post_perm.size();
-                post_perm.push_back(perm[v]);
+                std::fill(parent.begin(), parent.end(), -1);
+                std::fill(anc.begin(), anc.end(), -1);
             }
         }
     }
-    post_parent.assign(n, -1);
+    if (!done) cols(0, n, 0);
+    stage(done ? "    etree (dissection ranges)" : "    etree", ts);
+    // postorder with the children of a node in increasing order, roots in increasing order: the subtree of j takes
+    // size[j] consecutive labels starting after its earlier siblings' subtrees, j last
+    std::vector<i64> &size = anc, &post = invp;   // reused
+    std::fill(size.begin(), size.end(), 1);
     for (i64 j = 0; j < n; j++)
-        if (parent[j] >= 0) post_parent[post[j]] = post[parent[j]];
+        if (parent[j] >= 0) size[parent[j]] += size[j];
+    stage("    postorder sizes", ts);
+    std::vector<i64> start(n), acc(n, 0);
+    i64 roots = 0;
+    for (i64 j = 0; j < n; j++) {   // offset of j among its siblings
+        if (parent[j] >= 0) {
+            start[j] = acc[parent[j]];
+            acc[parent[j]] += size[j];
+        } else {
+            start[j] = roots;
+            roots += size[j];
+        }
+    }
+    for (i64 j = n - 1; j >= 0; j--) {
+        if (parent[j] >= 0) start[j] += start[parent[j]];
+        post[j] = start[j] + size[j] - 1;
+    }
+    stage("    postorder starts", ts);
+    post_perm.resize(n);
+    post_parent.resize(n);
+    parallel_for(n, threads, [&](i64 a, i64 b) {
+        for (i64 j = a; j < b; j++) {
+            post_perm[post[j]] = perm[j];
+            post_parent[post[j]] = parent[j] >= 0 ? post[parent[j]] : -1;
+        }
+    });
     stage("    postorder", ts);
 }
 
@@ -772,48 +1043,106 @@ void etree_postorder(const Adj &G, const std::vector<i64> &perm, std::vector<i64
 //
 // The labels are a postorder of the elimination tree.  L[i, j] != 0 iff j lies in the row subtree T_i, whose leaves
 // are among the j < i with A[i, j] != 0.  Every node counts +1; for each row subtree, each leaf j (a neighbour of i
-// that is not a descendant of the previous leaf) adds +1 at j and -1 at the least common ancestor of j and the
-// previous leaf (found with a disjoint-set forest over the nodes already visited); each leaf of the tree counts 1
-// and each non-root node subtracts 1 from its parent.  The column count of j (with the diagonal) is then the sum of
-// these weights over the subtree of j.  O(nnz(A) a(n)).
-void column_counts(const Adj &G, const std::vector<i64> &perm, const std::vector<i64> &parent, std::vector<i64> &cc) {
+// that is not a descendant of the previous leaf, visiting the neighbours in increasing order) adds +1 at j and -1 at
+// the least common ancestor of j and the previous leaf; each leaf of the tree counts 1 and each non-root node
+// subtracts 1 from its parent.  The column count of j (with the diagonal) is then the sum of these weights over the
+// subtree of j.
+//
+// The rows are independent, so they run in parallel.  In a postorder the least common ancestor of a < b is the first
+// ancestor of a labelled b or more; it is found by climbing with jump pointers (Myers, "An applicative random-access
+// stack", IPL 17, 1983: each node keeps its parent and one longer jump, so a monotone search along the path to the
+// root takes O(log depth) steps).
+void column_counts(const Adj &G, const std::vector<i64> &perm, const std::vector<i64> &parent, std::vector<i64> &cc,
+                   int threads = 1) {
     const i64 n = G.n;
     double ts = now();
     std::vector<i64> invp(n);
-    for (i64 k = 0; k < n; k++) invp[perm[k]] = k;
-    // first descendant of every node (labels are a postorder, so a subtree is the range [first[j], j])
-    std::vector<i64> first(n, -1);
-    for (i64 k = 0; k < n; k++)
-        for (i64 j = k; j != -1 && first[j] == -1; j = parent[j]) first[j] = k;
-    std::vector<i64> delta(n), maxfirst(n, -1), prevleaf(n, -1), set(n);
-    for (i64 j = 0; j < n; j++) {
-        set[j] = j;
-        delta[j] = first[j] == j ? 1 : 0;   // leaves of the elimination tree
+    parallel_for(n, threads, [&](i64 a, i64 b) {
+        for (i64 k = a; k < b; k++) invp[perm[k]] = k;
+    });
+    stage("      cc invp", ts);
+    // first descendant of every node (a subtree is the range [first[j], j]), depth and jump pointer
+    std::vector<i64> first(n), depth(n), jump(n);
+    for (i64 j = 0; j < n; j++) first[j] = j;
+    for (i64 j = 0; j < n; j++)
+        if (parent[j] >= 0) first[parent[j]] = std::min(first[parent[j]], first[j]);
+    for (i64 j = n - 1; j >= 0; j--) {
+        const i64 p = parent[j];
+        if (p < 0) {
+            depth[j] = 0;
+            jump[j] = j;
+            continue;
+        }
+        depth[j] = depth[p] + 1;
+        const i64 jp = jump[p];
+        jump[j] = (jp != p && depth[p] - depth[jp] == depth[jp] - depth[jump[jp]]) ? jump[jp] : p;
     }
+    stage("      cc jump", ts);
+    // the first ancestor of a (a < b) labelled b or more
+    auto lca = [&](i64 a, i64 b) {
+        while (true) {
+            const i64 s = jump[a];
+            if (s != a && s < b) {
+                a = s;
+                continue;
+            }
+            const i64 p = parent[a];
+            if (p < 0 || p >= b) return p;
+            a = p;
+        }
+    };
+    std::vector<i64> delta(n, 0);
     for (i64 j = 0; j < n; j++) {
-        if (parent[j] != -1) delta[parent[j]]--;
-        const i64 v = perm[j];
-        for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) {
-            const i64 i = invp[G.adj[p]];
-            if (i <= j || first[j] <= maxfirst[i]) continue;   // j is no new leaf of the row subtree of i
-            maxfirst[i] = first[j];
-            const i64 jprev = prevleaf[i];
-            prevleaf[i] = j;
-            delta[j]++;
-            if (jprev != -1) {
-                // least common ancestor of jprev and j: the representative of jprev's set
-                i64 q = jprev;
-                while (set[q] != q) q = set[q];
-                for (i64 s = jprev; s != q;) {
-                    const i64 t = set[s];
-                    set[s] = q;
-                    s = t;
+        if (first[j] == j) delta[j]++;   // leaves of the elimination tree
+        if (parent[j] >= 0) delta[parent[j]]--;
+    }
+    stage("      cc delta", ts);
+    // rows in blocks on the threads, each adding into its own copy of the weights (or, for a very large tree, into the
+    // shared ones with atomic adds)
+    const int T = (int)std::max<i64>(1, std::min<i64>(threads, n / 1024));
+    const bool own = (double)n * T <= (double)(1 << 26);
+    std::vector<std::vector<i32>> part(own && T > 1 ? T : 0);
+    pool_run(T, [&](int t) {
+        i32 *mine = nullptr;
+        if (!part.empty()) {
+            part[t].assign(n, 0);
+            mine = part[t].data();
+        }
+        auto add = [&](i64 k, i64 v) {
+            if (T == 1) delta[k] += v;
+            else if (mine) mine[k] += (i32)v;
+            else std::atomic_ref<i64>(delta[k]).fetch_add(v, std::memory_order_relaxed);
+        };
+        std::vector<i64> nb;
+        for (i64 i = n * t / T; i < n * (t + 1) / T; i++) {
+            nb.clear();
+            const i64 v = perm[i];
+            for (i64 p = G.xadj[v]; p < G.xadj[v + 1]; p++) {
+                const i64 j = invp[G.adj[p]];
+                if (j < i) nb.push_back(j);
+            }
+            std::sort(nb.begin(), nb.end());
+            i64 maxfirst = -1, jprev = -1;
+            for (i64 j : nb) {
+                if (first[j] <= maxfirst) continue;   // j is no new leaf of the row subtree of i
+                maxfirst = first[j];
+                add(j, 1);
+                if (jprev >= 0) {
+                    const i64 q = lca(jprev, j);   // exists: jprev and j both descend from i
+                    if (q >= 0) add(q, -1);
                 }
-                delta[q]--;
+                jprev = j;
             }
         }
-        if (parent[j] != -1) set[j] = parent[j];
-    }
+    });
+    if (!part.empty())
+        parallel_for(n, threads, [&](i64 a, i64 b) {
+            for (int t = 0; t < T; t++) {
+                const i32 *mine = part[t].data();
+                for (i64 k = a; k < b; k++) delta[k] += mine[k];
+            }
+        });
+    stage("      cc rows", ts);
     cc = delta;
     for (i64 j = 0; j < n; j++)
         if (parent[j] != -1) cc[parent[j]] += cc[j];
@@ -916,7 +1245,8 @@ std::string supernodal_tree(const Adj &G, const std::vector<i64> &perm, const st
     // per front: (buffer, offset, length) of its separator
     std::vector<int32_t> fbuf(nf, -1);
     std::vector<i64> foff(nf, 0), flen(nf, 0);
-    std::vector<std::vector<i32>> bufs(threads + 1);
+    std::vector<std::vector<i32>> bufs(threads), topsep(nf), marks(threads);
+    constexpr int32_t TOP = -2;   // fbuf of a front above the cut: its separator is topsep[f]
     std::atomic<bool> bad(false);
     auto front = [&](i64 f, std::vector<i32> &out, int bid, std::vector<i32> &mark, std::vector<i32> &buf) {
         const i64 r0 = Rptr[f], r1 = Rptr[f + 1];
@@ -932,7 +1262,7 @@ std::string supernodal_tree(const Adj &G, const std::vector<i64> &perm, const st
             }
         }
         for (i64 c = chead[f]; c >= 0; c = cnext[c]) {
-            const i32 *sc = bufs[fbuf[c]].data() + foff[c];
+            const i32 *sc = fbuf[c] == TOP ? topsep[c].data() : bufs[fbuf[c]].data() + foff[c];
             for (i64 k = 0; k < flen[c]; k++) {
                 const i64 u = sc[k];
                 if (u < r0) bad = true;
@@ -944,13 +1274,15 @@ std::string supernodal_tree(const Adj &G, const std::vector<i64> &perm, const st
         }
         std::sort(buf.begin(), buf.end());
         fbuf[f] = bid;
-        foff[f] = (i64)out.size();
+        foff[f] = bid == TOP ? 0 : (i64)out.size();
         flen[f] = (i64)buf.size();
         out.insert(out.end(), buf.begin(), buf.end());
     };
+    double tst = now();
     std::atomic<i64> next(0);
     auto worker = [&](int t) {
-        std::vector<i32> mark(n, -1), buf;
+        std::vector<i32> &mark = marks[t], buf;
+        mark.assign(n, -1);
         while (true) {
             const i64 k = next.fetch_add(1);
             if (k >= (i64)tasks.size()) break;
@@ -961,17 +1293,49 @@ std::string supernodal_tree(const Adj &G, const std::vector<i64> &perm, const st
     {
         pool_run(threads, worker);
     }
+    stage("    separators below the cut", tst);
     {
-        std::vector<i32> mark(n, -1), buf;
+        // above the cut: the fronts of one height (longest path down to the cut) are independent; heights in order
+        std::vector<i64> height(nf, 0), hptr, hidx;
+        i64 hmax = -1;
+        for (i64 f = 0; f < nf; f++) {
+            if (!top[f]) continue;
+            for (i64 c = chead[f]; c >= 0; c = cnext[c])
+                if (top[c]) height[f] = std::max(height[f], height[c] + 1);
+            hmax = std::max(hmax, height[f]);
+        }
+        hptr.assign(hmax + 2, 0);
         for (i64 f = 0; f < nf; f++)
-            if (top[f]) front(f, bufs[threads], threads, mark, buf);
+            if (top[f]) hptr[height[f] + 1]++;
+        for (i64 h = 0; h <= hmax; h++) hptr[h + 1] += hptr[h];
+        hidx.resize(hptr[hmax + 1]);
+        {
+            std::vector<i64> pos(hptr.begin(), hptr.end() - 1);
+            for (i64 f = 0; f < nf; f++)
+                if (top[f]) hidx[pos[height[f]]++] = f;
+        }
+        for (i64 h = 0; h <= hmax; h++) {
+            std::atomic<i64> nx(hptr[h]);
+            pool_run((int)std::min<i64>(threads, hptr[h + 1] - hptr[h]), [&](int t) {
+                std::vector<i32> buf;
+                for (i64 k; (k = nx.fetch_add(1)) < hptr[h + 1];) {
+                    const i64 f = hidx[k];
+                    front(f, topsep[f], TOP, marks[t], buf);
+                }
+            });
+        }
     }
+    stage("    separators above the cut", tst);
     if (bad) return "front structure is not a postorder of its tree";
     Sptr.assign(nf + 1, 0);
     for (i64 f = 0; f < nf; f++) Sptr[f + 1] = Sptr[f] + flen[f];
     Stgt.resize(Sptr[nf]);
-    for (i64 f = 0; f < nf; f++)
-        std::copy(bufs[fbuf[f]].begin() + foff[f], bufs[fbuf[f]].begin() + foff[f] + flen[f], Stgt.begin() + Sptr[f]);
+    parallel_for(nf, threads, [&](i64 a, i64 b) {
+        for (i64 f = a; f < b; f++) {
+            const i32 *src = fbuf[f] == TOP ? topsep[f].data() : bufs[fbuf[f]].data() + foff[f];
+            std::copy(src, src + flen[f], Stgt.begin() + Sptr[f]);
+        }
+    });
     // the tree the separators define must be the one given
     parent.assign(nf, -1);
     std::vector<i64> fof(n);
@@ -1156,38 +1520,54 @@ std::string finish(const Adj &G, i64 n, const i64 *colptr, const i64 *rowval, st
     out.entry_row.resize(nnz);
     out.entry_col.resize(nnz);
     stage("    entry arrays", ts);
+    const int nth = analysis_threads(n);
     std::vector<i32> fof(n);
-    for (i64 f = 0; f < nf; f++)
-        for (i64 v = out.Rptr[f]; v < out.Rptr[f + 1]; v++) fof[v] = (i32)f;
-    std::vector<i64> eptr(nf + 1, 0);
-    std::vector<i32> eidx(nnz);
+    parallel_for(nf, nth, [&](i64 a, i64 b) {
+        for (i64 f = a; f < b; f++)
+            for (i64 v = out.Rptr[f]; v < out.Rptr[f + 1]; v++) fof[v] = (i32)f;
+    });
+    // blocks of columns on the threads: per-block counts per front, then each block places its entries after those
+    // of the blocks before it (the order a serial pass over the columns gives)
     const bool split = out.nB > 1;
-    for (i64 c = 0; c < n; c++) {
-        const i64 j = out.invp[c];
-        for (i64 p = colptr[c]; p < colptr[c + 1]; p++) {
-            const i64 i = out.invp[rowval[p]];
-            if (split && out.comp[i] != out.comp[j]) {
-                out.entry_front[p] = -1;
-                continue;
+    const int T = (int)std::max<i64>(1, std::min<i64>(nth, n / 1024));
+    std::vector<std::vector<i64>> cnt(T);
+    std::vector<i64> eptr(nf + 1, 0), colof(nnz);   // colof: column of A of each entry
+    std::vector<i32> eidx(nnz);
+    pool_run(T, [&](int t) {
+        std::vector<i64> &h = cnt[t];
+        h.assign(nf, 0);
+        for (i64 c = n * t / T; c < n * (t + 1) / T; c++) {
+            const i64 j = out.invp[c];
+            for (i64 p = colptr[c]; p < colptr[c + 1]; p++) {
+                colof[p] = c;
+                const i64 i = out.invp[rowval[p]];
+                if (split && out.comp[i] != out.comp[j]) {
+                    out.entry_front[p] = -1;
+                    continue;
+                }
+                const i64 f = fof[std::min<i64>(i, j)];
+                out.entry_front[p] = f;
+                h[f]++;
             }
-            const i64 f = fof[std::min<i64>(i, j)];
-            out.entry_front[p] = f;
-            eptr[f + 1]++;
         }
-    }
+    });
     stage("    entry fronts", ts);
-    for (i64 f = 0; f < nf; f++) eptr[f + 1] += eptr[f];
-    {
-        std::vector<i64> pos(eptr.begin(), eptr.end() - 1);
-        for (i64 p = 0; p < nnz; p++)
-            if (out.entry_front[p] >= 0) eidx[pos[out.entry_front[p]]++] = (i32)p;
+    for (i64 f = 0; f < nf; f++) {
+        i64 run = eptr[f];
+        for (int t = 0; t < T; t++) {
+            const i64 c = cnt[t][f];
+            cnt[t][f] = run;
+            run += c;
+        }
+        eptr[f + 1] = run;
     }
-    std::vector<i64> colof(nnz);   // column of A of each entry
-    for (i64 c = 0; c < n; c++)
-        for (i64 p = colptr[c]; p < colptr[c + 1]; p++) colof[p] = c;
+    pool_run(T, [&](int t) {
+        std::vector<i64> &pos = cnt[t];
+        for (i64 p = colptr[n * t / T]; p < colptr[n * (t + 1) / T]; p++)
+            if (out.entry_front[p] >= 0) eidx[pos[out.entry_front[p]]++] = (i32)p;
+    });
     stage("  entry lists", ts);
     std::atomic<bool> outside(false);
-    const int nth = analysis_threads(n);
     std::atomic<i64> nextf(0);
     pool_run(nth, [&](int) {
         std::vector<i32> where(n, -1);
@@ -1279,23 +1659,34 @@ std::string analyze_given(i64 n, const i64 *colptr, const i64 *rowval, const i64
 std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOptions &opts, const i64 *given_perm,
                     Symbolic &out) {
     double t0 = now();
-    std::string err = check_csc(n, colptr, rowval);
+    const int nth = analysis_threads(n);
+    std::string err = check_csc(n, colptr, rowval, nth);
     if (!err.empty()) return err;
     // 0. strongly connected components in a topological order (sccs, chordal_ssymbolic.jl:26-57): the pattern that is
-    //    ordered and factorized is that of the diagonal blocks; every order below is regrouped by component
+    //    ordered and factorized is that of the diagonal blocks; every order below is regrouped by component.  A
+    //    symmetric pattern has no arcs between its components, which are its connected components.
     std::vector<i32> comp;
-    const i64 nB = strong_components(n, colptr, rowval, comp);
-    const std::vector<i32> *cp = nB > 1 ? &comp : nullptr;
+    double tsc = t0;
+    stage("  check", tsc);
     Adj G;
-    err = symmetrize(n, colptr, rowval, G, cp);
-    if (!err.empty()) return err;
-    {
-        double tt = t0;
-        stage("  symmetrize", tt);
+    i64 nB;
+    if (pattern_symmetric(n, colptr, rowval, nth)) {
+        offdiagonal(n, colptr, rowval, G, nth);
+        stage("  symmetric pattern", tsc);
+        nB = connected_components(G, comp, nth);
+        stage("  connected components", tsc);
+    } else {
+        nB = strong_components(n, colptr, rowval, comp);
+        stage("  strong components", tsc);
+        err = symmetrize(n, colptr, rowval, G, nB > 1 ? &comp : nullptr);
+        if (!err.empty()) return err;
+        stage("  symmetrize", tsc);
     }
+    const std::vector<i32> *cp = nB > 1 ? &comp : nullptr;
     // 1. fill-reducing order
     std::vector<i64> perm0(n);
     std::vector<i64> perm1, pcol, ccol;   // set here by the automatic choice (2. and 3. below otherwise)
+    std::vector<NDRange> sub;   // nested dissection's ranges
     if (opts.ordering == 4) {
         // both orders (minimum degree on its own thread while nested dissection uses the pool); keep the one whose
         // factor has fewer entries
@@ -1306,7 +1697,7 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
         tamd.join();
         std::vector<i64> p1[2], pc[2], cc[2];
         if (cp) {
-            group_by_component(nd.order, comp, nB);
+            group_by_component(nd.order, comp, nB, &nd.ranges);
             group_by_component(pa, comp, nB);
         }
         const std::vector<i64> *cand[2] = {&nd.order, &pa};
@@ -1314,8 +1705,8 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
             etree_postorder(G, *cand[1], p1[1], pc[1]);
             column_counts(G, p1[1], pc[1], cc[1]);
         });
-        etree_postorder(G, *cand[0], p1[0], pc[0]);
-        column_counts(G, p1[0], pc[0], cc[0]);
+        etree_postorder(G, *cand[0], p1[0], pc[0], &nd.ranges, nth);
+        column_counts(G, p1[0], pc[0], cc[0], nth);
         t1.join();
         i64 fill[2] = {0, 0};
         for (int c = 0; c < 2; c++)
@@ -1328,7 +1719,8 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
     } else if (opts.ordering == 0) {
         ND nd(G, opts.nd_leaf);
         nd.run(analysis_threads(n));
-        perm0 = nd.order;
+        perm0.swap(nd.order);
+        sub.swap(nd.ranges);
     } else if (opts.ordering == 3) {
         perm0 = amd_order(G);
     } else if (opts.ordering == 1) {
@@ -1342,16 +1734,16 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
             perm0[k] = given_perm[k];
         }
     }
-    if (cp && opts.ordering != 4) group_by_component(perm0, comp, nB);
+    if (cp && opts.ordering != 4) group_by_component(perm0, comp, nB, &sub);
     out.seconds_order = now() - t0;
     double ts = t0;
     stage("symmetrize + order", ts);
     // 2. postordered elimination tree
-    if (opts.ordering != 4) etree_postorder(G, perm0, perm1, pcol);
+    if (opts.ordering != 4) etree_postorder(G, perm0, perm1, pcol, sub.empty() ? nullptr : &sub, nth);
     stage("etree + postorder", ts);
     // 3. column counts, then fundamental supernodes: j + 1 continues j's supernode when it is j's parent, has no
     //    other child, and its column holds exactly one entry fewer
-    if (opts.ordering != 4) column_counts(G, perm1, pcol, ccol);
+    if (opts.ordering != 4) column_counts(G, perm1, pcol, ccol, nth);
     std::vector<i64> nchild(n, 0);
     for (i64 j = 0; j < n; j++)
         if (pcol[j] >= 0) nchild[pcol[j]]++;
@@ -1427,11 +1819,22 @@ std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOption
     stage("    amalgamation setup", ts);
     std::vector<i64> kptr, kidx;
     csr(ns, [&](i64 s) { return par1[s]; }, kptr, kidx);
-    std::vector<i64> cs;
+    std::vector<i64> cs, ckey;
     for (i64 p = 0; p < ns; p++) {
-        // children with few columns first: they gain the most
+        // children with few columns first: they gain the most (a stable insertion sort: a front has few children)
         cs.assign(kidx.begin() + kptr[p], kidx.begin() + kptr[p + 1]);
-        std::stable_sort(cs.begin(), cs.end(), [&](i64 a, i64 b) { return mnn[find(a)] < mnn[find(b)]; });
+        ckey.resize(cs.size());
+        for (size_t a = 0; a < cs.size(); a++) ckey[a] = mnn[find(cs[a])];
+        for (size_t a = 1; a < cs.size(); a++) {
+            const i64 c = cs[a], k = ckey[a];
+            size_t b = a;
+            for (; b > 0 && ckey[b - 1] > k; b--) {
+                cs[b] = cs[b - 1];
+                ckey[b] = ckey[b - 1];
+            }
+            cs[b] = c;
+            ckey[b] = k;
+        }
         for (i64 c : cs) {
             i64 rc = find(c), rp = find(p);
             i64 nn = mnn[rp] + mnn[rc], na = mna[rp];
