@@ -142,6 +142,20 @@ pp_status pp_refactor(pp_ctx *ctx, pp_fac *fac, const void *nzval, int on_device
 pp_status pp_fac_export(pp_ctx *ctx, const pp_fac *fac, void *LD, void *UD, void *LL, void *UL);
 pp_status pp_fac_destroy(pp_fac *fac);
 
+/* mlu(s, A::AbstractMatrix): the dense n x n matrix A (column-major, leading dimension lda >= n; device memory when
+ * on_device != 0, else host) factorized in its own vertex order, A* = U* L* -- the reference's DenseSLU
+ * (src/CPU/abstract_slu.jl:55-58, src/CPU/dense_slu.jl:1-44, dense sgetrf! src/CPU/dense/sgetrf.jl:5-70).  The
+ * factor owns its structure (one front, no separator) and takes every call that takes a pp_fac: pp_star (sgetri!,
+ * src/CPU/dense/sgetri.jl:3-35), pp_lmul / pp_rmul / pp_sgetrs (sgetrs!, src/CPU/dense/sgetrs.jl:3-57),
+ * pp_fac_export (LD: the n x n in-place L + U of DenseSLU.A). */
+pp_status pp_dense_factor(pp_ctx *ctx, int semiring, int dtype, int64_t n, const void *A, int64_t lda, int on_device,
+                          pp_fac **fac);
+/* copyto!(F, A) + lu!(F) of a dense factorization (src/CPU/dense_slu.jl:23-33): new values, factorized in place. */
+pp_status pp_dense_refactor(pp_ctx *ctx, pp_fac *fac, const void *A, int64_t lda, int on_device);
+/* sgetrf!(s, A) on a device matrix: A <- L + U with A* = U* L*, in place (src/CPU/dense/sgetrf.jl:5-17; the
+ * reference's GPU method CPU.sgetrf!(s, A::CuMatrix), ext/PATHPACKCUDAExt/dense/dense.jl:31-33). */
+pp_status pp_dense_sgetrf(pp_ctx *ctx, int semiring, int dtype, int64_t n, void *A, int64_t lda);
+
 /* ===== star and solves (device) ===== */
 
 /* Matrix(F): the full star A* (n x n, column-major, ldc >= n, original labels) into `out`: a device pointer when

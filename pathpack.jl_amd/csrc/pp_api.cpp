@@ -43,6 +43,7 @@ pp_sym::~pp_sym() {
 pp_fac::~pp_fac() {
     // the blocks (stream-ordered pool of the context's stream): the plans and the factor arrays
     for (void *p : plan.owned) hipFreeAsync(p, ctx->stream);
+    delete own_sym;   // a dense factorization's own structure (host only)
 }
 
 static bool supported(int semiring, int dtype) {
@@ -366,14 +367,16 @@ static size_t factor_bytes(const pp::Symbolic &S, const pp::FactorPlan &P, size_
 
 // finish: wait for the factorization before returning (pp_factor); pp_mstar queues the star behind it instead, and
 // passes the star's bytes as `extra` so that the one check covers both before anything is queued
+// dense: nzval is a dense n x n matrix with leading dimension dense_lda (pp_dense_factor; csym its one-front
+// structure), in device memory when on_device, else in host memory
 static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, int dtype, const void *nzval,
                                bool on_device, pp_fac **out, bool finish = true, size_t extra = 0,
-                               const char *who = "pp_factor") {
+                               const char *who = "pp_factor", i64 dense_lda = 0) {
     if (!ctx) return fail(nullptr, PP_EINVAL, "pp_factor: null context");
     if (!csym || !out) return fail(ctx, PP_EINVAL, "pp_factor: null argument");
     *out = nullptr;
     if (!supported(semiring, dtype)) return fail(ctx, PP_EUNSUPPORTED, "pp_factor: unsupported semiring / element type");
-    if (csym->S.nnz > 0 && !nzval) return fail(ctx, PP_EINVAL, "pp_factor: null nzval");
+    if ((csym->S.nnz > 0 || (dense_lda && csym->S.n > 0)) && !nzval) return fail(ctx, PP_EINVAL, "pp_factor: null nzval");
     CHECK_HIP(ctx, hipSetDevice(ctx->device));
     pp_sym *sym = const_cast<pp_sym *>(csym);   // the plans are a cache of the immutable structure
     const pp::Symbolic &S = sym->S;
@@ -411,7 +414,8 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     }
     const pp::FactorPlan &P = *sym->fplan;
     const size_t nD = (size_t)S.Dptr[S.nf], nL = (size_t)S.Lptr[S.nf];
-    const size_t need = factor_bytes(S, P, es, on_device, extra);
+    const size_t dense_tmp = dense_lda && !on_device ? (size_t)S.n * (size_t)S.n * es : 0;   // the uploaded matrix
+    const size_t need = factor_bytes(S, P, es, on_device, extra) + dense_tmp;
     size_t freeb = 0, totalb = 0;
     if (mem_free(ctx, &freeb, &totalb) != hipSuccess) return failj(PP_EHIP, std::string(who) + ": hipMemGetInfo failed");
     if (need > freeb) {
@@ -476,7 +480,23 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
     }
     const void *dnz = nzval;
     void *tmpnz = nullptr;
-    if (!on_device && S.nnz > 0) {
+    if (dense_lda) {
+        const size_t n = (size_t)S.n;
+        fac->dense_src = nzval;
+        fac->dense_lda = dense_lda;
+        if (!on_device && n > 0) {
+            if (pp::ctx_alloc(ctx, &tmpnz, n * n * es, st) != hipSuccess)
+                return failf(PP_ENOMEM, std::string(who) + ": allocation of the matrix failed");
+            if (hipMemcpy2DAsync(tmpnz, n * es, nzval, (size_t)dense_lda * es, n * es, n, hipMemcpyHostToDevice, st) !=
+                hipSuccess) {
+                hipFreeAsync(tmpnz, st);
+                return failf(PP_EHIP, std::string(who) + ": upload of the matrix failed");
+            }
+            fac->dense_src = tmpnz;
+            fac->dense_lda = (i64)n;
+        }
+        dnz = nullptr;
+    } else if (!on_device && S.nnz > 0) {
         if (pp::ctx_alloc(ctx, &tmpnz, S.nnz * es, st) != hipSuccess) return failf(PP_ENOMEM, "pp_factor: hipMalloc of the values failed");
         if (hipMemcpyAsync(tmpnz, nzval, S.nnz * es, hipMemcpyHostToDevice, st) != hipSuccess) {
             hipFreeAsync(tmpnz, st);
@@ -485,6 +505,8 @@ static pp_status factor_common(pp_ctx *ctx, const pp_sym *csym, int semiring, in
         dnz = tmpnz;
     }
     e = pp::device_factor(ctx, fac, dnz);
+    fac->dense_src = nullptr;
+    fac->dense_lda = 0;
     if (tmpnz) hipFreeAsync(tmpnz, st);
     if (!e.empty()) return failf(PP_EHIP, "pp_factor: " + e);
     // block 2: the sweep plan, the permutation and the sweep packs (built from the factor)
@@ -570,6 +592,7 @@ pp_status pp_factor_device(pp_ctx *ctx, const pp_sym *sym, int semiring, int dty
 pp_status pp_refactor(pp_ctx *ctx, pp_fac *fac, const void *nzval, int on_device) {
     if (!ctx || !fac) return fail(ctx, PP_EINVAL, "pp_refactor: null argument");
     if (fac->ctx != ctx) return fail(ctx, PP_EINVAL, "pp_refactor: the factor belongs to another context");
+    if (fac->own_sym) return fail(ctx, PP_EINVAL, "pp_refactor: a dense factorization takes pp_dense_refactor");
     const pp::Symbolic &S = fac->sym->S;
     if (S.nnz > 0 && !nzval) return fail(ctx, PP_EINVAL, "pp_refactor: null nzval");
     CHECK_HIP(ctx, hipSetDevice(ctx->device));
@@ -601,6 +624,93 @@ pp_status pp_refactor(pp_ctx *ctx, pp_fac *fac, const void *nzval, int on_device
     hipError_t se = hipStreamSynchronize(st);
     if (!e.empty() || se != hipSuccess)
         return fail(ctx, PP_EHIP, "pp_refactor: " + (e.empty() ? std::string(hipGetErrorString(se)) : e));
+    return PP_OK;
+}
+
+pp_status pp_dense_factor(pp_ctx *ctx, int semiring, int dtype, int64_t n, const void *A, int64_t lda, int on_device,
+                          pp_fac **fac) {
+    if (!ctx) return fail(nullptr, PP_EINVAL, "pp_dense_factor: null context");
+    if (!fac) return fail(ctx, PP_EINVAL, "pp_dense_factor: null output");
+    *fac = nullptr;
+    if (n < 0 || n > (int64_t)1 << 30) return fail(ctx, PP_EINVAL, "pp_dense_factor: n out of range");
+    if (n > 0 && (!A || lda < n)) return fail(ctx, PP_EINVAL, "pp_dense_factor: null matrix or lda < n");
+    pp_sym *sym = new (std::nothrow) pp_sym;
+    if (!sym) return fail(ctx, PP_ENOMEM, "pp_dense_factor: out of host memory");
+    try {
+        pp::dense_structure(n, sym->S);
+    } catch (const std::bad_alloc &) {
+        delete sym;
+        return fail(ctx, PP_ENOMEM, "pp_dense_factor: out of host memory");
+    }
+    pp_status st = factor_common(ctx, sym, semiring, dtype, A, on_device != 0, fac, true, 0, "pp_dense_factor",
+                                 std::max<int64_t>(1, lda));
+    if (st != PP_OK) {
+        delete sym;
+        return st;
+    }
+    (*fac)->own_sym = sym;
+    return PP_OK;
+}
+
+pp_status pp_dense_refactor(pp_ctx *ctx, pp_fac *fac, const void *A, int64_t lda, int on_device) {
+    if (!ctx || !fac) return fail(ctx, PP_EINVAL, "pp_dense_refactor: null argument");
+    if (fac->ctx != ctx) return fail(ctx, PP_EINVAL, "pp_dense_refactor: the factor belongs to another context");
+    if (!fac->own_sym) return fail(ctx, PP_EINVAL, "pp_dense_refactor: not a dense factorization (pp_refactor)");
+    const i64 n = fac->sym->S.n;
+    if (n > 0 && (!A || lda < n)) return fail(ctx, PP_EINVAL, "pp_dense_refactor: null matrix or lda < n");
+    CHECK_HIP(ctx, hipSetDevice(ctx->device));
+    const size_t es = (size_t)pp::dtype_size(fac->dtype);
+    const pp::SweepPlan &W = *fac->sym->splan;
+    const size_t need = es * ((size_t)fac->sym->fplan->arena + (on_device ? 0 : (size_t)n * (size_t)n) +
+                              (size_t)W.nb * 2 * pp::BLK_W * pp::BLK_W);
+    size_t freeb = 0, totalb = 0;
+    CHECK_HIP(ctx, mem_free(ctx, &freeb, &totalb));
+    if (need > freeb)
+        return fail(ctx, PP_ENOMEM, "pp_dense_refactor: needs " + std::to_string(need) + " bytes of device memory, " +
+                                        std::to_string(freeb) + " free");
+    hipStream_t st = ctx->stream;
+    void *tmp = nullptr;
+    fac->dense_src = A;
+    fac->dense_lda = std::max<int64_t>(1, lda);
+    if (!on_device && n > 0) {
+        if (pp::ctx_alloc(ctx, &tmp, (size_t)n * n * es, st) != hipSuccess) {
+            fac->dense_src = nullptr;
+            fac->dense_lda = 0;
+            return fail(ctx, PP_ENOMEM, "pp_dense_refactor: allocation of the matrix failed");
+        }
+        if (hipMemcpy2DAsync(tmp, n * es, A, (size_t)lda * es, n * es, n, hipMemcpyHostToDevice, st) != hipSuccess) {
+            hipFreeAsync(tmp, st);
+            hipStreamSynchronize(st);
+            fac->dense_src = nullptr;
+            fac->dense_lda = 0;
+            return fail(ctx, PP_EHIP, "pp_dense_refactor: upload of the matrix failed");
+        }
+        fac->dense_src = tmp;
+        fac->dense_lda = n;
+    }
+    std::string e = pp::device_factor(ctx, fac, nullptr);
+    fac->dense_src = nullptr;
+    fac->dense_lda = 0;
+    if (tmp) hipFreeAsync(tmp, st);
+    if (e.empty()) e = pp::device_factor_packs(ctx, fac);
+    hipError_t se = hipStreamSynchronize(st);
+    if (!e.empty() || se != hipSuccess)
+        return fail(ctx, PP_EHIP, "pp_dense_refactor: " + (e.empty() ? std::string(hipGetErrorString(se)) : e));
+    return PP_OK;
+}
+
+pp_status pp_dense_sgetrf(pp_ctx *ctx, int semiring, int dtype, int64_t n, void *A, int64_t lda) {
+    pp_fac *fac = nullptr;
+    pp_status st = pp_dense_factor(ctx, semiring, dtype, n, A, lda, 1, &fac);
+    if (st != PP_OK) return st;
+    const size_t es = (size_t)pp::dtype_size(dtype);
+    hipError_t e = hipSuccess;
+    if (n > 0)
+        e = hipMemcpy2DAsync(A, (size_t)lda * es, fac->LD, (size_t)n * es, (size_t)n * es, (size_t)n,
+                             hipMemcpyDeviceToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    pp_fac_destroy(fac);
+    if (e != hipSuccess) return fail(ctx, PP_EHIP, std::string("pp_dense_sgetrf: ") + hipGetErrorString(e));
     return PP_OK;
 }
 

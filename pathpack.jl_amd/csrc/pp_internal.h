@@ -269,6 +269,11 @@ struct pp_fac {
     void *Dpack = nullptr, *Upack = nullptr, *Lpack = nullptr;
     void *Bpack = nullptr, *Hpack = nullptr;             // star blocks
     void *Nval = nullptr, *NTval = nullptr;              // N's values by column and by row (components coupled)
+    // a dense factorization (pp_dense_factor) owns its one-front structure; while it factorizes, the values are the
+    // n x n matrix dense_src (device memory, leading dimension dense_lda) instead of stored entries
+    pp_sym *own_sym = nullptr;
+    const void *dense_src = nullptr;
+    int64_t dense_lda = 0;
     ~pp_fac();
 };
 

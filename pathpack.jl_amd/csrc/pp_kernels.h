@@ -59,6 +59,15 @@ __global__ void k_scatter_entries(T *__restrict__ F, const i64 *__restrict__ pos
 }
 
 // dst[q] = src[idx[q]]: the values of N (by column and by row) from A's values
+// dst[i + j ldd] = src[i + j lds] for i < rows, j < cols: blockIdx.y strides over the columns, the threads of x over
+// the rows
+template <class T>
+__global__ __launch_bounds__(NT) void k_copy2d(T *__restrict__ dst, i64 ldd, const T *__restrict__ src, i64 lds,
+                                                i64 rows, i64 cols) {
+    for (i64 j = blockIdx.y; j < cols; j += gridDim.y)
+        for (i64 i = blockIdx.x * (i64)NT + threadIdx.x; i < rows; i += (i64)gridDim.x * NT) dst[i + j * ldd] = src[i + j * lds];
+}
+
 template <class T>
 __global__ void k_gather(T *__restrict__ dst, const T *__restrict__ src, const i64 *__restrict__ idx, i64 m) {
     for (i64 q = blockIdx.x * (i64)NT + threadIdx.x; q < m; q += (i64)gridDim.x * NT) dst[q] = src[idx[q]];
@@ -1996,7 +2005,15 @@ template <class S> struct FactorRun {
         timer_start(ctx, 0);
         T *F = nullptr;
         HIPCHK(ctx_alloc(ctx, (void **)&F, std::max<i64>(1, P.arena) * sizeof(T), st));
-        k_fill<T><<<grid1(P.arena), NT, 0, st>>>(F, P.arena, S::zero());
+        const i64 nd = fac->sym->S.n;
+        if (fac->dense_src && nd > 0) {
+            // a dense matrix: its one front is the whole matrix (column-major, leading dimension nj = n)
+            if (P.arena != nd * nd || P.Foff.empty() || P.Foff[0] != 0) return "dense factor: unexpected front arena";
+            const unsigned gx = (unsigned)std::min<i64>(16, (nd + NT - 1) / NT), gy = (unsigned)std::min<i64>(nd, 8192);
+            k_copy2d<T><<<dim3(gx, gy), NT, 0, st>>>(F, nd, (const T *)fac->dense_src, fac->dense_lda, nd, nd);
+        } else {
+            k_fill<T><<<grid1(P.arena), NT, 0, st>>>(F, P.arena, S::zero());
+        }
         LAUNCHCHK();
         if (fac->sym->S.nnz > 0)
             k_scatter_entries<T><<<grid1(fac->sym->S.nnz), NT, 0, st>>>(F, d.entry_pos, (const T *)nz, fac->sym->S.nnz);

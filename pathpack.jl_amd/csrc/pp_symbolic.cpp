@@ -1656,6 +1656,36 @@ std::string analyze_given(i64 n, const i64 *colptr, const i64 *rowval, const i64
     return "";
 }
 
+void dense_structure(i64 n, Symbolic &out) {
+    out = Symbolic();
+    out.n = n;
+    out.perm.resize(n);
+    std::iota(out.perm.begin(), out.perm.end(), 0);
+    out.invp = out.perm;
+    out.nf = n > 0 ? 1 : 0;
+    out.Rptr = n > 0 ? std::vector<i64>{0, n} : std::vector<i64>{0};
+    out.Sptr.assign(out.nf + 1, 0);
+    out.parent.assign(out.nf, -1);
+    out.fdsc.assign(out.nf, 0);
+    out.Dptr = n > 0 ? std::vector<i64>{0, n * n} : std::vector<i64>{0};
+    out.Lptr.assign(out.nf + 1, 0);
+    out.nB = 1;
+    out.Bptr = {0, n};
+    out.Fptr = {0, out.nf};
+    out.nN = 0;
+    out.Nptr.assign(n + 1, 0);
+    out.NTptr.assign(n + 1, 0);
+    out.lev_up.assign(1, 0);
+    out.lev_dn.assign(1, 0);
+    out.anc_lo.assign(1, 0);
+    out.nnz = 0;
+    work_counts(n, out.Rptr, out.Sptr, out.parent, out.madds_factor, out.madds_star, out.madds_rhs, out.nnzL);
+    out.madds_factor_alg = out.madds_factor;
+    out.madds_star_alg = out.madds_star;
+    out.madds_rhs_alg = out.madds_rhs;
+    out.nnzL_alg = out.nnzL;
+}
+
 std::string analyze(i64 n, const i64 *colptr, const i64 *rowval, const SymOptions &opts, const i64 *given_perm,
                     Symbolic &out) {
     double t0 = now();

@@ -86,4 +86,8 @@ void pool_run(int n, const std::function<void(int)> &fn);
 std::string analyze_given(i64 n, const i64 *colptr, const i64 *rowval, const i64 *perm, i64 nf, const i64 *Rptr,
                           Symbolic &out);
 
+// The structure of a dense n x n matrix factorized in its own order (the reference's DenseSLU, dense_slu.jl:1-44):
+// one front holding every vertex, no separator, no stored entries (the values are copied into the front whole).
+void dense_structure(i64 n, Symbolic &out);
+
 }  // namespace pp

@@ -31,6 +31,7 @@ from ._lib import (PathpackArgumentError, PathpackDeviceError, PathpackError, Pa
 __all__ = [
     "AbstractSemiring", "MinPlus", "MaxPlus", "MaxMin", "MinMax", "PlusProd", "OrAnd",
     "szero", "sone", "mlu", "lu_", "mstar", "lmul_", "rmul_", "transpose", "adjoint", "Matrix", "star_rows", "star_cols", "Factorization", "Symbolic", "symbolic",
+    "DenseFactorization", "dense_mlu", "sgetrf_",
     "Context", "context", "DeviceArray", "PathpackError", "PathpackArgumentError", "PathpackMemoryError",
     "PathpackUnsupportedError", "PathpackDeviceError",
 ]
@@ -377,6 +378,69 @@ class Factorization:
         return {"LD": LD[:nD], "UD": UD[:nD], "LL": LL[:nL], "UL": UL[:nL]}
 
 
+class DenseFactorization(Factorization):
+    """A* = U* L* of a dense matrix in its own order (pp_dense_factor; the reference's DenseSLU, dense_slu.jl:1-44):
+    one front, no structure to analyse.  ``A`` (``export()["A"]``) is the in-place L + U of DenseSLU.A."""
+
+    def __init__(self, s: AbstractSemiring, n: int, dtype, handle, ctx: Context):
+        self.s = s
+        self.sym = None
+        self.dtype = np.dtype(dtype)
+        self.handle = handle
+        self.ctx = ctx
+        self.n = n
+
+    @property
+    def perm(self) -> np.ndarray:
+        return np.arange(self.n, dtype=np.int64)
+
+    def export(self) -> dict:
+        n = self.n
+        LD = np.empty(max(1, n * n), self.dtype)
+        self.ctx.check(lib().pp_fac_export(self.ctx.handle, self.handle, _p(LD), None, None, None))
+        A = LD[:n * n].reshape((n, n), order="F")
+        return {"A": A, "LD": LD[:n * n], "UD": LD[:n * n], "LL": LD[:0], "UL": LD[:0]}
+
+
+def _dense_operand(A):
+    """(n, pointer, lda, on_device, keep-alive) of a square dense matrix: a numpy array (column-major copy) or an
+    n x n DeviceArray (column-major in HBM)."""
+    if isinstance(A, DeviceArray):
+        if len(A.shape) != 2 or A.shape[0] != A.shape[1]:
+            raise PathpackArgumentError(_lib.PP_EINVAL, "the matrix must be square")
+        return A.shape[0], ctypes.c_void_p(A.ptr), max(1, A.shape[0]), 1, A, A.dtype
+    if A.ndim != 2 or A.shape[0] != A.shape[1]:
+        raise PathpackArgumentError(_lib.PP_EINVAL, "the matrix must be square")
+    M = np.asfortranarray(A)
+    return M.shape[0], _p(M), max(1, M.shape[0]), 0, M, M.dtype
+
+
+def dense_mlu(s: AbstractSemiring, A, device: int = 0) -> DenseFactorization:
+    """mlu(s, A::AbstractMatrix) -> DenseSLU (abstract_slu.jl:55-58): the dense matrix factorized in its own
+    order on the device (pp_dense_factor).  ``A``: a square numpy array or DeviceArray."""
+    ctx = context(device)
+    n, ptr, lda, on_dev, keep, dtype = _dense_operand(A)
+    dt = _dtype_code(dtype)
+    if (dt == I32) != isinstance(s, OrAnd):
+        raise PathpackUnsupportedError(_lib.PP_EUNSUPPORTED, f"{s.name} does not support {dtype}")
+    h = ctypes.c_void_p()
+    ctx.check(lib().pp_dense_factor(ctx.handle, s.id, dt, n, ptr, lda, on_dev, ctypes.byref(h)))
+    del keep
+    return DenseFactorization(s, n, dtype, h, ctx)
+
+
+def sgetrf_(s: AbstractSemiring, A: "DeviceArray") -> "DeviceArray":
+    """sgetrf!(s, A) on a device matrix (dense/sgetrf.jl:5-17): A <- L + U with A* = U* L*, in place."""
+    n, ptr, lda, on_dev, keep, dtype = _dense_operand(A)
+    if not on_dev:
+        raise PathpackArgumentError(_lib.PP_EINVAL, "sgetrf_: A must be a DeviceArray")
+    dt = _dtype_code(dtype)
+    if (dt == I32) != isinstance(s, OrAnd):
+        raise PathpackUnsupportedError(_lib.PP_EUNSUPPORTED, f"{s.name} does not support {dtype}")
+    A.ctx.check(lib().pp_dense_sgetrf(A.ctx.handle, s.id, dt, n, ptr, lda))
+    return A
+
+
 def _factor(s: AbstractSemiring, sym: Symbolic, nzval, ctx: Context) -> Factorization:
     dt = _dtype_code(nzval.dtype)
     if (dt == I32) != isinstance(s, OrAnd):
@@ -391,18 +455,17 @@ def mlu(s: AbstractSemiring, A, alg=None, amalgamate: bool = True, device: int =
     """Factorize the star of A over the semiring s: A* = U* L* (mlu, abstract_slu.jl:44-58).  A dense numpy A is one
     dense front in its natural order (the reference's DenseSLU path, abstract_slu.jl:65-68)."""
     ctx = context(device)
+    if isinstance(A, np.ndarray) and sym is None:
+        return dense_mlu(s, A, device)
     if isinstance(A, np.ndarray):
+        # a dense matrix with a structure given from outside: one stored entry per matrix entry
         if A.ndim != 2 or A.shape[0] != A.shape[1]:
             raise PathpackArgumentError(_lib.PP_EINVAL, "the matrix must be square")
         n = A.shape[0]
         cp = np.arange(0, n * n + 1, n, dtype=np.int64)
         rv = np.tile(np.arange(n, dtype=np.int64), n)
         nz = np.asfortranarray(A).ravel(order="F")
-        csc = (n, cp, rv, nz)
-        if sym is None:
-            sym = symbolic_given(csc, np.arange(n), np.array([0, n]) if n > 0 else np.array([0]))
-        else:
-            sym.check_pattern(n, cp, rv)
+        sym.check_pattern(n, cp, rv)
         return _factor(s, sym, nz, ctx)
     n, cp, rv, nz = _as_csc(A)
     if sym is None:
@@ -417,6 +480,13 @@ def lu_(F: Factorization, A):
     have the pattern F was analysed for, factorized in place on the device (no new analysis, plan upload or factor
     buffers; the reference GPU API's repeated-weights plan, ext/PATHPACKCUDAExt/api.jl:545-600).  ``A`` may also be
     a DeviceArray of the nnz values in the pattern's CSC order.  Returns F."""
+    if isinstance(F, DenseFactorization):
+        n, ptr, lda, on_dev, keep, dtype = _dense_operand(A)
+        if n != F.n or np.dtype(dtype) != F.dtype:
+            raise PathpackArgumentError(_lib.PP_EINVAL, "lu_: the matrix must be n x n of the factor's type")
+        F.ctx.check(lib().pp_dense_refactor(F.ctx.handle, F.handle, ptr, lda, on_dev))
+        del keep
+        return F
     if isinstance(A, DeviceArray):
         if A.dtype != F.dtype or int(np.prod(A.shape)) != F.sym.nnz:
             raise PathpackArgumentError(_lib.PP_EINVAL, "lu_: the values must be nnz entries of the factor's type")

@@ -21,6 +21,7 @@ EXPORTS = [
     "pp_star", "pp_mstar", "pp_star_sources", "pp_lmul", "pp_rmul", "pp_sgemx", "pp_getrf_star_batched",
     "pp_buffer_alloc", "pp_buffer_free", "pp_upload", "pp_download", "pp_copy", "pp_calibrate_valu", "pp_set_timing",
     "pp_get_timing", "pp_set_debug", "pp_sgetrs", "pp_sgetrs_noalloc", "pp_sym_components",
+    "pp_dense_factor", "pp_dense_refactor", "pp_dense_sgetrf",
 ]
 
 
@@ -86,6 +87,10 @@ def lib() -> ctypes.CDLL:
         L.pp_factor.argtypes = [c_vp, c_vp, ctypes.c_int, ctypes.c_int, c_vp, ctypes.POINTER(c_vp)]
         L.pp_factor_device.argtypes = [c_vp, c_vp, ctypes.c_int, ctypes.c_int, c_vp, ctypes.POINTER(c_vp)]
         L.pp_refactor.argtypes = [c_vp, c_vp, c_vp, ctypes.c_int]
+        L.pp_dense_factor.argtypes = [c_vp, ctypes.c_int, ctypes.c_int, c_i64, c_vp, c_i64, ctypes.c_int,
+                                      ctypes.POINTER(c_vp)]
+        L.pp_dense_refactor.argtypes = [c_vp, c_vp, c_vp, c_i64, ctypes.c_int]
+        L.pp_dense_sgetrf.argtypes = [c_vp, ctypes.c_int, ctypes.c_int, c_i64, c_vp, c_i64]
         L.pp_fac_export.argtypes = [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]
         L.pp_fac_destroy.argtypes = [c_vp]
         L.pp_star.argtypes = [c_vp, c_vp, c_vp, c_i64, ctypes.c_int]

@@ -267,3 +267,51 @@ def test_plusprod_grid_vs_inverse():
     sym = P.symbolic(g)
     C = O.star(O.factor(O.PLUSPROD, oracle_sym(sym), g.colptr, g.rowval, g.nzval))
     assert_star_equal(O.PLUSPROD, C, O.plusprod_inverse(g.dense(0.0)), rtol=1e-12)
+
+
+def dense_matrix(s, dtype, n, rng, zeros=0.6):
+    """A dense n x n matrix with weights suited to s and a share of semiring zeros (no arc)."""
+    if s == O.ORAND:
+        A = rng.integers(1, 128, (n, n)).astype(np.int32)
+    elif s == O.PLUSPROD:
+        A = (rng.random((n, n)) * (0.9 / max(1, n))).astype(dtype)
+    elif s == O.MAXPLUS:
+        A = (-rng.integers(1, 101, (n, n))).astype(dtype)
+    else:
+        A = rng.integers(1, 101, (n, n)).astype(dtype)
+    A[rng.random((n, n)) < zeros] = O.zero(s, A.dtype)
+    return np.asfortranarray(A)
+
+
+def dense_pattern(A):
+    """A dense matrix as the stored entries of a one-front structure in its own order (every entry stored)."""
+    n = A.shape[0]
+    cp = np.arange(0, n * n + 1, n, dtype=np.int64)
+    rv = np.tile(np.arange(n, dtype=np.int64), n)
+    sym = O.Sym(n, [0, n] if n else [0], [0, 0] if n else [0], np.zeros(0, np.int64), np.arange(n))
+    return sym, cp, rv, np.asfortranarray(A).ravel(order="F")
+
+
+@pytest.mark.parametrize("s", ALL)
+def test_dense_lu_factors_the_closure(s):
+    """The dense LU (DenseSLU, dense/sgetrf.jl:5-175): A <- L + U with A* = U* L*, L unit lower.  The stars of the two
+    triangles are taken by Floyd-Warshall (by (I - T)^-1 for PlusProd), and the one-front multifrontal factor of the
+    same matrix is the same LU."""
+    rng = np.random.default_rng(100 + s)
+    dtype = dtype_for(s)
+    n = 37
+    A = dense_matrix(s, dtype, n, rng)
+    LU = O.getrf(s, A)
+    z = O.zero(s, LU.dtype)
+    U = np.where(np.triu(np.ones((n, n), bool)), LU, z).astype(LU.dtype)
+    L = np.where(np.tril(np.ones((n, n), bool), -1), LU, z).astype(LU.dtype)
+    if s == O.PLUSPROD:
+        I = np.eye(n)
+        got = np.linalg.inv(I - U) @ np.linalg.inv(I - L)
+        assert np.allclose(got, O.plusprod_inverse(A), rtol=1e-12, atol=0)
+    else:
+        got = semiring_matmul(s, O.floyd_warshall(s, U), O.floyd_warshall(s, L))
+        assert np.array_equal(got, O.floyd_warshall(s, A))
+    sym, cp, rv, nz = dense_pattern(A)
+    Fo = O.factor(s, sym, cp, rv, nz)
+    assert_star_equal(s, Fo.LD.reshape(n, n, order="F"), LU)
