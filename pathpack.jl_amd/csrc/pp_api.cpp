@@ -165,10 +165,6 @@ pp_status pp_destroy(pp_ctx *ctx) {
         if (e) hipEventDestroy(e);
     if (ctx->staging) hipHostFree(ctx->staging);
     if (ctx->staging2) hipHostFree(ctx->staging2);
-    if (ctx->copy_stream) {
-        hipStreamSynchronize(ctx->copy_stream);
-        hipStreamDestroy(ctx->copy_stream);
-    }
     for (auto &e : ctx->pev)
         if (e) hipEventDestroy(e);
     for (auto &p : ctx->outpin)

@@ -246,10 +246,8 @@ struct pp_ctx {
     size_t staging_bytes = 0;
     void *staging2 = nullptr;       // pinned host staging of the sweep plan
     size_t staging2_bytes = 0;
-    // star to host memory: a second stream for the device-to-host copies, the pipeline's events, and two pinned
-    // chunk buffers (kept between calls)
-    hipStream_t copy_stream = nullptr;
-    hipEvent_t pev[4] = {};
+    // star to host memory: the pipeline's events and two pinned chunk buffers (kept between calls)
+    hipEvent_t pev[2] = {};
     // the star blocks' packs are built on a second stream, overlapped with the start of the star: aux_from orders
     // them after the factorization, aux_done orders every later reader (block GEMMs) and writer (the next
     // factorization of the same buffers) after them
@@ -258,6 +256,7 @@ struct pp_ctx {
     bool aux_pending = false;        // aux_done is recorded
     void *outpin[2] = {nullptr, nullptr};
     size_t outpin_bytes = 0;
+    void *outpin_dev[2] = {nullptr, nullptr};   // their device-side addresses (the relabel kernel writes them)
 };
 
 struct pp_fac {

@@ -2461,11 +2461,12 @@ template <class S> struct StarRun {
         HIPCHK(hipFreeAsync(X, st));
         return "";
     }
-    // Relabel into host memory in K >= 4 column chunks: chunk k is relabelled into device buffer k % 2 (the
-    // context's stream), copied into pinned buffer k % 2 (the copy stream, after the relabel's event), then copied
-    // by the host's worker threads into `out`; the relabel of chunk k + 2 starts once chunk k's device-to-host copy
-    // is done, and its copy once the host has read the pinned buffer.  The device computes, the copy engine moves
-    // and the host copies three different chunks at a time.
+    // Relabel into host memory in K >= 4 column chunks: the relabel kernel writes chunk k straight into pinned buffer
+    // k % 2 over PCIe (its device-side address; the writes are coalesced 16-byte vectors), then the host's worker
+    // threads copy it into `out`; the relabel of chunk k + 2 is queued once the host has read chunk k's buffer.  The
+    // device writes one chunk while the host copies the other.  (A copy-engine transfer from a device-side chunk
+    // buffer ran at half the PCIe rate in some states of the device memory pool; the kernel's writes do not depend
+    // on them.)
     std::string to_host(const typename S::value_type *X, i64 n) {
         typedef typename S::value_type T;
         hipStream_t st = ctx->stream;
@@ -2474,42 +2475,39 @@ template <class S> struct StarRun {
         const i64 CB = (n + K - 1) / K;   // columns per chunk
         const i64 nchunk = (n + CB - 1) / CB;
         const size_t cbytes = (size_t)(CB * n) * sizeof(T);
-        if (!ctx->copy_stream) HIPCHK(hipStreamCreateWithFlags(&ctx->copy_stream, hipStreamNonBlocking));
         for (auto &ev : ctx->pev)
             if (!ev) HIPCHK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
         if (ctx->outpin_bytes < cbytes) {
+            HIPCHK(hipStreamSynchronize(st));
             for (auto &p : ctx->outpin)
                 if (p) hipHostFree(p);
             ctx->outpin[0] = ctx->outpin[1] = nullptr;
+            ctx->outpin_dev[0] = ctx->outpin_dev[1] = nullptr;
             ctx->outpin_bytes = 0;
-            for (auto &p : ctx->outpin) HIPCHK(hipHostMalloc(&p, cbytes, hipHostMallocDefault));
+            for (int b = 0; b < 2; b++) {
+                HIPCHK(hipHostMalloc(&ctx->outpin[b], cbytes, hipHostMallocDefault));
+                HIPCHK(hipHostGetDevicePointer(&ctx->outpin_dev[b], ctx->outpin[b], 0));
+            }
             ctx->outpin_bytes = cbytes;
         }
-        T *dc[2] = {nullptr, nullptr};
-        HIPCHK(ctx_alloc(ctx, (void **)&dc[0], 2 * cbytes, st));
-        dc[1] = dc[0] + CB * n;
-        hipStream_t cs = ctx->copy_stream;
         auto cols = [&](i64 k, i64 &j0, i64 &j1) {
             j0 = k * CB;
             j1 = std::min(n, j0 + CB);
         };
-        auto produce = [&](i64 k) -> std::string {   // relabel chunk k on the device, then its copy to pinned memory
+        auto produce = [&](i64 k) -> std::string {   // relabel chunk k into its pinned buffer
             i64 j0, j1;
             cols(k, j0, j1);
             const int b = (int)(k & 1);
-            relabel(X, n, dc[b], n, j0, j1);
+            relabel(X, n, (T *)ctx->outpin_dev[b], n, j0, j1);
             LAUNCHCHK();
             HIPCHK(hipEventRecord(ctx->pev[b], st));
-            HIPCHK(hipStreamWaitEvent(cs, ctx->pev[b], 0));
-            HIPCHK(hipMemcpyAsync(ctx->outpin[b], dc[b], (size_t)((j1 - j0) * n) * sizeof(T), hipMemcpyDeviceToHost, cs));
-            HIPCHK(hipEventRecord(ctx->pev[2 + b], cs));
             return "";
         };
         std::string e;
         for (i64 k = 0; k < std::min<i64>(2, nchunk) && e.empty(); k++) e = produce(k);
         for (i64 k = 0; k < nchunk && e.empty(); k++) {
             const int b = (int)(k & 1);
-            hipError_t he = hipEventSynchronize(ctx->pev[2 + b]);
+            hipError_t he = hipEventSynchronize(ctx->pev[b]);
             if (he != hipSuccess) {
                 e = std::string("hipEventSynchronize: ") + hipGetErrorString(he);
                 break;
@@ -2531,8 +2529,7 @@ template <class S> struct StarRun {
             });
             if (k + 2 < nchunk) e = produce(k + 2);
         }
-        hipStreamSynchronize(cs);
-        hipFreeAsync(dc[0], st);
+        HIPCHK(hipStreamSynchronize(st));
         return e;
     }
 };
