@@ -561,3 +561,30 @@ def test_coupled_components_match_oracle(name, s, fdtype):
         assert_star_equal(s, P.star_cols(F, src), Co[:, src], rtol=rtol)
     finally:
         ctx.set_poison(False)
+
+
+@pytest.mark.parametrize("name", ["grid16x17x15", "digraph300", "layered3d"])
+@pytest.mark.parametrize("s", [O.MINPLUS, O.MAXPLUS, O.MAXMIN, O.MINMAX, O.ORAND])
+def test_repeat_runs_are_bit_identical(name, s):
+    """Determinism (test/gpu/stress_large.jl:130-132: the same solve again, bit for bit): for the idempotent
+    semirings every result is the same bits on a second run -- the star, the solves (their forward step scatters with
+    atomic updates, whose order varies; min / max / or do not depend on it), and rows for sources.  Float32 for the
+    tropical semirings, Int32 for OrAnd; symmetric, directed and component-coupled patterns."""
+    dtype = dtype_for(s, np.float32)
+    base = {"grid16x17x15": lambda: W.grid((16, 17, 15)), "digraph300": lambda: W.random_digraph(300, 0.01, 3),
+            "layered3d": DAG_GRAPHS["layered3d"]}[name]()
+    g = weighted(base, s, dtype)
+    F = P.mlu(SEMIRINGS[s], g)
+    C1, C2 = P.Matrix(F), P.Matrix(F)
+    assert np.array_equal(bits(C1), bits(C2))
+    rng = np.random.default_rng(5 + s)
+    B = np.asfortranarray(rng.integers(0, 40, (g.n, 9)).astype(dtype))
+    assert np.array_equal(bits(P.lmul_(F, B.copy(order="F"))), bits(P.lmul_(F, B.copy(order="F"))))
+    Bt = np.asfortranarray(rng.integers(0, 40, (4, g.n)).astype(dtype))
+    assert np.array_equal(bits(P.rmul_(Bt.copy(order="F"), F)), bits(P.rmul_(Bt.copy(order="F"), F)))
+    src = rng.integers(0, g.n, 37)
+    assert np.array_equal(bits(P.star_rows(F, src)), bits(P.star_rows(F, src)))
+    assert np.array_equal(bits(P.star_cols(F, src)), bits(P.star_cols(F, src)))
+    # a second factorization of the same values: the same factor and the same star
+    F2 = P.mlu(SEMIRINGS[s], g, sym=None)
+    assert np.array_equal(bits(P.Matrix(F2)), bits(C1))
