@@ -13,8 +13,10 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <type_traits>
 
 #include "pathpack_hip.h"
@@ -1780,13 +1782,15 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
 // utils.jl:261-505): one workgroup per column
 template <class T>
 __global__ __launch_bounds__(NT) void k_relabel(const T *__restrict__ X, i64 n, T *__restrict__ C, i64 ldc,
-                                               const i64 *__restrict__ invp, i64 j0) {
+                                               const i64 *__restrict__ invp, i64 j0, const int32_t *__restrict__ cols) {
     const i64 j = j0 + blockIdx.x;
-    const T *src = X + invp[j] * n;
+    const T *src = X + (cols ? (i64)cols[j] : invp[j]) * n;
     T *dst = C + (j - j0) * ldc;
     for (i64 i = threadIdx.x; i < n; i += NT) dst[i] = src[invp[i]];
 }
 
+// With `cols`, output column j - j0 is instead X's column cols[j] with its rows relabelled (C[i, j - j0] =
+// X[invp[i], cols[j]]): the columns of X in a given order (the streamed star).
 // The same for the columns [j0, j1), with the source column staged in LDS (coalesced read, gather from LDS, coalesced
 // write), for columns of
 // at most RELABEL_LDS bytes; persistent workgroups, one per CU.  Rows move in 16-byte vectors (n and ldc multiples
@@ -1798,7 +1802,8 @@ constexpr int RELABEL_NT = 1024;
 
 template <class T>
 __global__ __launch_bounds__(RELABEL_NT) void k_relabel_lds(const T *__restrict__ X, i64 n, T *__restrict__ C, i64 ldc,
-                                                           const int32_t *__restrict__ invp, i64 j0, i64 j1) {
+                                                           const int32_t *__restrict__ invp, i64 j0, i64 j1,
+                                                           const int32_t *__restrict__ cols) {
     typedef typename Vec16<T>::type V;
     typedef typename Vec16<T>::idx I;
     constexpr int VW = 16 / sizeof(T);
@@ -1808,7 +1813,7 @@ __global__ __launch_bounds__(RELABEL_NT) void k_relabel_lds(const T *__restrict_
     const int nv = (int)(n / VW);
     V buf[RV];
     auto load = [&](i64 j) {
-        const V *src = reinterpret_cast<const V *>(X + (i64)invp[j] * n);
+        const V *src = reinterpret_cast<const V *>(X + (i64)(cols ? cols[j] : invp[j]) * n);
 #pragma unroll
         for (int u = 0; u < RV; u++) {
             const int v = threadIdx.x + u * RELABEL_NT;
@@ -2250,7 +2255,7 @@ static void launch_panels(bool fwd, int dmode, bool atomic, typename S::value_ty
 template <class S>
 static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmode, typename S::value_type *X, i64 ld,
                               bool star_rows, i64 nrows, const void *pack, const RowSub *rs = nullptr,
-                              int star_lists = -1) {
+                              int star_lists = -1, const std::function<std::string(i64)> *after = nullptr) {
     const SweepPlan &Wp = *fac->sym->splan;
     const DevPlan &d = fac->plan;
     hipStream_t st = ctx->stream;
@@ -2295,6 +2300,10 @@ static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmod
             }
             launch_blocks<S>(ctx, fac, fwd, X, ld, nrows, li, rs);
             LAUNCHCHK();
+            if (after) {
+                const std::string ae = (*after)(&li - lists.data());
+                if (!ae.empty()) return ae;
+            }
             continue;
         }
         SweepArgs a;
@@ -2322,10 +2331,18 @@ static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmod
         launch_panels<S>(fwd, dmode, atomic, X, ld, a, Wp, li, star_rows ? ROWS_STAR : ROWS_ALL, nrows, fac->Dpack, pack,
                          st, rs);
         LAUNCHCHK();
+        if (after) {
+            const std::string ae = (*after)(&li - lists.data());
+            if (!ae.empty()) return ae;
+        }
     }
     if (sl && !fwd) {
         subtrees();
         LAUNCHCHK();
+        if (after) {
+            const std::string ae = (*after)((i64)lists.size());
+            if (!ae.empty()) return ae;
+        }
     }
     return "";
 }
@@ -2404,17 +2421,60 @@ template <class S> struct StarRun {
     int host;
     std::string err;
     void operator()() { err = run(); }
-    // C[:, j0:j1] <- X relabelled, into device memory at C (leading dimension ldc)
-    void relabel(const typename S::value_type *X, i64 n, typename S::value_type *C, i64 ld, i64 j0, i64 j1) {
+    // C[:, j0:j1] <- X relabelled, into device memory at C (leading dimension ldc); with `cols`, C[:, j - j0] <- X's
+    // column cols[j] with its rows relabelled, on stream `st` with at most `wgs` workgroups
+    void relabel(const typename S::value_type *X, i64 n, typename S::value_type *C, i64 ld, i64 j0, i64 j1,
+                 const int32_t *cols = nullptr, hipStream_t st = nullptr, int wgs = 0) {
         typedef typename S::value_type T;
-        hipStream_t st = ctx->stream;
+        if (!st) st = ctx->stream;
         if (j1 <= j0) return;
         constexpr i64 VW = 16 / sizeof(T);
+        const i64 g = std::min<i64>(j1 - j0, wgs > 0 ? wgs : ctx->num_cu);
         if (n * (i64)sizeof(T) <= RELABEL_LDS && n % VW == 0 && ld % VW == 0 && ((uintptr_t)C & 15) == 0)
-            k_relabel_lds<T><<<(unsigned)std::min<i64>(j1 - j0, ctx->num_cu), RELABEL_NT, 0, st>>>(
-                X, n, C, ld, fac->plan.invp32, j0, j1);
+            k_relabel_lds<T><<<(unsigned)g, RELABEL_NT, 0, st>>>(X, n, C, ld, fac->plan.invp32, j0, j1, cols);
         else
-            k_relabel<T><<<(unsigned)(j1 - j0), NT, 0, st>>>(X, n, C, ld, fac->plan.invp, j0);
+            k_relabel<T><<<(unsigned)(j1 - j0), NT, 0, st>>>(X, n, C, ld, fac->plan.invp, j0, cols);
+    }
+    // The order in which the backward sweep leaves X's columns final (a unit's columns are final once its launch has
+    // run: later launches only read them), cut into groups at list boundaries: group g is X's columns
+    // order[gend[g - 1] .. gend[g]), final after list glist[g] (the subtree launch: lists.size()).  False when the
+    // columns are not each covered once.
+    bool stream_order(std::vector<int32_t> &order, std::vector<i64> &gend, std::vector<i64> &glist, i64 group) {
+        const SweepPlan &Wp = *fac->sym->splan;
+        const i64 n = fac->sym->S.n;
+        std::vector<char> seen(n, 0);
+        order.clear();
+        gend.clear();
+        glist.clear();
+        auto take = [&](int32_t id) {
+            for (i64 c = Wp.c0[id]; c < Wp.c0[id] + Wp.w[id]; c++) {
+                if (c < 0 || c >= n || seen[c]) return false;
+                seen[c] = 1;
+                order.push_back((int32_t)c);
+            }
+            return true;
+        };
+        i64 last = 0;
+        for (size_t l = 0; l < Wp.sbwd.size(); l++) {
+            const auto &li = Wp.sbwd[l];
+            for (i64 k = li.off; k < li.off + li.cnt; k++)
+                if (!take(Wp.plist[k])) return false;
+            if ((i64)order.size() - last >= group) {
+                gend.push_back((i64)order.size());
+                glist.push_back((i64)l);
+                last = (i64)order.size();
+            }
+        }
+        // (lists after the last cut join the subtrees' group)
+        for (size_t q = 0; q + 1 < Wp.sub_ptr.size(); q++)
+            for (i64 k = Wp.sub_ptr[q]; k < Wp.sub_ptr[q + 1]; k++)
+                if (!take(Wp.sub_pan[k])) return false;
+        if ((i64)order.size() != n) return false;
+        if ((i64)order.size() > last) {
+            gend.push_back(n);
+            glist.push_back((i64)Wp.sbwd.size());
+        }
+        return true;
     }
     std::string run() {
         typedef typename S::value_type T;
@@ -2435,6 +2495,28 @@ template <class S> struct StarRun {
         std::string e = run_sweeps<S>(ctx, fac, true, 0, X, n, true, n, fac->Upack);
         if (!e.empty()) return e;
         timer_stop(ctx, 1);
+        // star into host memory, components not coupled: each group of columns is relabelled and delivered while the
+        // rest of the backward sweep runs
+        if (host && n > 0 && !fac->sym->splan->coupled) {
+            std::vector<int32_t> order;
+            std::vector<i64> gend, glist;
+            const i64 CB = chunk_cols(n);
+            if (stream_order(order, gend, glist, 1)) {
+                timer_start(ctx, 2);
+                e = stream_to_host(X, n, order, gend, glist, CB);
+                if (!e.empty()) {
+                    hipStreamSynchronize(ctx->aux_stream);
+                    hipStreamSynchronize(st);
+                    hipFreeAsync(X, st);
+                    return e;
+                }
+                timer_stop(ctx, 2);
+                timer_start(ctx, 3);
+                timer_stop(ctx, 3);
+                HIPCHK(hipFreeAsync(X, st));
+                return "";
+            }
+        }
         timer_start(ctx, 2);
         e = run_sweeps<S>(ctx, fac, false, 0, X, n, true, n, fac->Lpack);
         if (!e.empty()) return e;
@@ -2467,29 +2549,134 @@ template <class S> struct StarRun {
     // device writes one chunk while the host copies the other.  (A copy-engine transfer from a device-side chunk
     // buffer ran at half the PCIe rate in some states of the device memory pool; the kernel's writes do not depend
     // on them.)
+    // columns per chunk of the star into host memory: K >= 4 chunks of about STAR_CHUNK_BYTES
+    i64 chunk_cols(i64 n) const {
+        const i64 total = n * n * (i64)sizeof(typename S::value_type);
+        const i64 K = std::min<i64>(n, std::max<i64>(4, (total + STAR_CHUNK_BYTES - 1) / STAR_CHUNK_BYTES));
+        return (n + K - 1) / K;
+    }
+    // the two pinned chunk buffers (and their device-side addresses) for chunks of CB columns
+    std::string pinned_chunks(i64 n, i64 CB) {
+        const size_t cbytes = (size_t)(CB * n) * sizeof(typename S::value_type);
+        for (auto &ev : ctx->pev)
+            if (!ev) HIPCHK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+        if (ctx->outpin_bytes >= cbytes) return "";
+        HIPCHK(hipStreamSynchronize(ctx->stream));
+        HIPCHK(hipStreamSynchronize(ctx->aux_stream));
+        for (auto &p : ctx->outpin)
+            if (p) hipHostFree(p);
+        ctx->outpin[0] = ctx->outpin[1] = nullptr;
+        ctx->outpin_dev[0] = ctx->outpin_dev[1] = nullptr;
+        ctx->outpin_bytes = 0;
+        for (int b = 0; b < 2; b++) {
+            HIPCHK(hipHostMalloc(&ctx->outpin[b], cbytes, hipHostMallocDefault));
+            HIPCHK(hipHostGetDevicePointer(&ctx->outpin_dev[b], ctx->outpin[b], 0));
+        }
+        ctx->outpin_bytes = cbytes;
+        return "";
+    }
+    // The backward sweep queued on the context's stream with an event after each group's last list; the columns, in
+    // the order the sweep finishes them, relabelled on the second stream into the pinned buffers by chunks of CB
+    // columns (each chunk after the event of the group holding its last column), and copied by the host's worker
+    // threads into their columns of `out` (X's column j is column perm[j] of the star).  The relabel uses 32
+    // workgroups: it waits on PCIe writes, and the sweep keeps the rest of the device.
+    std::string stream_to_host(typename S::value_type *X, i64 n, const std::vector<int32_t> &order,
+                               const std::vector<i64> &gend, const std::vector<i64> &glist, i64 CB) {
+        typedef typename S::value_type T;
+        hipStream_t st = ctx->stream, as = ctx->aux_stream;
+        std::string e = pinned_chunks(n, CB);
+        if (!e.empty()) return e;
+        const i64 ng = (i64)gend.size();
+        std::vector<hipEvent_t> gev(ng, nullptr);
+        auto cleanup = [&]() {
+            for (auto &ev : gev)
+                if (ev) hipEventDestroy(ev);
+        };
+        for (auto &ev : gev)
+            if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+                cleanup();
+                return "hipEventCreate failed";
+            }
+        // the column order on the device (second stream: the sweep does not wait for it)
+        int32_t *d_order = nullptr;
+        if (ctx_alloc(ctx, (void **)&d_order, (size_t)n * sizeof(int32_t), as) != hipSuccess) {
+            cleanup();
+            return "stream-ordered allocation of the column order failed";
+        }
+        if (hipMemcpyAsync(d_order, order.data(), (size_t)n * sizeof(int32_t), hipMemcpyHostToDevice, as) != hipSuccess) {
+            cleanup();
+            return "upload of the column order failed";
+        }
+        // the sweep, recording each group's event after its last list
+        i64 gnext = 0;
+        const std::function<std::string(i64)> after = [&](i64 l) -> std::string {
+            while (gnext < ng && glist[gnext] == l) {
+                if (hipEventRecord(gev[gnext], st) != hipSuccess) return "hipEventRecord failed";
+                gnext++;
+            }
+            return "";
+        };
+        e = run_sweeps<S>(ctx, fac, false, 0, X, n, true, n, fac->Lpack, nullptr, -1, &after);
+        while (e.empty() && gnext < ng) e = after(glist[gnext]);   // (groups after the last list run: none expected)
+        if (!e.empty()) {
+            hipStreamSynchronize(as);
+            hipFreeAsync(d_order, as);
+            cleanup();
+            return e;
+        }
+        // chunks of CB consecutive positions of the order (the last one shorter), each after the group of its last
+        // position: (first position, end, group)
+        std::vector<std::array<i64, 3>> ch;
+        for (i64 k = 0; k < n; k += CB) {
+            const i64 k1 = std::min(n, k + CB);
+            const i64 g = std::upper_bound(gend.begin(), gend.end(), k1 - 1) - gend.begin();
+            ch.push_back({k, k1, std::min(g, ng - 1)});
+        }
+        const i64 nchunk = (i64)ch.size();
+        i64 waited = -1;   // last group the second stream waits for
+        auto produce = [&](i64 c) -> std::string {
+            const int b = (int)(c & 1);
+            const i64 g = ch[c][2];
+            if (g > waited) {
+                HIPCHK(hipStreamWaitEvent(as, gev[g], 0));
+                waited = g;
+            }
+            relabel(X, n, (T *)ctx->outpin_dev[b], n, ch[c][0], ch[c][1], d_order, as, 32);
+            LAUNCHCHK();
+            HIPCHK(hipEventRecord(ctx->pev[b], as));
+            return "";
+        };
+        for (i64 c = 0; c < std::min<i64>(2, nchunk) && e.empty(); c++) e = produce(c);
+        for (i64 c = 0; c < nchunk && e.empty(); c++) {
+            const int b = (int)(c & 1);
+            hipError_t he = hipEventSynchronize(ctx->pev[b]);
+            if (he != hipSuccess) {
+                e = std::string("hipEventSynchronize: ") + hipGetErrorString(he);
+                break;
+            }
+            const T *src = (const T *)ctx->outpin[b];
+            const i64 k0 = ch[c][0], m = ch[c][1] - k0;
+            const int nt = (int)std::max<i64>(1, std::min<i64>(16, (m * n * (i64)sizeof(T)) >> 22));   // 4 MiB a thread
+            const i64 *perm = fac->sym->S.perm.data();
+            pool_run(nt, [&](int t) {
+                for (i64 k = m * t / nt; k < m * (t + 1) / nt; k++)
+                    std::memcpy((T *)out + perm[order[k0 + k]] * ldc, src + k * n, (size_t)n * sizeof(T));
+            });
+            if (c + 2 < nchunk) e = produce(c + 2);
+        }
+        hipError_t se = hipStreamSynchronize(as);
+        hipFreeAsync(d_order, st);
+        cleanup();
+        if (e.empty() && se != hipSuccess) e = std::string("hipStreamSynchronize: ") + hipGetErrorString(se);
+        return e;
+    }
     std::string to_host(const typename S::value_type *X, i64 n) {
         typedef typename S::value_type T;
         hipStream_t st = ctx->stream;
-        const i64 total = n * n * (i64)sizeof(T);
-        const i64 K = std::min<i64>(n, std::max<i64>(4, (total + STAR_CHUNK_BYTES - 1) / STAR_CHUNK_BYTES));
-        const i64 CB = (n + K - 1) / K;   // columns per chunk
+        const i64 CB = chunk_cols(n);   // columns per chunk
         const i64 nchunk = (n + CB - 1) / CB;
-        const size_t cbytes = (size_t)(CB * n) * sizeof(T);
-        for (auto &ev : ctx->pev)
-            if (!ev) HIPCHK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
-        if (ctx->outpin_bytes < cbytes) {
-            HIPCHK(hipStreamSynchronize(st));
-            for (auto &p : ctx->outpin)
-                if (p) hipHostFree(p);
-            ctx->outpin[0] = ctx->outpin[1] = nullptr;
-            ctx->outpin_dev[0] = ctx->outpin_dev[1] = nullptr;
-            ctx->outpin_bytes = 0;
-            for (int b = 0; b < 2; b++) {
-                HIPCHK(hipHostMalloc(&ctx->outpin[b], cbytes, hipHostMallocDefault));
-                HIPCHK(hipHostGetDevicePointer(&ctx->outpin_dev[b], ctx->outpin[b], 0));
-            }
-            ctx->outpin_bytes = cbytes;
-        }
+        std::string pe = pinned_chunks(n, CB);
+        if (!pe.empty()) return pe;
         auto cols = [&](i64 k, i64 &j0, i64 &j1) {
             j0 = k * CB;
             j1 = std::min(n, j0 + CB);
