@@ -169,6 +169,10 @@ pp_status pp_destroy(pp_ctx *ctx) {
         if (e) hipEventDestroy(e);
     for (auto &p : ctx->outpin)
         if (p) hipHostFree(p);
+    for (auto &p : ctx->xfer)
+        if (p) hipHostFree(p);
+    for (auto &e : ctx->xev)
+        if (e) hipEventDestroy(e);
     if (ctx->pool) {
         // every stream is synchronized: the pool's memory goes back to the driver (the factors of a context are
         // destroyed before it)
@@ -988,18 +992,101 @@ pp_status pp_buffer_free(pp_ctx *ctx, void *dptr) {
     return PP_OK;
 }
 
+}  // extern "C"
+
+// Large transfers between pageable host memory and the device go through two pinned chunks: a copy straight
+// between pageable memory and the device runs at a few GB/s, the pinned path at the PCIe rate.  Download: a copy
+// kernel writes chunk k into pinned buffer k % 2 (its device-side address) while the host's worker threads copy chunk
+// k - 1 out; upload: the host threads fill one buffer while the copy engine moves the other.
+static constexpr size_t XFER_CHUNK = 64u << 20, XFER_MIN = 1u << 20;
+
+static std::string xfer_setup(pp_ctx *ctx) {
+    for (int b = 0; b < 2; b++) {
+        if (!ctx->xev[b] && hipEventCreateWithFlags(&ctx->xev[b], hipEventDisableTiming) != hipSuccess)
+            return "hipEventCreate failed";
+        if (ctx->xfer[b]) continue;
+        if (hipHostMalloc(&ctx->xfer[b], XFER_CHUNK, hipHostMallocDefault) != hipSuccess) return "hipHostMalloc failed";
+        if (hipHostGetDevicePointer(&ctx->xfer_dev[b], ctx->xfer[b], 0) != hipSuccess) return "hipHostGetDevicePointer failed";
+    }
+    return "";
+}
+
+static void host_copy(void *dst, const void *src, size_t bytes) {
+    const int nt = (int)std::max<size_t>(1, std::min<size_t>(16, bytes >> 22));   // 4 MiB a thread
+    pp::pool_run(nt, [&](int t) {
+        const size_t a = bytes * t / nt, z = bytes * (t + 1) / nt;
+        std::memcpy((char *)dst + a, (const char *)src + a, z - a);
+    });
+}
+
+static std::string staged_download(pp_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    std::string e = xfer_setup(ctx);
+    if (!e.empty()) return e;
+    const size_t nchunk = (bytes + XFER_CHUNK - 1) / XFER_CHUNK;
+    auto produce = [&](size_t k) -> std::string {
+        const size_t off = k * XFER_CHUNK, len = std::min(XFER_CHUNK, bytes - off);
+        std::string ce = pp::device_copy(ctx, ctx->xfer_dev[k & 1], (const char *)src + off, len);
+        if (!ce.empty()) return ce;
+        return hipEventRecord(ctx->xev[k & 1], ctx->stream) == hipSuccess ? "" : "hipEventRecord failed";
+    };
+    for (size_t k = 0; k < std::min<size_t>(2, nchunk) && e.empty(); k++) e = produce(k);
+    for (size_t k = 0; k < nchunk && e.empty(); k++) {
+        if (hipEventSynchronize(ctx->xev[k & 1]) != hipSuccess) return "hipEventSynchronize failed";
+        const size_t off = k * XFER_CHUNK, len = std::min(XFER_CHUNK, bytes - off);
+        host_copy((char *)dst + off, ctx->xfer[k & 1], len);
+        if (k + 2 < nchunk) e = produce(k + 2);
+    }
+    return e;
+}
+
+static std::string staged_upload(pp_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    std::string e = xfer_setup(ctx);
+    if (!e.empty()) return e;
+    const size_t nchunk = (bytes + XFER_CHUNK - 1) / XFER_CHUNK;
+    for (size_t k = 0; k < nchunk; k++) {
+        const int b = (int)(k & 1);
+        if (k >= 2 && hipEventSynchronize(ctx->xev[b]) != hipSuccess) return "hipEventSynchronize failed";
+        const size_t off = k * XFER_CHUNK, len = std::min(XFER_CHUNK, bytes - off);
+        host_copy(ctx->xfer[b], (const char *)src + off, len);
+        if (hipMemcpyAsync((char *)dst + off, ctx->xfer[b], len, hipMemcpyHostToDevice, ctx->stream) != hipSuccess)
+            return "hipMemcpyAsync failed";
+        if (hipEventRecord(ctx->xev[b], ctx->stream) != hipSuccess) return "hipEventRecord failed";
+    }
+    return hipStreamSynchronize(ctx->stream) == hipSuccess ? "" : "hipStreamSynchronize failed";
+}
+
+extern "C" {
+
 pp_status pp_upload(pp_ctx *ctx, void *dst, const void *src, size_t bytes) {
     if (!ctx || (bytes && (!dst || !src))) return fail(ctx, PP_EINVAL, "pp_upload: null argument");
-    if (bytes) CHECK_HIP(ctx, hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    if (!bytes) return PP_OK;
+    CHECK_HIP(ctx, hipSetDevice(ctx->device));
+    if (bytes < XFER_MIN) {
+        CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        CHECK_HIP(ctx, hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+        return PP_OK;
+    }
+    CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    std::string e = staged_upload(ctx, dst, src, bytes);
+    if (!e.empty()) {
+        hipStreamSynchronize(ctx->stream);
+        return fail(ctx, PP_EHIP, "pp_upload: " + e);
+    }
     return PP_OK;
 }
 
 pp_status pp_download(pp_ctx *ctx, void *dst, const void *src, size_t bytes) {
     if (!ctx || (bytes && (!dst || !src))) return fail(ctx, PP_EINVAL, "pp_download: null argument");
-    if (bytes) {
-        CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (!bytes) return PP_OK;
+    CHECK_HIP(ctx, hipSetDevice(ctx->device));
+    CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (bytes < XFER_MIN) {
         CHECK_HIP(ctx, hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+        return PP_OK;
     }
+    std::string e = staged_download(ctx, dst, src, bytes);
+    hipError_t se = hipStreamSynchronize(ctx->stream);
+    if (!e.empty() || se != hipSuccess) return fail(ctx, PP_EHIP, "pp_download: " + (e.empty() ? std::string(hipGetErrorString(se)) : e));
     return PP_OK;
 }
 

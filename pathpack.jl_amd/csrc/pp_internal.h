@@ -257,6 +257,9 @@ struct pp_ctx {
     void *outpin[2] = {nullptr, nullptr};
     size_t outpin_bytes = 0;
     void *outpin_dev[2] = {nullptr, nullptr};   // their device-side addresses (the relabel kernel writes them)
+    // pp_upload / pp_download of large buffers: two pinned staging chunks and their device-side addresses
+    void *xfer[2] = {nullptr, nullptr}, *xfer_dev[2] = {nullptr, nullptr};
+    hipEvent_t xev[2] = {};
 };
 
 struct pp_fac {
