@@ -259,10 +259,15 @@ __global__ __launch_bounds__(NT) void k_front_step(typename S::value_type *__res
 #pragma unroll
         for (int j = 0; j < NB; j++) v[j] = A[r + (i64)(off + min(j, b - 1)) * n];
     }
-    if (wave == 2 && mc > 0) {
-        const int c = c0 + min(lane, mc - 1);
+    // the row panel's block (NB rows x the tile's TG columns) into Us, by waves 2 and 3: 32 consecutive threads read a
+    // column's NB consecutive rows (coalesced); wave 2 takes its column from Us after the barrier below
+    if (wave >= 2 && mc > 0) {
+        const int t = threadIdx.x - 128;
 #pragma unroll
-        for (int i = 0; i < NB; i++) v[i] = A[(off + min(i, b - 1)) + (i64)c * n];
+        for (int q = 0; q < NB * TG / 128; q++) {
+            const int idx = t + 128 * q, row = idx % NB, col = idx / NB;
+            Us[row][col] = A[(off + min(row, b - 1)) + (i64)(c0 + min(col, mc - 1)) * n];
+        }
     }
     if (wave == 0) {
         // LU of D in registers (dense/sgetrf.jl:151-175, the operations of lds_lu in the same order): lane i holds
@@ -272,6 +277,11 @@ __global__ __launch_bounds__(NT) void k_front_step(typename S::value_type *__res
         T d[NB];
 #pragma unroll
         for (int j = 0; j < NB; j++) d[j] = A[(off + ic) + (i64)(off + min(j, b - 1)) * n];
+        // Rows at or above the pivot keep their entries.  Except for PlusProd, their multiplier is the semiring zero
+        // instead of a select per entry: zero (x) u (+) d = d for every u these semirings can hold (min/max drop the
+        // NaN of inf - inf), and the entries stay canonical, so the update is readlane, (x), (+).  PlusProd selects:
+        // 0 * inf is NaN.
+        constexpr bool zero_mul = S::id != S_PLUSPROD;
 #pragma unroll
         for (int k = 0; k < NB; k++) {
             const bool below = i > k;
@@ -279,10 +289,15 @@ __global__ __launch_bounds__(NT) void k_front_step(typename S::value_type *__res
                 const T l = S::prod(d[k], S::star(bcast_lane(d[k], k)));
                 d[k] = below ? l : d[k];
             }
+            const T lm = below ? d[k] : S::zero();
 #pragma unroll
             for (int j = k + 1; j < NB; j++) {
-                const T w = S::muladd(d[k], bcast_lane(d[j], k), d[j]);
-                d[j] = below ? w : d[j];
+                if constexpr (zero_mul) {
+                    d[j] = S::muladd(lm, bcast_lane(d[j], k), d[j]);
+                } else {
+                    const T w = S::muladd(d[k], bcast_lane(d[j], k), d[j]);
+                    d[j] = below ? w : d[j];
+                }
             }
         }
         if (lane < NB) {
@@ -298,17 +313,14 @@ __global__ __launch_bounds__(NT) void k_front_step(typename S::value_type *__res
     }
     __syncthreads();
     if (wave == 1 && mr > 0) {
-        // rows of the column panel: x <- x U_D*
+        // rows of the column panel: x <- x U_D*, right-looking (x_i is final after step i and then updates every later
+        // x_j): each x_j receives the terms i = 0, 1, ... in the order of the one-by-one substitution, and a step's
+        // updates are independent of each other
 #pragma unroll
-        for (int j = 0; j < NB; j++) {
-            T s = v[j];
+        for (int i = 0; i < NB; i++) {
+            if (!S::integral) v[i] = S::prod(v[i], S::star(Dl[i + i * LDd]));
 #pragma unroll
-            for (int i = 0; i < j; i++) s = S::muladd(v[i], Dl[i + j * LDd], s);
-            if (!S::integral) s = S::prod(s, S::star(Dl[j + j * LDd]));
-            v[j] = s;
-            // compiler barrier: column j is computed before the LDS reads of column j + 1 are issued, which bounds
-            // the live registers
-            asm volatile("" : "+v"(v[j])::"memory");
+            for (int j = i + 1; j < NB; j++) v[j] = S::muladd(v[i], Dl[i + j * LDd], v[j]);
         }
 #pragma unroll
         for (int j = 0; j < NB; j++) Ls[j][lane] = v[j];
@@ -322,15 +334,13 @@ __global__ __launch_bounds__(NT) void k_front_step(typename S::value_type *__res
         }
     }
     if (wave == 2 && mc > 0) {
-        // columns of the row panel: y <- L_D* y
+        // columns of the row panel: y <- L_D* y, right-looking as above (L unit lower)
 #pragma unroll
-        for (int i = 0; i < NB; i++) {
-            T s = v[i];
+        for (int i = 0; i < NB; i++) v[i] = Us[i][lane];
 #pragma unroll
-            for (int k = 0; k < i; k++) s = S::muladd(Dl[i + k * LDd], v[k], s);
-            v[i] = s;
-            asm volatile("" : "+v"(v[i])::"memory");
-        }
+        for (int k = 0; k < NB; k++)
+#pragma unroll
+            for (int i = k + 1; i < NB; i++) v[i] = S::muladd(Dl[i + k * LDd], v[k], v[i]);
 #pragma unroll
         for (int i = 0; i < NB; i++) Us[i][lane] = v[i];
         if (ti == 0 && lane < mc) {
