@@ -1981,6 +1981,118 @@ __global__ __launch_bounds__(NT) void k_getrf_star(typename S::value_type *__res
     }
 }
 
+// One wave per front (4-byte elements, nb <= 64): lane r holds row r of the front in registers (a[j] = A[r, j]),
+// the factor and both stars are computed there and the pivot rows and columns are broadcast with readlane.  Every
+// entry gets the same terms in the same order as the CPU loops (k_getrf_star, the oracle): the LU pivot by pivot
+// (l = A[k, p] (x) A[p, p]*, then A[k, j] <- A[k, j] (+) l (x) A[p, j]); TU = U* by rows, lane r computing
+// X[r, j] = (X[r, j] (+) sum_{k<j} X[r, k] (x) U[k, j]) (x) U[j, j]*; TL = L* by columns, lane c computing
+// X[i, c] = X[i, c] (+) sum_{k<i} L[i, k] (x) X[k, c].  For the idempotent semirings the k-sums take two terms per
+// v_min3 / v_max3 (min and max are exact, so their grouping changes nothing); PlusProd sums them one by one.
+// TL leaves through an LDS transpose (32 rows at a time) so that every store is a coalesced column segment.
+template <class S>
+__global__ __launch_bounds__(256) void k_getrf_star_wave(typename S::value_type *__restrict__ Aall,
+                                                        typename S::value_type *__restrict__ TLall,
+                                                        typename S::value_type *__restrict__ TUall, int nb, i64 batch) {
+    typedef typename S::value_type T;
+    static_assert(sizeof(T) == 4, "128 registers of 4 bytes per lane");
+    constexpr int N = 64;
+    __shared__ T tbuf[4][32 * (N + 1)];
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const i64 f = (i64)blockIdx.x * 4 + wv;
+    if (f >= batch) return;   // whole waves; no barrier in this kernel
+    const i64 base = f * nb * nb;
+    T *G = Aall + base;
+    const bool act = lane < nb;
+    T a[N];
+#pragma unroll
+    for (int j = 0; j < N; j++) a[j] = (act && j < nb) ? G[lane + (i64)j * nb] : S::zero();
+    // the LU (sgetrf2): pivot p scales column p below it by A[p, p]*, then updates the trailing rows.  The loops
+    // run over all 64 rows and columns: a real entry (both indices < nb) only meets pivots and terms with smaller
+    // indices, so the padding (the semiring zero, then whatever the arithmetic makes of it) never reaches one.
+#pragma unroll
+    for (int p = 0; p < N; p++) {
+        const bool below = lane > p;
+        if (!S::integral) {
+            const T sp = S::star(bcast_lane(a[p], p));
+            const T l = S::prod(a[p], sp);
+            a[p] = below ? l : a[p];
+        }
+#pragma unroll
+        for (int j = p + 1; j < N; j++) {
+            const T nv = S::muladd(a[p], bcast_lane(a[j], p), a[j]);
+            a[j] = below ? nv : a[j];
+        }
+    }
+    if (act) {
+#pragma unroll
+        for (int j = 0; j < N; j++)
+            if (j < nb) G[lane + (i64)j * nb] = a[j];
+    }
+    constexpr bool PAIR = S::id != S_PLUSPROD;
+    if (TUall) {
+        T x[N];
+#pragma unroll
+        for (int j = 0; j < N; j++) x[j] = j == lane ? S::one() : S::zero();
+#pragma unroll
+        for (int j = 0; j < N; j++) {
+            T part = S::zero();
+            int k = 0;
+            if (PAIR) {
+#pragma unroll
+                for (; k + 2 <= j; k += 2)
+                    part = S::muladd2(x[k], bcast_lane(a[j], k), x[k + 1], bcast_lane(a[j], k + 1), part);
+            }
+#pragma unroll
+            for (; k < j; k++) part = S::muladd(x[k], bcast_lane(a[j], k), part);
+            T acc = S::plus(x[j], part);
+            if (!S::integral) acc = S::prod(acc, S::star(bcast_lane(a[j], j)));
+            x[j] = acc;
+        }
+        if (act) {
+            T *TU = TUall + base;
+#pragma unroll
+            for (int j = 0; j < N; j++)
+                if (j < nb) TU[lane + (i64)j * nb] = x[j];
+        }
+    }
+    if (TLall) {
+        T x[N];   // lane c: column c of L*
+#pragma unroll
+        for (int i = 0; i < N; i++) x[i] = i == lane ? S::one() : S::zero();
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            T part = S::zero();
+            int k = 0;
+            if (PAIR) {
+#pragma unroll
+                for (; k + 2 <= i; k += 2)
+                    part = S::muladd2(bcast_lane(a[k], i), x[k], bcast_lane(a[k + 1], i), x[k + 1], part);
+            }
+#pragma unroll
+            for (; k < i; k++) part = S::muladd(bcast_lane(a[k], i), x[k], part);
+            x[i] = S::plus(x[i], part);
+        }
+        // TL[i, c] = x[i] of lane c: through LDS, 32 rows at a time; then each store instruction writes 32
+        // consecutive rows of two columns
+        T *TL = TLall + base;
+        T *tb = tbuf[wv];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+#pragma unroll
+            for (int i = 0; i < 32; i++) tb[i * (N + 1) + lane] = x[32 * h + i];
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            const int r = lane & 31, c0 = lane >> 5;
+#pragma unroll
+            for (int c = 0; c < N; c += 2) {
+                const int cc = c + c0, ii = 32 * h + r;
+                if (cc < nb && ii < nb) TL[ii + (i64)cc * nb] = tb[r * (N + 1) + cc];
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+}
+
 // ===== drivers =====
 
 // Timing slots: events on the context's stream, read by pp_get_timing (no synchronization here).
@@ -2923,7 +3035,12 @@ template <class S> struct GetrfStarRun {
     std::string run() {
         typedef typename S::value_type T;
         if (batch == 0) return "";
-        k_getrf_star<S><<<(unsigned)batch, NT, 0, ctx->stream>>>((T *)A, (T *)TL, (T *)TU, (int)nb);
+        if constexpr (sizeof(T) == 4) {
+            k_getrf_star_wave<S><<<(unsigned)((batch + 3) / 4), 256, 0, ctx->stream>>>((T *)A, (T *)TL, (T *)TU,
+                                                                                     (int)nb, batch);
+        } else {
+            k_getrf_star<S><<<(unsigned)batch, NT, 0, ctx->stream>>>((T *)A, (T *)TL, (T *)TU, (int)nb);
+        }
         LAUNCHCHK();
         return "";
     }
