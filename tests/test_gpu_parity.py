@@ -588,3 +588,44 @@ def test_repeat_runs_are_bit_identical(name, s):
     # a second factorization of the same values: the same factor and the same star
     F2 = P.mlu(SEMIRINGS[s], g, sym=None)
     assert np.array_equal(bits(P.Matrix(F2)), bits(C1))
+
+
+DEVICE_STAR_GRAPHS = {
+    "grid16x17x15": lambda: W.grid((16, 17, 15)),          # blocks, panels and subtrees; n = 4080
+    "grid24x24x24": lambda: W.grid((24, 24, 24)),          # 128-column blocks; n = 13824
+    "grid64x64": lambda: W.grid((64, 64)),                 # mostly subtrees
+    "components": lambda: W.disjoint_union([W.grid((10, 10, 9)), W.grid((30, 29)), W.rgg(300, seed=5)],
+                                           isolated=3, name="components"),   # separate components, not coupled
+}
+
+
+@pytest.mark.parametrize("name", list(DEVICE_STAR_GRAPHS))
+@pytest.mark.parametrize("s,fdtype", [(O.MINPLUS, np.float32), (O.MAXMIN, np.float32), (O.PLUSPROD, np.float64),
+                                      (O.ORAND, np.float32), (O.MAXPLUS, np.float64)])
+def test_star_into_device_memory(name, s, fdtype):
+    """Matrix(F) into device memory (the relabel into a device array after the sweeps), under poisoned buffers:
+    against the oracle, and bit for bit against the star delivered into host memory (relabelled in chunks while the
+    backward sweep runs)."""
+    dtype = dtype_for(s, fdtype)
+    g = weighted(DEVICE_STAR_GRAPHS[name](), s, dtype)
+    sym = P.symbolic(g)
+    ctx = P.context(0)
+    ctx.set_poison(True)
+    try:
+        F = P.mlu(SEMIRINGS[s], g, sym=sym)
+        D = P.Matrix(F, device=True).numpy()
+        H = P.Matrix(F)
+    finally:
+        ctx.set_poison(False)
+    assert np.array_equal(bits(D), bits(H))
+    if g.n <= 5000:
+        Fo = O.factor(s, oracle_sym(sym), g.colptr, g.rowval, g.nzval)
+        assert_star_equal(s, D, O.star(Fo), rtol=rtol_for(s, dtype))
+    elif s == O.MINPLUS:
+        # the oracle's full star of n = 13824 is out of a test's budget: the star's defining equation
+        # C = I (+) C (x) A on spread columns instead (one solution for positive weights), and Dijkstra rows
+        from test_gpu_full_size import minplus_fixed_point_violations
+        cols = np.unique(np.linspace(0, g.n - 1, 96).astype(np.int64))
+        assert minplus_fixed_point_violations(D, g, cols) == 0
+        src = np.array([0, 4321, g.n - 1])
+        assert np.array_equal(D[src, :].astype(np.float64), O.dijkstra_rows(g, src))
