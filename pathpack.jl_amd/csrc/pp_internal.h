@@ -136,6 +136,8 @@ struct SweepPlan {
         i64 pCu, pC64;               // forward units (tiles x chunks) and backward tiles over the rows [rowC_lo, rowC_hi)
     };
     std::vector<List> fwd, bwd;      // in execution order (panels; the solves)
+    // the solves over all their rows: one list per level holding every width class (cls = -1), one launch each
+    std::vector<List> fwdm, bwdm;
     std::vector<List> sfwd, sbwd;    // the star's (panels of small fronts and blocks)
     // Strongly connected components coupled by N (several components and arcs between them): schedules over the
     // component DAG, one entry per level.  "up" (Y <- Y A*: rmul!, the rows and the off-diagonal blocks of the star):

@@ -828,13 +828,8 @@ template <class S> __device__ inline void atomic_plus(typename S::value_type *ad
 // chunk's targets, X[:, E_t] <- X[:, E_t] (+) sum_j x_j (x) P(j, t).  The solution is not stored: the workgroups of
 // the other chunks read the same unsolved columns, and no later forward step reads them; the backward sweep solves
 // them again as it loads them (the same operations in the same order).
-template <class S, int W, bool ATOMIC, int DMODE>
-__global__ __launch_bounds__(NT) void k_fwd(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
-                                            const typename S::value_type *__restrict__ Dpack,
-                                            const typename S::value_type *__restrict__ P) {
-    typedef typename S::value_type T;
-    __shared__ T xsh[W][TILE_ROWS];
-    int pi, tile, chunk;
+// (panel, row tile, target chunk) of a forward workgroup
+__device__ inline void locate_fwd(const SweepArgs &a, int &pi, int &tile, int &chunk) {
     if (a.pre) {
         pi = search(a.pre, a.np, blockIdx.x);
         const int u = blockIdx.x - a.pre[pi];
@@ -848,6 +843,15 @@ __global__ __launch_bounds__(NT) void k_fwd(typename S::value_type *__restrict__
         pi = search(a.cpre, a.np, u);
         chunk = u - a.cpre[pi];
     }
+}
+
+// The forward step of list entry pi (width class W) for a row tile and target chunk; xsh: W x TILE_ROWS of LDS.
+template <class S, int W, bool ATOMIC, int DMODE>
+__device__ __forceinline__ void fwd_step(typename S::value_type *__restrict__ X, i64 ld, const SweepArgs &a,
+                                         const typename S::value_type *__restrict__ Dpack,
+                                         const typename S::value_type *__restrict__ P, int pi, int tile, int chunk,
+                                         typename S::value_type (*xsh)[TILE_ROWS]) {
+    typedef typename S::value_type T;
     const int p = a.plist[pi];
     const int lo = a.pre ? a.row_lo[p] : 0, hi = a.pre ? a.row_hi[p] : a.nrows;
     const int lane = threadIdx.x & 63;
@@ -948,6 +952,37 @@ __global__ __launch_bounds__(NT) void k_fwd(typename S::value_type *__restrict__
     }
 }
 
+template <class S, int W, bool ATOMIC, int DMODE>
+__global__ __launch_bounds__(NT) void k_fwd(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
+                                            const typename S::value_type *__restrict__ Dpack,
+                                            const typename S::value_type *__restrict__ P) {
+    __shared__ typename S::value_type xsh[W][TILE_ROWS];
+    int pi, tile, chunk;
+    locate_fwd(a, pi, tile, chunk);
+    fwd_step<S, W, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh);
+}
+
+// A list whose panels have different width classes (one level of the solves): each workgroup takes its panel's
+// class.  One launch per level instead of one per level and class.
+template <class S, bool ATOMIC, int DMODE>
+__global__ __launch_bounds__(NT) void k_fwd_mixed(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
+                                                  const typename S::value_type *__restrict__ Dpack,
+                                                  const typename S::value_type *__restrict__ P) {
+    __shared__ typename S::value_type xsh[PANEL_W][TILE_ROWS];
+    int pi, tile, chunk;
+    locate_fwd(a, pi, tile, chunk);
+    const int w = a.p_w[a.plist[pi]];
+    const int cls = w <= 1 ? 0 : 32 - __builtin_clz(w - 1);
+    switch (cls) {
+    case 0: fwd_step<S, 1, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
+    case 1: fwd_step<S, 2, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
+    case 2: fwd_step<S, 4, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
+    case 3: fwd_step<S, 8, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
+    case 4: fwd_step<S, 16, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
+    default: fwd_step<S, 32, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
+    }
+}
+
 // Locate (panel, row tile) of a backward / solve workgroup.  With a prefix (star rows): panel-major over each
 // panel's own rows.  Without (one row range [row_base, row_base + nrows) for the whole list): workgroups are dealt to
 // the 8 XCDs round-robin, so XCD x gets the tiles t = x mod 8; within an XCD the workgroups run panel by panel, so a
@@ -967,14 +1002,14 @@ __device__ inline void locate_tile(const SweepArgs &a, int np, int &pi, int &til
 
 constexpr int BWD_NSET = 5;
 
+// The backward step of list entry pi (width class W) for a row tile; red: (KSPLIT - 1) W TILE_ROWS of LDS for the
+// split gather list's partial sums.
 template <class S, int W, int DMODE, int KSPLIT>
-__global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(sizeof(typename S::value_type) == 4 ? 4 : 2))) void k_sweep_bwd(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
-                                                           const typename S::value_type *__restrict__ Dpack,
-                                                           const typename S::value_type *__restrict__ Q) {
+__device__ __forceinline__ void bwd_step(typename S::value_type *__restrict__ X, i64 ld, const SweepArgs &a,
+                                         const typename S::value_type *__restrict__ Dpack,
+                                         const typename S::value_type *__restrict__ Q, int pi, int tile,
+                                         typename S::value_type *__restrict__ red) {
     typedef typename S::value_type T;
-    __shared__ T red[KSPLIT > 1 ? KSPLIT - 1 : 1][W][TILE_ROWS];
-    int pi, tile;
-    locate_tile(a, a.np, pi, tile);
     const int p = a.plist[pi];
     const int lo = a.pre ? a.row_lo[p] : a.row_base, hi = a.pre ? a.row_hi[p] : a.row_base + a.nrows;
     const int lane = threadIdx.x & 63;
@@ -1058,14 +1093,14 @@ __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(siz
     if (KSPLIT > 1) {
         if (q > 0) {
 #pragma unroll
-            for (int j = 0; j < W; j++) red[q - 1][j][lane] = acc[j];
+            for (int j = 0; j < W; j++) red[((q - 1) * W + j) * TILE_ROWS + lane] = acc[j];
         }
         __syncthreads();
         if (q != 0) return;
 #pragma unroll
         for (int qq = 0; qq < KSPLIT - 1; qq++)
 #pragma unroll
-            for (int j = 0; j < W; j++) acc[j] = S::plus(acc[j], red[qq][j][lane]);
+            for (int j = 0; j < W; j++) acc[j] = S::plus(acc[j], red[(qq * W + j) * TILE_ROWS + lane]);
     }
 #pragma unroll
     for (int j = W - 1; j >= 0; j--) {
@@ -1079,6 +1114,37 @@ __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(siz
 #pragma unroll
         for (int j = 0; j < W; j++)
             if (j < w) X[(i64)(c0 + j) * ld + r] = acc[j];
+    }
+}
+
+template <class S, int W, int DMODE, int KSPLIT>
+__global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(sizeof(typename S::value_type) == 4 ? 4 : 2))) void k_sweep_bwd(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
+                                                           const typename S::value_type *__restrict__ Dpack,
+                                                           const typename S::value_type *__restrict__ Q) {
+    __shared__ typename S::value_type red[(KSPLIT > 1 ? KSPLIT - 1 : 1) * W * TILE_ROWS];
+    int pi, tile;
+    locate_tile(a, a.np, pi, tile);
+    bwd_step<S, W, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red);
+}
+
+// A list whose panels have different width classes (one level of the solves): each workgroup takes its panel's
+// class.
+template <class S, int DMODE, int KSPLIT>
+__global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(sizeof(typename S::value_type) == 4 ? 4 : 2))) void k_sweep_bwd_mixed(typename S::value_type *__restrict__ X, i64 ld, SweepArgs a,
+                                                                 const typename S::value_type *__restrict__ Dpack,
+                                                                 const typename S::value_type *__restrict__ Q) {
+    __shared__ typename S::value_type red[(KSPLIT > 1 ? KSPLIT - 1 : 1) * PANEL_W * TILE_ROWS];
+    int pi, tile;
+    locate_tile(a, a.np, pi, tile);
+    const int w = a.p_w[a.plist[pi]];
+    const int cls = w <= 1 ? 0 : 32 - __builtin_clz(w - 1);
+    switch (cls) {
+    case 0: bwd_step<S, 1, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
+    case 1: bwd_step<S, 2, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
+    case 2: bwd_step<S, 4, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
+    case 3: bwd_step<S, 8, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
+    case 4: bwd_step<S, 16, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
+    default: bwd_step<S, 32, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
     }
 }
 
@@ -2356,11 +2422,63 @@ static void launch_blocks(pp_ctx *ctx, const pp_fac *fac, bool fwd, typename S::
     else launch_blk<S, 4, 4>(ctx, fwd, X, ld, a, fac->Hpack, fac->Bpack);
 }
 
+// A list of every width class (cls < 0) over the rows [0, nrows): the class is taken per workgroup.
+template <class S, int KS>
+static void launch_bwd_mixed(unsigned grid, int dmode, typename S::value_type *X, i64 ld, const SweepArgs &a,
+                             const typename S::value_type *D, const typename S::value_type *Pk, hipStream_t st) {
+    typedef typename S::value_type T;
+    if constexpr (bwd_lds<T, PANEL_W>(KS) <= 98304) {
+        if (dmode == 0) k_sweep_bwd_mixed<S, 0, KS><<<grid, 64 * KS, 0, st>>>(X, ld, a, D, Pk);
+        else k_sweep_bwd_mixed<S, 1, KS><<<grid, 64 * KS, 0, st>>>(X, ld, a, D, Pk);
+    }
+}
+
+template <class S>
+static void launch_list_mixed(bool fwd, int dmode, bool atomic, typename S::value_type *X, i64 ld,
+                              const SweepArgs &base, const SweepPlan &Wp, const SweepPlan::List &li, i64 nrows,
+                              const void *Dpack, const void *pack, hipStream_t st) {
+    typedef typename S::value_type T;
+    const T *D = (const T *)Dpack, *Pk = (const T *)pack;
+    SweepArgs a = base;
+    const i64 ntile = (nrows + TILE_ROWS - 1) / TILE_ROWS;
+    if (fwd) {
+        a.cpre = base.pre + li.pC;
+        a.pre = nullptr;
+        const unsigned grid = (unsigned)(ntile * Wp.tiles[li.pC + li.cnt]);
+        if (!grid) return;
+        if (atomic) {
+            if (dmode == 0) k_fwd_mixed<S, true, 0><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+            else k_fwd_mixed<S, true, 1><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+        } else {
+            if (dmode == 0) k_fwd_mixed<S, false, 0><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+            else k_fwd_mixed<S, false, 1><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
+        }
+        return;
+    }
+    a.pre = nullptr;
+    const unsigned grid = (unsigned)(li.cnt * ((ntile + 7) / 8) * 8);
+    if (!grid) return;
+    // as launch_list: split each tile's gather list over ks waves when the list has too few tiles to fill the chip
+    const i64 tiles_total = li.cnt * ntile, emean = li.esum / std::max<i64>(1, li.cnt);
+    int ks = 1;
+    while (ks < 8 && tiles_total * ks < 4096 && emean >= 64 * ks && bwd_lds<T, PANEL_W>(2 * ks) <= 98304) ks *= 2;
+    switch (ks) {
+    case 1: launch_bwd_mixed<S, 1>(grid, dmode, X, ld, a, D, Pk, st); break;
+    case 2: launch_bwd_mixed<S, 2>(grid, dmode, X, ld, a, D, Pk, st); break;
+    case 4: launch_bwd_mixed<S, 4>(grid, dmode, X, ld, a, D, Pk, st); break;
+    default: launch_bwd_mixed<S, 8>(grid, dmode, X, ld, a, D, Pk, st); break;
+    }
+}
+
 // One panel list, dispatched on its width class.
 template <class S>
 static void launch_panels(bool fwd, int dmode, bool atomic, typename S::value_type *X, i64 ld, const SweepArgs &a,
                           const SweepPlan &Wp, const SweepPlan::List &li, int rows_mode, i64 nrows, const void *Dpack,
                           const void *pack, hipStream_t st, const RowSub *rs) {
+    if (li.cls < 0) {
+        launch_list_mixed<S>(fwd, dmode, atomic, X, ld, a, Wp, li, nrows, Dpack, pack, st);
+        return;
+    }
     switch (li.cls) {
     case 0: launch_list<S, 1>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
     case 1: launch_list<S, 2>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
@@ -2382,7 +2500,9 @@ static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmod
     const DevPlan &d = fac->plan;
     hipStream_t st = ctx->stream;
     const bool sl = star_lists < 0 ? star_rows : star_lists != 0;
-    const auto &lists = sl ? (fwd ? Wp.sfwd : Wp.sbwd) : (fwd ? Wp.fwd : Wp.bwd);
+    // the solves (every panel over all rows) take one launch per level, the width classes together
+    const bool mixed = !sl && !star_rows && !rs;
+    const auto &lists = sl ? (fwd ? Wp.sfwd : Wp.sbwd) : mixed ? (fwd ? Wp.fwdm : Wp.bwdm) : (fwd ? Wp.fwd : Wp.bwd);
     if (nrows == 0) return "";
     auto subtrees = [&]() {
         typedef typename S::value_type T;

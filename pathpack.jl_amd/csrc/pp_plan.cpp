@@ -413,6 +413,23 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
     P.sbwd.clear();
     make_lists(lvA, true, P.fwd);
     make_lists(lvB, false, P.bwd);
+    // the same panels with the classes of a level in one list (wider panels first)
+    auto make_mixed = [&](const std::vector<i64> &lv, bool fwd, std::vector<SweepPlan::List> &out) {
+        i64 L = 0;
+        for (i64 p = 0; p < nu; p++) L = std::max(L, lv[p] + 1);
+        std::vector<std::vector<int32_t>> buckets(L);
+        for (i64 p = 0; p < P.np; p++)
+            if (lv[p] >= 0) buckets[lv[p]].push_back((int32_t)p);
+        for (auto &b : buckets) {
+            if (b.empty()) continue;
+            std::stable_sort(b.begin(), b.end(), [&](int32_t x, int32_t y) { return P.w[x] > P.w[y]; });
+            emit(-1, b, fwd, out);
+        }
+    };
+    P.fwdm.clear();
+    P.bwdm.clear();
+    make_mixed(lvA, true, P.fwdm);
+    make_mixed(lvB, false, P.bwdm);
     make_lists(slvA, true, P.sfwd);
     make_lists(slvB, false, P.sbwd);
     // the schedules over the component DAG (panels only, as the solves)
