@@ -799,6 +799,13 @@ __device__ inline int search(const int32_t *pre, int np, int u) {
     return lo;
 }
 
+// Element offset of column col of a column-major array with leading dimension ld: a 32 x 32 -> 64-bit product
+// (two scalar instructions for uniform operands, where the 64 x 64 product of a sign-extended index takes seven).
+// Exact: column indices are int32 and non-negative, and every leading dimension here is below 2^32.
+__device__ __forceinline__ i64 cofs(int col, i64 ld) {
+    return (i64)((uint64_t)(uint32_t)col * (uint64_t)(uint32_t)ld);
+}
+
 // X[addr] <- X[addr] (+) v by compare-and-swap on the bit pattern; returns at once when (+) leaves the value
 // unchanged (the common case for min / max / or).  Exact and order-independent for the idempotent semirings.
 // PlusProd uses the hardware's atomic add (order-dependent rounding, as any parallel sum).
@@ -872,7 +879,7 @@ __device__ __forceinline__ void fwd_step(typename S::value_type *__restrict__ X,
     T *xr = X + (valid ? r : hi - 1);
     auto ldg = [&](int g, T(&v)[4]) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = xr[(i64)E[min(tb + 4 * (4 * g + u), t1 - 1)] * ld];
+        for (int u = 0; u < 4; u++) v[u] = xr[cofs(E[min(tb + 4 * (4 * g + u), t1 - 1)], ld)];
         __builtin_amdgcn_sched_barrier(0);   // issue the loads here, ahead of the arithmetic that follows
     };
     T A[4], B[4], C[4];
@@ -885,7 +892,7 @@ __device__ __forceinline__ void fwd_step(typename S::value_type *__restrict__ X,
         const T *D = Dpack + a.p_doff[p];
 #pragma unroll
         for (int j = 0; j < W; j++) {
-            const T v = xr[(i64)(c0 + min(j, w - 1)) * ld];
+            const T v = xr[cofs(c0 + min(j, w - 1), ld)];
             x[j] = j < w ? v : S::zero();
         }
 #pragma unroll
@@ -915,7 +922,7 @@ __device__ __forceinline__ void fwd_step(typename S::value_type *__restrict__ X,
 #pragma unroll
                 for (int j = 0; j < W; j += 2) v = S::muladd2(x[j], pc[j], x[j + 1], pc[j + 1], v);
             }
-            atomic_plus<S>(X + (i64)E[t] * ld + r, v);
+            atomic_plus<S>(X + cofs(E[t], ld) + r, v);
         }
         return;
     }
@@ -933,7 +940,7 @@ __device__ __forceinline__ void fwd_step(typename S::value_type *__restrict__ X,
 #pragma unroll
                     for (int j = 0; j < W; j += 2) acc = S::muladd2(x[j], pc[j], x[j + 1], pc[j + 1], acc);
                 }
-                xr[(i64)E[t] * ld] = acc;
+                xr[cofs(E[t], ld)] = acc;
             }
         }
     };
@@ -1033,7 +1040,7 @@ __device__ __forceinline__ void bwd_step(typename S::value_type *__restrict__ X,
     const T *qp = Qp + (i64)(4 * g0) * W;
     auto ld4 = [&](const int32_t *ei, T(&v)[4]) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = xr[(i64)ei[u] * ld];
+        for (int u = 0; u < 4; u++) v[u] = xr[cofs(ei[u], ld)];
         __builtin_amdgcn_sched_barrier(0);   // issue the loads here, ahead of the arithmetic that follows
     };
     auto mad4 = [&](const T(&v)[4], const T *qq) {
@@ -1057,7 +1064,7 @@ __device__ __forceinline__ void bwd_step(typename S::value_type *__restrict__ X,
         // the panel's columns as the forward sweep left them, unsolved: finish its step x <- x D* here
 #pragma unroll
         for (int j = 0; j < W; j++) {
-            const T v = xr[(i64)(c0 + min(j, w - 1)) * ld];
+            const T v = xr[cofs(c0 + min(j, w - 1), ld)];
             acc[j] = j < w ? v : S::zero();
         }
 #pragma unroll
@@ -1085,7 +1092,7 @@ __device__ __forceinline__ void bwd_step(typename S::value_type *__restrict__ X,
             if (g + u < ngw) mad4(xs[u], qp + 4 * u * W);
     }
     for (int k = kt; k < kend; k++) {
-        const T v0 = xr[(i64)E[k] * ld];
+        const T v0 = xr[cofs(E[k], ld)];
         const T *q0 = Qp + (i64)k * W;
 #pragma unroll
         for (int j = 0; j < W; j++) acc[j] = S::muladd(v0, q0[j], acc[j]);
@@ -1113,7 +1120,7 @@ __device__ __forceinline__ void bwd_step(typename S::value_type *__restrict__ X,
     if (valid) {
 #pragma unroll
         for (int j = 0; j < W; j++)
-            if (j < w) X[(i64)(c0 + j) * ld + r] = acc[j];
+            if (j < w) X[cofs(c0 + j, ld) + r] = acc[j];
     }
 }
 
@@ -1174,7 +1181,7 @@ __device__ inline void sub_fwd_panel(typename S::value_type *__restrict__ X, i64
     T x[W];
 #pragma unroll
     for (int j = 0; j < W; j++) {
-        const T v = xr[(i64)(c0 + min(j, w - 1)) * ld];
+        const T v = xr[cofs(c0 + min(j, w - 1), ld)];
         x[j] = j < w ? v : S::zero();
     }
 #pragma unroll
@@ -1189,7 +1196,7 @@ __device__ inline void sub_fwd_panel(typename S::value_type *__restrict__ X, i64
     T A[4], B[4];
     auto ld4 = [&](int t0, T(&v)[4]) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = xr[(i64)E[min(t0 + u, e - 1)] * ld];
+        for (int u = 0; u < 4; u++) v[u] = xr[cofs(E[min(t0 + u, e - 1)], ld)];
     };
     auto upd4 = [&](int t0, const T(&v)[4]) {
 #pragma unroll
@@ -1204,7 +1211,7 @@ __device__ inline void sub_fwd_panel(typename S::value_type *__restrict__ X, i64
 #pragma unroll
                     for (int j = 0; j < W; j += 2) acc = S::muladd2(x[j], pc[j], x[j + 1], pc[j + 1], acc);
                 }
-                if (store) xr[(i64)E[t] * ld] = acc;
+                if (store) xr[cofs(E[t], ld)] = acc;
             }
         }
     };
@@ -1234,7 +1241,7 @@ __device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64
     // gathers in groups of four, three register sets in rotation (eight loads in flight)
     auto ld4 = [&](int t0, T(&v)[4]) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = xr[(i64)E[min(t0 + u, e - 1)] * ld];
+        for (int u = 0; u < 4; u++) v[u] = xr[cofs(E[min(t0 + u, e - 1)], ld)];
     };
     auto mad4 = [&](int t0, const T(&v)[4]) {
         const T *qq = Qp + (i64)t0 * W;
@@ -1266,7 +1273,7 @@ __device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64
     if (r >= a.rowA_lo[p] && r < a.rowA_hi[p]) {
 #pragma unroll
         for (int j = 0; j < W; j++) {
-            const T v = xr[(i64)(c0 + min(j, w - 1)) * ld];
+            const T v = xr[cofs(c0 + min(j, w - 1), ld)];
             acc[j] = j < w ? v : S::zero();
         }
 #pragma unroll
@@ -1304,7 +1311,7 @@ __device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64
     if (store) {
 #pragma unroll
         for (int j = 0; j < W; j++)
-            if (j < w) X[(i64)(c0 + j) * ld + r] = acc[j];
+            if (j < w) X[cofs(c0 + j, ld) + r] = acc[j];
     }
 }
 
@@ -1624,10 +1631,10 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
 #pragma unroll
         for (int q = 0; q < AQ; q++) {
             const int ev = (tid + 256 * q) * VW, r = ev % BM, k = k0 + ev / BM;
-            i64 col;
+            int col;
             if constexpr (FWD) col = c0 + min(k, w - 1);
             else col = k < w ? c0 + k : (k < K ? pick(q) : c0);
-            srcs[q] = X + (r0 + r) + col * ld;
+            srcs[q] = X + (r0 + r) + cofs(col, ld);
         }
 #pragma unroll
         for (int q = 0; q < AQ; q++) {
@@ -1710,7 +1717,7 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int t = ct * BN + wc + 16 * bj + 4 * r + lq;
-                    macc[bi][bj][r] = (FWD && row >= lo && row < hi && t < e) ? X[row + (i64)E[t] * ld] : 0.0;
+                    macc[bi][bj][r] = (FWD && row >= lo && row < hi && t < e) ? X[row + cofs(E[t], ld)] : 0.0;
                 }
         }
     }
@@ -1729,7 +1736,7 @@ __global__ __launch_bounds__(256) void k_blk(typename S::value_type *__restrict_
             for (int j = 0; j < TN; j++) {
                 const int t = ct * BN + colof(j);
                 if (t >= e) continue;
-                const T *src = X + r + (i64)E[t] * ld;
+                const T *src = X + r + cofs(E[t], ld);
                 if (st == 2 && vec) {
 #pragma unroll
                     for (int h = 0; h < 4; h += VW) {
