@@ -806,6 +806,13 @@ __device__ __forceinline__ i64 cofs(int col, i64 ld) {
     return (i64)((uint64_t)(uint32_t)col * (uint64_t)(uint32_t)ld);
 }
 
+// p[i] of a plan array (read-only for the whole launch) through the constant address space: a wave-uniform index
+// then gives a scalar load even after the kernel's own stores to X, which the compiler cannot otherwise tell apart
+// from the plan's memory (it would load the index into a vector register and wait for it before the gather).
+template <class T> __device__ __forceinline__ T cld(const T *p, i64 i) {
+    return ((const __attribute__((address_space(4))) T *)p)[i];
+}
+
 // X[addr] <- X[addr] (+) v by compare-and-swap on the bit pattern; returns at once when (+) leaves the value
 // unchanged (the common case for min / max / or).  Exact and order-independent for the idempotent semirings.
 // PlusProd uses the hardware's atomic add (order-dependent rounding, as any parallel sum).
@@ -879,7 +886,7 @@ __device__ __forceinline__ void fwd_step(typename S::value_type *__restrict__ X,
     T *xr = X + (valid ? r : hi - 1);
     auto ldg = [&](int g, T(&v)[4]) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = xr[cofs(E[min(tb + 4 * (4 * g + u), t1 - 1)], ld)];
+        for (int u = 0; u < 4; u++) v[u] = xr[cofs(cld(E, min(tb + 4 * (4 * g + u), t1 - 1)), ld)];
         __builtin_amdgcn_sched_barrier(0);   // issue the loads here, ahead of the arithmetic that follows
     };
     T A[4], B[4], C[4];
@@ -922,7 +929,7 @@ __device__ __forceinline__ void fwd_step(typename S::value_type *__restrict__ X,
 #pragma unroll
                 for (int j = 0; j < W; j += 2) v = S::muladd2(x[j], pc[j], x[j + 1], pc[j + 1], v);
             }
-            atomic_plus<S>(X + cofs(E[t], ld) + r, v);
+            atomic_plus<S>(X + cofs(cld(E, t), ld) + r, v);
         }
         return;
     }
@@ -940,7 +947,7 @@ __device__ __forceinline__ void fwd_step(typename S::value_type *__restrict__ X,
 #pragma unroll
                     for (int j = 0; j < W; j += 2) acc = S::muladd2(x[j], pc[j], x[j + 1], pc[j + 1], acc);
                 }
-                xr[cofs(E[t], ld)] = acc;
+                xr[cofs(cld(E, t), ld)] = acc;
             }
         }
     };
@@ -1173,10 +1180,10 @@ __device__ inline void sub_fwd_panel(typename S::value_type *__restrict__ X, i64
                                      bool store, const typename S::value_type *__restrict__ Dpack,
                                      const typename S::value_type *__restrict__ Pk) {
     typedef typename S::value_type T;
-    const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
-    const T *D = Dpack + a.p_doff[p];
-    const T *Pp = Pk + a.p_poff[p];
-    const int32_t *E = a.Eidx + a.p_eoff[p];
+    const int w = cld(a.p_w, p), e = cld(a.p_e, p), c0 = cld(a.p_c0, p);
+    const T *D = Dpack + cld(a.p_doff, p);
+    const T *Pp = Pk + cld(a.p_poff, p);
+    const int32_t *E = a.Eidx + cld(a.p_eoff, p);
     T *xr = X + r;
     T x[W];
 #pragma unroll
@@ -1196,7 +1203,7 @@ __device__ inline void sub_fwd_panel(typename S::value_type *__restrict__ X, i64
     T A[4], B[4];
     auto ld4 = [&](int t0, T(&v)[4]) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = xr[cofs(E[min(t0 + u, e - 1)], ld)];
+        for (int u = 0; u < 4; u++) v[u] = xr[cofs(cld(E, min(t0 + u, e - 1)), ld)];
     };
     auto upd4 = [&](int t0, const T(&v)[4]) {
 #pragma unroll
@@ -1211,7 +1218,7 @@ __device__ inline void sub_fwd_panel(typename S::value_type *__restrict__ X, i64
 #pragma unroll
                     for (int j = 0; j < W; j += 2) acc = S::muladd2(x[j], pc[j], x[j + 1], pc[j + 1], acc);
                 }
-                if (store) xr[cofs(E[t], ld)] = acc;
+                if (store) xr[cofs(cld(E, t), ld)] = acc;
             }
         }
     };
@@ -1232,24 +1239,38 @@ __device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64
                                      bool store, const typename S::value_type *__restrict__ Dpack,
                                      const typename S::value_type *__restrict__ Qk) {
     typedef typename S::value_type T;
-    const int w = a.p_w[p], e = a.p_e[p], c0 = a.p_c0[p];
-    const T *D = Dpack + a.p_doff[p];
-    const T *Qp = Qk + a.p_poff[p];
-    const int32_t *E = a.Eidx + a.p_eoff[p];
+    const int w = cld(a.p_w, p), e = cld(a.p_e, p), c0 = cld(a.p_c0, p);
+    const T *D = Dpack + cld(a.p_doff, p);
+    const T *Qp = Qk + cld(a.p_poff, p);
+    const int32_t *E = a.Eidx + cld(a.p_eoff, p);
     const T *xr = X + r;
     T acc[W];
     // gathers in groups of four, three register sets in rotation (eight loads in flight)
     auto ld4 = [&](int t0, T(&v)[4]) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = xr[cofs(E[min(t0 + u, e - 1)], ld)];
+        for (int u = 0; u < 4; u++) v[u] = xr[cofs(cld(E, min(t0 + u, e - 1)), ld)];
     };
     auto mad4 = [&](int t0, const T(&v)[4]) {
         const T *qq = Qp + (i64)t0 * W;
         if (t0 + 4 <= e) {
+            // in chunks of 8 columns; a chunk's pack pointer passes through an empty asm that takes the 8 results of
+            // the chunk before (of the previous group, for the first), so its scalar loads cannot be hoisted above
+            // that chunk: 32 pack scalars live at a time rather than the whole loop body's (which spill into vector
+            // lanes, a readlane per operand)
+            constexpr int JC = W < 8 ? W : 8;
 #pragma unroll
-            for (int j = 0; j < W; j++) {
-                acc[j] = S::muladd2(v[0], qq[j], v[1], qq[W + j], acc[j]);
-                acc[j] = S::muladd2(v[2], qq[2 * W + j], v[3], qq[3 * W + j], acc[j]);
+            for (int jc = 0; jc < W; jc += JC) {
+                const T *qc = qq + jc;
+                if constexpr (W >= 16) {
+                    const int b = jc == 0 ? W - JC : jc - JC;
+                    asm volatile("" : "+s"(qc) : "v"(acc[b]), "v"(acc[b + 1]), "v"(acc[b + 2]), "v"(acc[b + 3]),
+                                 "v"(acc[b + 4]), "v"(acc[b + 5]), "v"(acc[b + 6]), "v"(acc[b + 7]));
+                }
+#pragma unroll
+                for (int j = 0; j < JC; j++) {
+                    acc[jc + j] = S::muladd2(v[0], cld(qc, j), v[1], cld(qc, W + j), acc[jc + j]);
+                    acc[jc + j] = S::muladd2(v[2], cld(qc, 2 * W + j), v[3], cld(qc, 3 * W + j), acc[jc + j]);
+                }
             }
         } else {
 #pragma unroll
@@ -1270,7 +1291,7 @@ __device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64
         if (4 * u < e) ld4(4 * u, xs[u]);
 #pragma unroll
     for (int j = 0; j < W; j++) acc[j] = S::zero();
-    if (r >= a.rowA_lo[p] && r < a.rowA_hi[p]) {
+    if (r >= cld(a.rowA_lo, p) && r < cld(a.rowA_hi, p)) {
 #pragma unroll
         for (int j = 0; j < W; j++) {
             const T v = xr[cofs(c0 + min(j, w - 1), ld)];
@@ -1329,11 +1350,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FWD ? 1 : 6)
     const i64 r = (i64)lo + (i64)tile * TILE_ROWS + threadIdx.x;
     const int k0 = a.ptr[s], k1 = a.ptr[s + 1];
     for (int kk = 0; kk < k1 - k0; kk++) {
-        const int p = __builtin_amdgcn_readfirstlane(a.pan[FWD ? k0 + kk : k1 - 1 - kk]);
-        const int w = a.p_w[p];
+        const int p = __builtin_amdgcn_readfirstlane(cld(a.pan, FWD ? k0 + kk : k1 - 1 - kk));
+        const int w = cld(a.p_w, p);
         // rows of this step: the panel's own rows [alo, ahi) forward, all the tile's rows backward; lanes outside
         // compute on a row inside and store nothing
-        const int plo = FWD ? a.rowA_lo[p] : lo, phi = FWD ? a.rowA_hi[p] : hi;
+        const int plo = FWD ? cld(a.rowA_lo, p) : lo, phi = FWD ? cld(a.rowA_hi, p) : hi;
         const i64 t0 = (i64)lo + (i64)tile * TILE_ROWS;
         if (plo >= phi || t0 >= phi || t0 + TILE_ROWS <= plo) continue;   // (a source subset can leave none)
         const bool store = r >= plo && r < phi;
