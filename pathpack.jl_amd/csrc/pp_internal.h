@@ -53,21 +53,28 @@ constexpr int EXTRACT_COLS = 32;  // frontal columns per factor-extraction workg
 constexpr int EIDX_PAD = 32;      // zero entries after the last gather list: sweeps read up to 16 entries ahead
 constexpr int NB = 32;         // pivot block of the blocked front factorization
 constexpr int PANEL_W = 32;    // widest sweep panel
-constexpr int NCLASS = 6;      // sweep width classes 1, 2, 4, 8, 16, 32
+constexpr int NCLASS = 8;      // sweep width classes 1, 2, 4, 8, 12, 16, 24, 32
 constexpr int TILE_ROWS = 64;    // rows per scatter / backward workgroup (one per lane, 4 waves)
 constexpr int SCATTER_T = 128;   // extension columns per scatter workgroup
 constexpr int BLK_W = 128;       // widest star block (the GEMM tile's column count)
 constexpr int BLK_K = 32;        // pack rows are padded to a multiple (of every k step of the block GEMMs)
-constexpr int BLK_CLS = 7;       // list class of star blocks with bn = BLK_W (BLK_CLS + 1: bn = BLK_W / 2)
+constexpr int BLK_CLS = NCLASS;  // list class of star blocks with bn = BLK_W (BLK_CLS + 1: bn = BLK_W / 2)
 constexpr int PREP_T = 64;       // output tile of the block-pack GEMMs
 constexpr int SUB_L = 512;       // largest star subtree: columns plus the root's separator
 constexpr long STAR_CHUNK_BYTES = 128L << 20;   // column chunk of a star written to host memory
 
-inline int width_class(int w) {
-    int c = 0;
-    while ((1 << c) < w) c++;
-    return c;
+// The width class of a panel of w columns: the narrowest of 1, 2, 4, 8, 12, 16, 24, 32 that holds it.  Its packs
+// are padded to that width, and its sweep steps run in the kernels instantiated for it.  (Classes 12 and 24 cut the
+// padded work of the common 9-12 and 17-24 column panels by a quarter against powers of two.)
+__host__ __device__ constexpr int width_class(int w) {
+    return w <= 1 ? 0 : w <= 2 ? 1 : w <= 4 ? 2 : w <= 8 ? 3 : w <= 12 ? 4 : w <= 16 ? 5 : w <= 24 ? 6 : 7;
 }
+__host__ __device__ constexpr int class_width(int c) {
+    return c < 4 ? 1 << c : (c & 1) ? 16 << ((c - 5) >> 1) : 12 << ((c - 4) >> 1);
+}
+static_assert(class_width(4) == 12 && class_width(5) == 16 && class_width(6) == 24 && class_width(7) == 32 &&
+                  class_width(NCLASS - 1) == PANEL_W,
+              "width classes");
 
 inline i64 round_up(i64 x, i64 m) { return (x + m - 1) / m * m; }
 // The star's cut of a front wider than PANEL_W: blocks of BLK_W columns while more than 3/4 BLK_W remain, then one

@@ -729,20 +729,18 @@ __global__ __launch_bounds__(NT) void k_build_packs(const typename S::value_type
     typedef typename S::value_type T;
     const int p = blockIdx.x;
     const int f = p_front[p], w = p_w[p], e = p_e[p], lo = p_lo[p];
-    int Wc = 1;
-    while (Wc < w) Wc <<= 1;
+    const int Wc = class_width(width_class(w));
     const int a = nn[f], c = nj[f] - a;
     const int lj0 = p_c0[p] - (int)Rptr[f];
     const T *D = LD + Dptr[f];
     const T *Lf = LL + Lptr[f];   // c x a
     const T *Uf = UL + Lptr[f];   // a x c
-    const int sh = __builtin_ctz(Wc);
     for (int q = threadIdx.x; q < Wc * Wc; q += NT) {
-        const int i = q & (Wc - 1), j = q >> sh;
+        const int j = q / Wc, i = q - j * Wc;
         Dpack[p_doff[p] + q] = (i < w && j < w) ? D[(lj0 + i) + (i64)(lj0 + j) * a] : S::zero();
     }
     for (int q = threadIdx.x; q < Wc * e; q += NT) {
-        const int j = q & (Wc - 1), t = q >> sh;   // element (j, t) at t*Wc + j
+        const int t = q / Wc, j = q - t * Wc;      // element (j, t) at t*Wc + j
         const int col = lo + t;                    // local index of the extension column
         T u = S::zero(), l = S::zero();
         if (j < w) {
@@ -986,13 +984,15 @@ __global__ __launch_bounds__(NT) void k_fwd_mixed(typename S::value_type *__rest
     int pi, tile, chunk;
     locate_fwd(a, pi, tile, chunk);
     const int w = a.p_w[a.plist[pi]];
-    const int cls = w <= 1 ? 0 : 32 - __builtin_clz(w - 1);
+    const int cls = width_class(w);
     switch (cls) {
     case 0: fwd_step<S, 1, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
     case 1: fwd_step<S, 2, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
     case 2: fwd_step<S, 4, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
     case 3: fwd_step<S, 8, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
-    case 4: fwd_step<S, 16, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
+    case 4: fwd_step<S, 12, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
+    case 5: fwd_step<S, 16, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
+    case 6: fwd_step<S, 24, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
     default: fwd_step<S, 32, ATOMIC, DMODE>(X, ld, a, Dpack, P, pi, tile, chunk, xsh); break;
     }
 }
@@ -1151,13 +1151,15 @@ __global__ __launch_bounds__(64 * KSPLIT) __attribute__((amdgpu_waves_per_eu(siz
     int pi, tile;
     locate_tile(a, a.np, pi, tile);
     const int w = a.p_w[a.plist[pi]];
-    const int cls = w <= 1 ? 0 : 32 - __builtin_clz(w - 1);
+    const int cls = width_class(w);
     switch (cls) {
     case 0: bwd_step<S, 1, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
     case 1: bwd_step<S, 2, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
     case 2: bwd_step<S, 4, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
     case 3: bwd_step<S, 8, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
-    case 4: bwd_step<S, 16, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
+    case 4: bwd_step<S, 12, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
+    case 5: bwd_step<S, 16, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
+    case 6: bwd_step<S, 24, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
     default: bwd_step<S, 32, DMODE, KSPLIT>(X, ld, a, Dpack, Q, pi, tile, red); break;
     }
 }
@@ -1257,7 +1259,7 @@ __device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64
             // the chunk before (of the previous group, for the first), so its scalar loads cannot be hoisted above
             // that chunk: 32 pack scalars live at a time rather than the whole loop body's (which spill into vector
             // lanes, a readlane per operand)
-            constexpr int JC = W < 8 ? W : 8;
+            constexpr int JC = W % 8 == 0 ? 8 : W;
 #pragma unroll
             for (int jc = 0; jc < W; jc += JC) {
                 const T *qc = qq + jc;
@@ -1359,14 +1361,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FWD ? 1 : 6)
         if (plo >= phi || t0 >= phi || t0 + TILE_ROWS <= plo) continue;   // (a source subset can leave none)
         const bool store = r >= plo && r < phi;
         const i64 rr = r < plo ? plo : (r >= phi ? phi - 1 : r);
-        const int cls = w <= 1 ? 0 : 32 - __builtin_clz(w - 1);
+        const int cls = width_class(w);
         if (FWD) {
             switch (cls) {
             case 0: sub_fwd_panel<S, 1>(X, ld, a, p, rr, store, Dpack, Pk); break;
             case 1: sub_fwd_panel<S, 2>(X, ld, a, p, rr, store, Dpack, Pk); break;
             case 2: sub_fwd_panel<S, 4>(X, ld, a, p, rr, store, Dpack, Pk); break;
             case 3: sub_fwd_panel<S, 8>(X, ld, a, p, rr, store, Dpack, Pk); break;
-            case 4: sub_fwd_panel<S, 16>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            case 4: sub_fwd_panel<S, 12>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            case 5: sub_fwd_panel<S, 16>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            case 6: sub_fwd_panel<S, 24>(X, ld, a, p, rr, store, Dpack, Pk); break;
             default: sub_fwd_panel<S, 32>(X, ld, a, p, rr, store, Dpack, Pk); break;
             }
         } else {
@@ -1375,7 +1379,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FWD ? 1 : 6)
             case 1: sub_bwd_panel<S, 2>(X, ld, a, p, rr, store, Dpack, Pk); break;
             case 2: sub_bwd_panel<S, 4>(X, ld, a, p, rr, store, Dpack, Pk); break;
             case 3: sub_bwd_panel<S, 8>(X, ld, a, p, rr, store, Dpack, Pk); break;
-            case 4: sub_bwd_panel<S, 16>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            case 4: sub_bwd_panel<S, 12>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            case 5: sub_bwd_panel<S, 16>(X, ld, a, p, rr, store, Dpack, Pk); break;
+            case 6: sub_bwd_panel<S, 24>(X, ld, a, p, rr, store, Dpack, Pk); break;
             default: sub_bwd_panel<S, 32>(X, ld, a, p, rr, store, Dpack, Pk); break;
             }
         }
@@ -2463,16 +2469,25 @@ static void launch_bwd_mixed(unsigned grid, int dmode, typename S::value_type *X
 
 template <class S>
 static void launch_list_mixed(bool fwd, int dmode, bool atomic, typename S::value_type *X, i64 ld,
-                              const SweepArgs &base, const SweepPlan &Wp, const SweepPlan::List &li, i64 nrows,
-                              const void *Dpack, const void *pack, hipStream_t st) {
+                              const SweepArgs &base, const SweepPlan &Wp, const SweepPlan::List &li, int rows_mode,
+                              i64 nrows, const void *Dpack, const void *pack, hipStream_t st, const RowSub *rs) {
     typedef typename S::value_type T;
     const T *D = (const T *)Dpack, *Pk = (const T *)pack;
     SweepArgs a = base;
     const i64 ntile = (nrows + TILE_ROWS - 1) / TILE_ROWS;
     if (fwd) {
+        // as launch_list: per (64-row tile, target chunk) of each panel's rows, or of rows [0, nrows)
+        const std::vector<int32_t> &HT = rs ? rs->tiles : Wp.tiles;
         a.cpre = base.pre + li.pC;
-        a.pre = nullptr;
-        const unsigned grid = (unsigned)(ntile * Wp.tiles[li.pC + li.cnt]);
+        unsigned grid;
+        if (rows_mode != ROWS_ALL) {
+            const i64 pu = rows_mode == ROWS_OFFD ? li.pCu : li.pAu;
+            a.pre = base.pre + pu;
+            grid = (unsigned)HT[pu + li.cnt];
+        } else {
+            a.pre = nullptr;
+            grid = (unsigned)(ntile * HT[li.pC + li.cnt]);
+        }
         if (!grid) return;
         if (atomic) {
             if (dmode == 0) k_fwd_mixed<S, true, 0><<<grid, NT, 0, st>>>(X, ld, a, D, Pk);
@@ -2483,6 +2498,7 @@ static void launch_list_mixed(bool fwd, int dmode, bool atomic, typename S::valu
         }
         return;
     }
+    // backward: rows [0, nrows) of every panel (the solves)
     a.pre = nullptr;
     const unsigned grid = (unsigned)(li.cnt * ((ntile + 7) / 8) * 8);
     if (!grid) return;
@@ -2504,7 +2520,8 @@ static void launch_panels(bool fwd, int dmode, bool atomic, typename S::value_ty
                           const SweepPlan &Wp, const SweepPlan::List &li, int rows_mode, i64 nrows, const void *Dpack,
                           const void *pack, hipStream_t st, const RowSub *rs) {
     if (li.cls < 0) {
-        launch_list_mixed<S>(fwd, dmode, atomic, X, ld, a, Wp, li, nrows, Dpack, pack, st);
+        // (mixed lists: forward over any rows; backward only in the solves, over rows [0, nrows))
+        launch_list_mixed<S>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs);
         return;
     }
     switch (li.cls) {
@@ -2512,7 +2529,9 @@ static void launch_panels(bool fwd, int dmode, bool atomic, typename S::value_ty
     case 1: launch_list<S, 2>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
     case 2: launch_list<S, 4>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
     case 3: launch_list<S, 8>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
-    case 4: launch_list<S, 16>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
+    case 4: launch_list<S, 12>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
+    case 5: launch_list<S, 16>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
+    case 6: launch_list<S, 24>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
     default: launch_list<S, 32>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs); break;
     }
 }

@@ -180,7 +180,7 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
             P.e.push_back((int32_t)e);
             P.lo_ext.push_back((int32_t)lo);
             P.chunks.push_back((int32_t)std::max<i64>(1, (e + SCATTER_T - 1) / SCATTER_T));
-            const i64 Wc = (i64)1 << width_class((int)w);
+            const i64 Wc = class_width(width_class((int)w));
             P.eoff.push_back((i64)P.Eidx.size());
             for (i64 v = c0 + w; v < Rp + nn; v++) P.Eidx.push_back((int32_t)v);
             for (i64 q = S.Sptr[f]; q < S.Sptr[f + 1]; q++) P.Eidx.push_back((int32_t)S.Stgt[q]);
@@ -430,7 +430,26 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
     P.bwdm.clear();
     make_mixed(lvA, true, P.fwdm);
     make_mixed(lvB, false, P.bwdm);
-    make_lists(slvA, true, P.sfwd);
+    // the star's forward lists: per level, its panels of every width class in one list (one launch, wider panels
+    // first) and its blocks by tile width
+    {
+        i64 L = 0;
+        for (i64 p = 0; p < nu; p++) L = std::max(L, slvA[p] + 1);
+        constexpr int NC = BLK_CLS + 2;
+        std::vector<std::vector<int32_t>> buckets(L * NC);
+        for (i64 p = 0; p < nu; p++)
+            if (slvA[p] >= 0) buckets[slvA[p] * NC + (p < P.np ? 0 : unit_class(p))].push_back((int32_t)p);
+        for (i64 b = 0; b < (i64)buckets.size(); b++) {
+            auto &bk = buckets[b];
+            if (bk.empty()) continue;
+            if (b % NC == 0) {
+                std::stable_sort(bk.begin(), bk.end(), [&](int32_t x, int32_t y) { return P.w[x] > P.w[y]; });
+                emit(-1, bk, true, P.sfwd);
+            } else {
+                emit((int)(b % NC), bk, true, P.sfwd);
+            }
+        }
+    }
     make_lists(slvB, false, P.sbwd);
     // the schedules over the component DAG (panels only, as the solves)
     P.cup.clear();
@@ -485,7 +504,7 @@ SweepSizes sweep_sizes(const Symbolic &S) {
         const i64 nn = S.Rptr[f + 1] - S.Rptr[f], nj = nn + (S.Sptr[f + 1] - S.Sptr[f]);
         for (i64 k = 0; k * PANEL_W < nn; k++) {   // panels (every front)
             const i64 w = std::min<i64>(PANEL_W, nn - k * PANEL_W), e = nj - (k * PANEL_W + w);
-            const i64 Wc = (i64)1 << width_class((int)w);
+            const i64 Wc = class_width(width_class((int)w));
             z.units++;
             z.eidx += e;
             z.npack += Wc * e;
