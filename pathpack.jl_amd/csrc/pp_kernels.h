@@ -2498,12 +2498,28 @@ static void launch_list_mixed(bool fwd, int dmode, bool atomic, typename S::valu
         }
         return;
     }
-    // backward: rows [0, nrows) of every panel (the solves)
-    a.pre = nullptr;
-    const unsigned grid = (unsigned)(li.cnt * ((ntile + 7) / 8) * 8);
+    // backward, as launch_list: per-panel row tiles (the star's rows when they differ across the list, or the rows
+    // of the second pass), the list's common star rows, or rows [0, nrows) (the solves)
+    const std::vector<int32_t> &HT = rs ? rs->tiles : Wp.tiles;
+    unsigned grid;
+    i64 nt = ntile;
+    if (rows_mode == ROWS_OFFD || (rows_mode == ROWS_STAR && !li.uniB)) {
+        const i64 pb = rows_mode == ROWS_OFFD ? li.pC64 : li.pB64;
+        a.pre = base.pre + pb;
+        grid = (unsigned)HT[pb + li.cnt];
+        nt = grid / std::max<i64>(1, li.cnt);
+    } else {
+        a.pre = nullptr;
+        if (rows_mode == ROWS_STAR) {
+            a.row_base = rs ? rs->map(li.rowB_lo) : li.rowB_lo;
+            a.nrows = (rs ? rs->map(li.rowB_hi) : li.rowB_hi) - a.row_base;
+            nt = (a.nrows + TILE_ROWS - 1) / TILE_ROWS;
+        }
+        grid = (unsigned)(li.cnt * ((nt + 7) / 8) * 8);
+    }
     if (!grid) return;
     // as launch_list: split each tile's gather list over ks waves when the list has too few tiles to fill the chip
-    const i64 tiles_total = li.cnt * ntile, emean = li.esum / std::max<i64>(1, li.cnt);
+    const i64 tiles_total = li.cnt * nt, emean = li.esum / std::max<i64>(1, li.cnt);
     int ks = 1;
     while (ks < 8 && tiles_total * ks < 4096 && emean >= 64 * ks && bwd_lds<T, PANEL_W>(2 * ks) <= 98304) ks *= 2;
     switch (ks) {
@@ -2520,7 +2536,6 @@ static void launch_panels(bool fwd, int dmode, bool atomic, typename S::value_ty
                           const SweepPlan &Wp, const SweepPlan::List &li, int rows_mode, i64 nrows, const void *Dpack,
                           const void *pack, hipStream_t st, const RowSub *rs) {
     if (li.cls < 0) {
-        // (mixed lists: forward over any rows; backward only in the solves, over rows [0, nrows))
         launch_list_mixed<S>(fwd, dmode, atomic, X, ld, a, Wp, li, rows_mode, nrows, Dpack, pack, st, rs);
         return;
     }

@@ -430,27 +430,28 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
     P.bwdm.clear();
     make_mixed(lvA, true, P.fwdm);
     make_mixed(lvB, false, P.bwdm);
-    // the star's forward lists: per level, its panels of every width class in one list (one launch, wider panels
-    // first) and its blocks by tile width
-    {
+    // the star's lists: per level, its panels of every width class in one list (one launch, wider panels first)
+    // and its blocks by tile width
+    auto make_star_lists = [&](const std::vector<i64> &lv, bool fwd, std::vector<SweepPlan::List> &out) {
         i64 L = 0;
-        for (i64 p = 0; p < nu; p++) L = std::max(L, slvA[p] + 1);
+        for (i64 p = 0; p < nu; p++) L = std::max(L, lv[p] + 1);
         constexpr int NC = BLK_CLS + 2;
         std::vector<std::vector<int32_t>> buckets(L * NC);
         for (i64 p = 0; p < nu; p++)
-            if (slvA[p] >= 0) buckets[slvA[p] * NC + (p < P.np ? 0 : unit_class(p))].push_back((int32_t)p);
+            if (lv[p] >= 0) buckets[lv[p] * NC + (p < P.np ? 0 : unit_class(p))].push_back((int32_t)p);
         for (i64 b = 0; b < (i64)buckets.size(); b++) {
             auto &bk = buckets[b];
             if (bk.empty()) continue;
             if (b % NC == 0) {
                 std::stable_sort(bk.begin(), bk.end(), [&](int32_t x, int32_t y) { return P.w[x] > P.w[y]; });
-                emit(-1, bk, true, P.sfwd);
+                emit(-1, bk, fwd, out);
             } else {
-                emit((int)(b % NC), bk, true, P.sfwd);
+                emit((int)(b % NC), bk, fwd, out);
             }
         }
-    }
-    make_lists(slvB, false, P.sbwd);
+    };
+    make_star_lists(slvA, true, P.sfwd);
+    make_star_lists(slvB, false, P.sbwd);
     // the schedules over the component DAG (panels only, as the solves)
     P.cup.clear();
     P.cdn.clear();
