@@ -406,7 +406,7 @@ def bench_getrf(args):
                     T, "f32", "16384 independent 64x64 MinPlus fronts, entries U{0..1000} with 10% +Inf, diagonal 0 "
                     "(SplitMix64 seed 0x5EED+32); A <- L+U, TL <- L*, TU <- U*; step includes a 268 MB device copy "
                     "restoring A", {"nb": nb, "batch": batch, "madds_per_front": per})
-    r["roofline"] = valu_roofline("k_getrf_star<MinPlus<float>>", madds, T,
+    r["roofline"] = valu_roofline("k_getrf_star_wave<MinPlus<float>>", madds, T,
                                   {"hbm_floor_ms": round(4.0 * A.size * 4 / HBM_PEAK * 1e3, 3)})
     if not args.no_cpu:
         sb = 512
