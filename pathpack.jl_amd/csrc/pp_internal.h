@@ -142,8 +142,8 @@ struct SweepPlan {
         i64 pT[2];                   // block lists: per-block prefix of GEMM tiles for 64 and 128 rows per tile
         i64 pCu, pC64;               // forward units (tiles x chunks) and backward tiles over the rows [rowC_lo, rowC_hi)
     };
-    std::vector<List> fwd, bwd;      // in execution order (panels; the solves)
-    // the solves over all their rows: one list per level holding every width class (cls = -1), one launch each
+    // the panels of every front (the solves, the transposed sweeps of source columns): one list per level holding
+    // every width class (cls = -1), one launch each, in execution order
     std::vector<List> fwdm, bwdm;
     std::vector<List> sfwd, sbwd;    // the star's (panels of small fronts and blocks)
     // Strongly connected components coupled by N (several components and arcs between them): schedules over the

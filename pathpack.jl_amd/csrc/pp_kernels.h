@@ -2562,9 +2562,9 @@ static std::string run_sweeps(pp_ctx *ctx, const pp_fac *fac, bool fwd, int dmod
     const DevPlan &d = fac->plan;
     hipStream_t st = ctx->stream;
     const bool sl = star_lists < 0 ? star_rows : star_lists != 0;
-    // the solves (every panel over all rows) take one launch per level, the width classes together
-    const bool mixed = !sl && !star_rows && !rs;
-    const auto &lists = sl ? (fwd ? Wp.sfwd : Wp.sbwd) : mixed ? (fwd ? Wp.fwdm : Wp.bwdm) : (fwd ? Wp.fwd : Wp.bwd);
+    // the star's lists (blocks, panels, subtrees), or panels only (the solves, and the transposed sweeps of source
+    // columns): both take one launch per level for the panels, their width classes together
+    const auto &lists = sl ? (fwd ? Wp.sfwd : Wp.sbwd) : (fwd ? Wp.fwdm : Wp.bwdm);
     if (nrows == 0) return "";
     auto subtrees = [&]() {
         typedef typename S::value_type T;

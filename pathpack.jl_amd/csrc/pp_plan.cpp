@@ -379,17 +379,7 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
         }
     };
     // the lists of the units with lv >= 0: by level (increasing), then width class
-    auto make_lists = [&](const std::vector<i64> &lv, bool fwd, std::vector<SweepPlan::List> &out) {
-        i64 L = 0;
-        for (i64 p = 0; p < nu; p++) L = std::max(L, lv[p] + 1);
-        constexpr int NC = BLK_CLS + 2;
-        std::vector<std::vector<int32_t>> buckets(L * NC);
-        for (i64 p = 0; p < nu; p++)
-            if (lv[p] >= 0) buckets[lv[p] * NC + unit_class(p)].push_back((int32_t)p);
-        for (i64 b = 0; b < (i64)buckets.size(); b++)
-            if (!buckets[b].empty()) emit((int)(b % NC), buckets[b], fwd, out);
-    };
-    // the same for a subset of the units
+    // the lists of a subset of the units with lv >= 0: by level (increasing), then width class
     auto make_lists_of = [&](const std::vector<int32_t> &units, const std::vector<i64> &lv, bool fwd,
                              std::vector<SweepPlan::List> &out) {
         std::vector<std::pair<i64, int32_t>> key;   // (level * classes + class, unit)
@@ -407,13 +397,9 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
     };
     P.plist.clear();
     P.tiles.clear();
-    P.fwd.clear();
-    P.bwd.clear();
     P.sfwd.clear();
     P.sbwd.clear();
-    make_lists(lvA, true, P.fwd);
-    make_lists(lvB, false, P.bwd);
-    // the same panels with the classes of a level in one list (wider panels first)
+    // the panels (every front's) by level, the width classes of a level in one list (wider panels first)
     auto make_mixed = [&](const std::vector<i64> &lv, bool fwd, std::vector<SweepPlan::List> &out) {
         i64 L = 0;
         for (i64 p = 0; p < nu; p++) L = std::max(L, lv[p] + 1);
@@ -566,8 +552,8 @@ void build_row_subset(const SweepPlan &P, const Symbolic &S, RowSub &R) {
                 });
             }
     };
-    for (const auto &li : P.fwd) redo(li, true);
-    for (const auto &li : P.bwd) redo(li, false);
+    for (const auto &li : P.fwdm) redo(li, true);
+    for (const auto &li : P.bwdm) redo(li, false);
     for (const auto &li : P.sfwd) redo(li, true);
     for (const auto &li : P.sbwd) redo(li, false);
     // subtrees
