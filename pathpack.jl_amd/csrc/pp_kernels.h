@@ -1187,6 +1187,8 @@ __device__ inline void sub_fwd_panel(typename S::value_type *__restrict__ X, i64
     const T *Pp = Pk + cld(a.p_poff, p);
     const int32_t *E = a.Eidx + cld(a.p_eoff, p);
     T *xr = X + r;
+    // (a group's four indices are read unclamped, so they merge into one scalar load: up to three entries past the
+    // list are the next panel's or the zero padding after the last list, in range, and their loads go unused)
     T x[W];
 #pragma unroll
     for (int j = 0; j < W; j++) {
@@ -1205,7 +1207,7 @@ __device__ inline void sub_fwd_panel(typename S::value_type *__restrict__ X, i64
     T A[4], B[4];
     auto ld4 = [&](int t0, T(&v)[4]) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = xr[cofs(cld(E, min(t0 + u, e - 1)), ld)];
+        for (int u = 0; u < 4; u++) v[u] = xr[cofs(cld(E, t0 + u), ld)];
     };
     auto upd4 = [&](int t0, const T(&v)[4]) {
 #pragma unroll
@@ -1250,7 +1252,7 @@ __device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64
     // gathers in groups of four, three register sets in rotation (eight loads in flight)
     auto ld4 = [&](int t0, T(&v)[4]) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = xr[cofs(cld(E, min(t0 + u, e - 1)), ld)];
+        for (int u = 0; u < 4; u++) v[u] = xr[cofs(cld(E, t0 + u), ld)];
     };
     auto mad4 = [&](int t0, const T(&v)[4]) {
         const T *qq = Qp + (i64)t0 * W;
