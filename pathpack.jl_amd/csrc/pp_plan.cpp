@@ -1,9 +1,16 @@
 // pp_plan.cpp -- host construction of the device plans (see pp_internal.h).
 #include <algorithm>
+#include <atomic>
 
 #include "pp_internal.h"
 
 namespace pp {
+
+namespace {
+// Workers to ask the analysis's thread pool for, for a loop of `count` items: one per 8192 items, at most 16 (the
+// loops take their items in chunks, so any number of workers that the pool runs covers them).
+int plan_workers(i64 count) { return (int)std::min<i64>(16, std::max<i64>(1, count / 8192)); }
+}  // namespace
 
 std::string build_factor_plan(const Symbolic &S, FactorPlan &P) {
     const i64 nf = S.nf;
@@ -38,23 +45,34 @@ std::string build_factor_plan(const Symbolic &S, FactorPlan &P) {
             for (i64 f = 0; f < nf; f++)
                 if (S.parent[f] >= 0) kid[pos[S.parent[f]]++] = (int32_t)f;
         }
-        std::vector<int32_t> where(S.n, -1);
-        for (i64 p = 0; p < nf; p++) {
-            if (kids[p + 1] == kids[p]) continue;
-            const i64 a = S.Rptr[p + 1] - S.Rptr[p];
-            for (i64 v = S.Rptr[p]; v < S.Rptr[p + 1]; v++) where[v] = (int32_t)(v - S.Rptr[p]);
-            for (i64 q = S.Sptr[p]; q < S.Sptr[p + 1]; q++) where[S.Stgt[q]] = (int32_t)(a + (q - S.Sptr[p]));
-            for (int32_t k = kids[p]; k < kids[p + 1]; k++) {
-                const int32_t f = kid[k];
-                for (i64 q = S.Sptr[f]; q < S.Sptr[f + 1]; q++) {
-                    const int32_t r = where[S.Stgt[q]];
-                    if (r < 0) return "separator not contained in the parent's bag";
-                    P.relpos[q] = r;
+        // parents in chunks of 64 taken in turn by the pool's workers, each with its own map (every child's
+        // positions are written by its parent's worker alone)
+        const int nw = plan_workers((i64)S.Stgt.size());
+        std::atomic<i64> next(0);
+        std::atomic<bool> bad(false);
+        auto work = [&](int) {
+            std::vector<int32_t> where(S.n, -1);
+            for (i64 p0; (p0 = next.fetch_add(64)) < nf && !bad.load(std::memory_order_relaxed);)
+                for (i64 p = p0; p < std::min<i64>(nf, p0 + 64); p++) {
+                    if (kids[p + 1] == kids[p]) continue;
+                    const i64 a = S.Rptr[p + 1] - S.Rptr[p];
+                    for (i64 v = S.Rptr[p]; v < S.Rptr[p + 1]; v++) where[v] = (int32_t)(v - S.Rptr[p]);
+                    for (i64 q = S.Sptr[p]; q < S.Sptr[p + 1]; q++) where[S.Stgt[q]] = (int32_t)(a + (q - S.Sptr[p]));
+                    for (int32_t k = kids[p]; k < kids[p + 1]; k++) {
+                        const int32_t f = kid[k];
+                        for (i64 q = S.Sptr[f]; q < S.Sptr[f + 1]; q++) {
+                            const int32_t r = where[S.Stgt[q]];
+                            if (r < 0) bad.store(true);
+                            P.relpos[q] = r;
+                        }
+                    }
+                    for (i64 v = S.Rptr[p]; v < S.Rptr[p + 1]; v++) where[v] = -1;
+                    for (i64 q = S.Sptr[p]; q < S.Sptr[p + 1]; q++) where[S.Stgt[q]] = -1;
                 }
-            }
-            for (i64 v = S.Rptr[p]; v < S.Rptr[p + 1]; v++) where[v] = -1;
-            for (i64 q = S.Sptr[p]; q < S.Sptr[p + 1]; q++) where[S.Stgt[q]] = -1;
-        }
+        };
+        if (nw > 1) pool_run(nw, work);
+        else work(0);
+        if (bad.load()) return "separator not contained in the parent's bag";
     }
     // children
     P.chptr.assign(nf + 1, 0);
@@ -70,9 +88,20 @@ std::string build_factor_plan(const Symbolic &S, FactorPlan &P) {
     // entries of A
     // (an arc between two strongly connected components belongs to N, not to a front: position -1, skipped)
     P.entry_pos.resize(S.nnz);
-    for (i64 p = 0; p < S.nnz; p++) {
-        const i64 f = S.entry_front[p];
-        P.entry_pos[p] = f < 0 ? -1 : P.Foff[f] + S.entry_row[p] + (i64)S.entry_col[p] * P.nj[f];
+    {
+        // chunks taken in turn (the pool may run fewer workers than asked)
+        constexpr i64 CH = 8192;
+        std::atomic<i64> next(0);
+        auto work = [&](int) {
+            for (i64 p0; (p0 = next.fetch_add(CH)) < S.nnz;)
+                for (i64 p = p0; p < std::min<i64>(S.nnz, p0 + CH); p++) {
+                    const i64 f = S.entry_front[p];
+                    P.entry_pos[p] = f < 0 ? -1 : P.Foff[f] + S.entry_row[p] + (i64)S.entry_col[p] * P.nj[f];
+                }
+        };
+        const int nw = plan_workers(S.nnz);
+        if (nw > 1) pool_run(nw, work);
+        else work(0);
     }
     // heights
     std::vector<i64> h(nf, 0);
