@@ -918,7 +918,7 @@ __device__ __forceinline__ void fwd_step(typename S::value_type *__restrict__ X,
         for (int j = 0; j < W; j++) x[j] = xsh[j][lane];
     }
     if (ATOMIC) {
-        for (int t = tb; t < t1; t += 4) {
+        auto contribution = [&](int t) {
             const T *pc = Pp + (i64)t * W;
             T v = S::zero();
             if (W == 1) {
@@ -927,7 +927,38 @@ __device__ __forceinline__ void fwd_step(typename S::value_type *__restrict__ X,
 #pragma unroll
                 for (int j = 0; j < W; j += 2) v = S::muladd2(x[j], pc[j], x[j + 1], pc[j + 1], v);
             }
-            atomic_plus<S>(X + cofs(cld(E, t), ld) + r, v);
+            return v;
+        };
+        if constexpr (std::is_same<S, PlusProd<T>>::value) {
+            for (int t = tb; t < t1; t += 4) atomic_plus<S>(X + cofs(cld(E, t), ld) + r, contribution(t));
+        } else {
+            // (+) is min, max or or: the current values of four targets are loaded together, then each
+            // contribution goes in by compare-and-swap from its loaded value.  A value changed since the load has
+            // moved further in the direction of (+), so a contribution that the loaded value absorbs is absorbed
+            // by the current one too; a failed swap retries from the value it returns.
+            typedef typename std::conditional<sizeof(T) == 8, unsigned long long, unsigned int>::type U;
+            for (int t0 = tb; t0 < t1; t0 += 16) {
+                U *ad[4];
+                U old[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    ad[u] = reinterpret_cast<U *>(X + cofs(cld(E, min(t0 + 4 * u, t1 - 1)), ld) + r);
+                    old[u] = __hip_atomic_load(ad[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    if (t0 + 4 * u >= t1) break;
+                    const T c = contribution(t0 + 4 * u);
+                    U o = old[u];
+                    while (true) {
+                        const U nb = __builtin_bit_cast(U, S::plus(__builtin_bit_cast(T, o), c));
+                        if (nb == o) break;
+                        const U prev = atomicCAS(ad[u], o, nb);
+                        if (prev == o) break;
+                        o = prev;
+                    }
+                }
+            }
         }
         return;
     }
