@@ -936,28 +936,48 @@ __device__ __forceinline__ void fwd_step(typename S::value_type *__restrict__ X,
             // contribution goes in by compare-and-swap from its loaded value.  A value changed since the load has
             // moved further in the direction of (+), so a contribution that the loaded value absorbs is absorbed
             // by the current one too; a failed swap retries from the value it returns.
+            // The four swaps of a group are issued together and checked after; the next group's loads are issued
+            // before them (two register sets in rotation).
             typedef typename std::conditional<sizeof(T) == 8, unsigned long long, unsigned int>::type U;
-            for (int t0 = tb; t0 < t1; t0 += 16) {
-                U *ad[4];
-                U old[4];
+            auto load4 = [&](int t0, U *(&ad)[4], U(&old)[4]) {
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
                     ad[u] = reinterpret_cast<U *>(X + cofs(cld(E, min(t0 + 4 * u, t1 - 1)), ld) + r);
                     old[u] = __hip_atomic_load(ad[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
+            };
+            auto swap4 = [&](int t0, U *const(&ad)[4], const U(&old)[4]) {
+                T c[4];
+                U nb[4], prev[4];
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
-                    if (t0 + 4 * u >= t1) break;
-                    const T c = contribution(t0 + 4 * u);
-                    U o = old[u];
+                    c[u] = t0 + 4 * u < t1 ? contribution(t0 + 4 * u) : S::zero();
+                    nb[u] = __builtin_bit_cast(U, S::plus(__builtin_bit_cast(T, old[u]), c[u]));
+                    prev[u] = old[u];
+                    if (t0 + 4 * u < t1 && nb[u] != old[u]) prev[u] = atomicCAS(ad[u], old[u], nb[u]);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    if (prev[u] == old[u]) continue;   // swapped, absorbed, or past the chunk
+                    U o = prev[u];                     // the swap failed: retry from the value it returned
                     while (true) {
-                        const U nb = __builtin_bit_cast(U, S::plus(__builtin_bit_cast(T, o), c));
-                        if (nb == o) break;
-                        const U prev = atomicCAS(ad[u], o, nb);
-                        if (prev == o) break;
-                        o = prev;
+                        const U n2 = __builtin_bit_cast(U, S::plus(__builtin_bit_cast(T, o), c[u]));
+                        if (n2 == o) break;
+                        const U p2 = atomicCAS(ad[u], o, n2);
+                        if (p2 == o) break;
+                        o = p2;
                     }
                 }
+            };
+            U *adA[4], *adB[4];
+            U oldA[4], oldB[4];
+            if (tb < t1) load4(tb, adA, oldA);
+            for (int t0 = tb; t0 < t1; t0 += 32) {
+                if (t0 + 16 < t1) load4(t0 + 16, adB, oldB);
+                swap4(t0, adA, oldA);
+                if (t0 + 16 >= t1) break;
+                if (t0 + 32 < t1) load4(t0 + 32, adA, oldA);
+                swap4(t0 + 16, adB, oldB);
             }
         }
         return;
