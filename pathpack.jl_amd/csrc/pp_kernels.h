@@ -712,7 +712,9 @@ __global__ __launch_bounds__(NT) void k_extract_ref(const T *__restrict__ F, con
 }
 
 // Dpack (Wc x Wc) / Upack / Lpack (e x Wc) of every panel, Wc = the panel's width class; padding holds the semiring
-// zero.  One workgroup per panel.
+// zero.  Dpack's diagonal holds the stars of the panel's diagonal entries (the triangle solves read the diagonal only
+// through its star), so the division of the real semirings' star is made once per entry, not once per row tile.
+// One workgroup per panel.
 template <class S>
 __global__ __launch_bounds__(NT) void k_build_packs(const typename S::value_type *__restrict__ LD,
                                                    const typename S::value_type *__restrict__ LL,
@@ -737,7 +739,12 @@ __global__ __launch_bounds__(NT) void k_build_packs(const typename S::value_type
     const T *Uf = UL + Lptr[f];   // a x c
     for (int q = threadIdx.x; q < Wc * Wc; q += NT) {
         const int j = q / Wc, i = q - j * Wc;
-        Dpack[p_doff[p] + q] = (i < w && j < w) ? D[(lj0 + i) + (i64)(lj0 + j) * a] : S::zero();
+        T d = S::zero();
+        if (i < w && j < w) {
+            d = D[(lj0 + i) + (i64)(lj0 + j) * a];
+            if (i == j) d = S::star(d);
+        }
+        Dpack[p_doff[p] + q] = d;
     }
     for (int q = threadIdx.x; q < Wc * e; q += NT) {
         const int t = q / Wc, j = q - t * Wc;      // element (j, t) at t*Wc + j
@@ -905,7 +912,7 @@ __device__ __forceinline__ void fwd_step(typename S::value_type *__restrict__ X,
             T acc = x[j];
 #pragma unroll
             for (int i = 0; i < j; i++) acc = S::muladd(x[i], DMODE == 0 ? D[i + j * W] : D[j + i * W], acc);
-            if (DMODE == 0 && !S::integral) acc = S::prod(acc, S::star(D[j + j * W]));
+            if (DMODE == 0 && !S::integral) acc = S::prod(acc, D[j + j * W]);
             x[j] = j < w ? acc : S::zero();
         }
 #pragma unroll
@@ -1130,7 +1137,7 @@ __device__ __forceinline__ void bwd_step(typename S::value_type *__restrict__ X,
             T s = acc[j];
 #pragma unroll
             for (int i = 0; i < j; i++) s = S::muladd(acc[i], DMODE == 0 ? D[i + j * W] : D[j + i * W], s);
-            if (DMODE == 0 && !S::integral) s = S::prod(s, S::star(D[j + j * W]));
+            if (DMODE == 0 && !S::integral) s = S::prod(s, D[j + j * W]);
             acc[j] = j < w ? s : S::zero();
         }
     }
@@ -1172,7 +1179,7 @@ __device__ __forceinline__ void bwd_step(typename S::value_type *__restrict__ X,
         T s = acc[j];
 #pragma unroll
         for (int i = j + 1; i < W; i++) s = S::muladd(acc[i], DMODE == 0 ? D[i + j * W] : D[j + i * W], s);
-        if (DMODE == 1 && !S::integral) s = S::prod(s, S::star(D[j + j * W]));
+        if (DMODE == 1 && !S::integral) s = S::prod(s, D[j + j * W]);
         acc[j] = j < w ? s : S::zero();
     }
     if (valid) {
@@ -1251,7 +1258,7 @@ __device__ inline void sub_fwd_panel(typename S::value_type *__restrict__ X, i64
         T acc = x[j];
 #pragma unroll
         for (int i = 0; i < j; i++) acc = S::muladd(x[i], D[i + j * W], acc);
-        if (!S::integral) acc = S::prod(acc, S::star(D[j + j * W]));
+        if (!S::integral) acc = S::prod(acc, D[j + j * W]);
         x[j] = j < w ? acc : S::zero();
     }
     if (e == 0) return;
@@ -1357,7 +1364,7 @@ __device__ inline void sub_bwd_panel(typename S::value_type *__restrict__ X, i64
             T s = acc[j];
 #pragma unroll
             for (int i = 0; i < j; i++) s = S::muladd(acc[i], D[i + j * W], s);
-            if (!S::integral) s = S::prod(s, S::star(D[j + j * W]));
+            if (!S::integral) s = S::prod(s, D[j + j * W]);
             acc[j] = j < w ? s : S::zero();
         }
     }
