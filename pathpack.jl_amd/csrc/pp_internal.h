@@ -136,7 +136,7 @@ struct SweepPlan {
         // offsets into `tiles` of per-panel prefix sums (cnt + 1 entries each): forward units (tiles x chunks)
         // over the star's forward rows, backward tiles over its backward rows, chunks
         i64 pAu, pB64, pC;
-        i64 esum;                    // sum of the panels' gather-list lengths
+        i64 esum, emax;              // sum and maximum of the panels' gather-list lengths
         bool uniB;                   // every panel of the list has the same backward rows [rowB_lo, rowB_hi)
         int32_t rowB_lo, rowB_hi;
         i64 pT[2];                   // block lists: per-block prefix of GEMM tiles for 64 and 128 rows per tile

@@ -2446,10 +2446,11 @@ static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type
             grid = (unsigned)(li.cnt * ((ntile + 7) / 8) * 8);
         }
         // split each row tile's gather list over ks waves when the list has too few tiles to fill the chip (about
-        // 4096 waves), keeping at least 32 gather columns per wave and the split's LDS within 96 KiB
-        const i64 tiles_total = li.cnt * ntile, emean = li.esum / std::max<i64>(1, li.cnt);
+        // 4096 waves), keeping at least 32 gather columns per wave of its longest list (which sets the launch's
+        // duration) and the split's LDS within 96 KiB
+        const i64 tiles_total = li.cnt * ntile;
         int ks = 1;
-        while (ks < 8 && tiles_total * ks < 4096 && emean >= 64 * ks && bwd_lds<T, W>(2 * ks) <= 98304) ks *= 2;
+        while (ks < 8 && tiles_total * ks < 4096 && li.emax >= 64 * ks && bwd_lds<T, W>(2 * ks) <= 98304) ks *= 2;
         if (grid) {
             switch (ks) {
             case 1: launch_bwd<S, W, 1>(grid, dmode, X, ld, a, D, Pk, st); break;
@@ -2579,9 +2580,9 @@ static void launch_list_mixed(bool fwd, int dmode, bool atomic, typename S::valu
     }
     if (!grid) return;
     // as launch_list: split each tile's gather list over ks waves when the list has too few tiles to fill the chip
-    const i64 tiles_total = li.cnt * nt, emean = li.esum / std::max<i64>(1, li.cnt);
+    const i64 tiles_total = li.cnt * nt;
     int ks = 1;
-    while (ks < 8 && tiles_total * ks < 4096 && emean >= 64 * ks && bwd_lds<T, PANEL_W>(2 * ks) <= 98304) ks *= 2;
+    while (ks < 8 && tiles_total * ks < 4096 && li.emax >= 64 * ks && bwd_lds<T, PANEL_W>(2 * ks) <= 98304) ks *= 2;
     switch (ks) {
     case 1: launch_bwd_mixed<S, 1>(grid, dmode, X, ld, a, D, Pk, st); break;
     case 2: launch_bwd_mixed<S, 2>(grid, dmode, X, ld, a, D, Pk, st); break;

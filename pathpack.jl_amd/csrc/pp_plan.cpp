@@ -397,8 +397,11 @@ std::string build_sweep_plan(const Symbolic &S, SweepPlan &P) {
                         return rowtiles(P.rowB_lo[p], P.rowB_hi[p], bm);
                     });
                 }
-            li.esum = 0;
-            for (int32_t p : bucket) li.esum += P.e[p];
+            li.esum = li.emax = 0;
+            for (int32_t p : bucket) {
+                li.esum += P.e[p];
+                li.emax = std::max<i64>(li.emax, P.e[p]);
+            }
             li.uniB = true;
             li.rowB_lo = P.rowB_lo[bucket[0]];
             li.rowB_hi = P.rowB_hi[bucket[0]];
