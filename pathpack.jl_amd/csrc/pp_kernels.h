@@ -2027,30 +2027,32 @@ __global__ __launch_bounds__(NT) void k_permute_cols(T *__restrict__ B, i64 ldb,
     }
 }
 
-// lmul!: Y[r, invp[c]] = B[c, r] (dir 0) or back (dir 1); B n x nrhs (ldb), Y nrhs x n (ld nrhs); 32 x 32 tiles
+// lmul!: Y[r, invp[c]] = B[c, r] (dir 0) or back (dir 1); B n x nrhs (ldb), Y nrhs x n (ld nrhs).  64 x 64 tiles
+// through LDS: both sides move 64 consecutive elements per row of the tile, 16 elements per thread.
 template <class T>
 __global__ __launch_bounds__(NT) void k_transpose_perm(T *__restrict__ B, i64 ldb, T *__restrict__ Y, i64 n, i64 nrhs,
                                                       const i64 *__restrict__ invp, int dir) {
-    __shared__ T tile[32][33];
-    const i64 c0 = (i64)blockIdx.x * 32, r0 = (i64)blockIdx.y * 32;
-    const int tx = threadIdx.x % 32, ty = threadIdx.x / 32;   // 8 rows of 32
+    constexpr int TT = 64, TR = NT / TT;
+    __shared__ T tile[TT][TT + 1];
+    const i64 c0 = (i64)blockIdx.x * TT, r0 = (i64)blockIdx.y * TT;
+    const int tx = threadIdx.x % TT, ty = threadIdx.x / TT;
     if (dir == 0) {
-        for (int k = ty; k < 32; k += 8) {
+        for (int k = ty; k < TT; k += TR) {
             const i64 c = c0 + tx, r = r0 + k;
             if (c < n && r < nrhs) tile[k][tx] = B[c + r * ldb];
         }
         __syncthreads();
-        for (int k = ty; k < 32; k += 8) {
+        for (int k = ty; k < TT; k += TR) {
             const i64 c = c0 + k, r = r0 + tx;
             if (c < n && r < nrhs) Y[r + invp[c] * nrhs] = tile[tx][k];
         }
     } else {
-        for (int k = ty; k < 32; k += 8) {
+        for (int k = ty; k < TT; k += TR) {
             const i64 c = c0 + k, r = r0 + tx;
             if (c < n && r < nrhs) tile[tx][k] = Y[r + invp[c] * nrhs];
         }
         __syncthreads();
-        for (int k = ty; k < 32; k += 8) {
+        for (int k = ty; k < TT; k += TR) {
             const i64 c = c0 + tx, r = r0 + k;
             if (c < n && r < nrhs) B[c + r * ldb] = tile[k][tx];
         }
@@ -2445,12 +2447,12 @@ static void launch_list(bool fwd, int dmode, bool atomic, typename S::value_type
             ntile = (a.nrows + TILE_ROWS - 1) / TILE_ROWS;
             grid = (unsigned)(li.cnt * ((ntile + 7) / 8) * 8);
         }
-        // split each row tile's gather list over ks waves when the list has too few tiles to fill the chip (about
-        // 4096 waves), keeping at least 32 gather columns per wave of its longest list (which sets the launch's
+        // split each row tile's gather list over ks waves when the list has too few tiles to fill the chip (8192
+        // waves: the gathers' latency wants several waves per SIMD), keeping at least 32 gather columns per wave of its longest list (which sets the launch's
         // duration) and the split's LDS within 96 KiB
         const i64 tiles_total = li.cnt * ntile;
         int ks = 1;
-        while (ks < 8 && tiles_total * ks < 4096 && li.emax >= 64 * ks && bwd_lds<T, W>(2 * ks) <= 98304) ks *= 2;
+        while (ks < 8 && tiles_total * ks < 8192 && li.emax >= 64 * ks && bwd_lds<T, W>(2 * ks) <= 98304) ks *= 2;
         if (grid) {
             switch (ks) {
             case 1: launch_bwd<S, W, 1>(grid, dmode, X, ld, a, D, Pk, st); break;
@@ -2582,7 +2584,7 @@ static void launch_list_mixed(bool fwd, int dmode, bool atomic, typename S::valu
     // as launch_list: split each tile's gather list over ks waves when the list has too few tiles to fill the chip
     const i64 tiles_total = li.cnt * nt;
     int ks = 1;
-    while (ks < 8 && tiles_total * ks < 4096 && li.emax >= 64 * ks && bwd_lds<T, PANEL_W>(2 * ks) <= 98304) ks *= 2;
+    while (ks < 8 && tiles_total * ks < 8192 && li.emax >= 64 * ks && bwd_lds<T, PANEL_W>(2 * ks) <= 98304) ks *= 2;
     switch (ks) {
     case 1: launch_bwd_mixed<S, 1>(grid, dmode, X, ld, a, D, Pk, st); break;
     case 2: launch_bwd_mixed<S, 2>(grid, dmode, X, ld, a, D, Pk, st); break;
@@ -3208,7 +3210,7 @@ template <class S> struct SolveRun {
         std::string pe = poison_fill(ctx, Y, (size_t)(n * nrhs) * sizeof(T));
         if (!pe.empty()) return pe;
         timer_start(ctx, 4);
-        const dim3 g((unsigned)((n + 31) / 32), (unsigned)((nrhs + 31) / 32));
+        const dim3 g((unsigned)((n + 63) / 64), (unsigned)((nrhs + 63) / 64));
         auto layout = [&](int dir) {
             if (left) k_transpose_perm<T><<<g, NT, 0, st>>>((T *)B, ldb, Y, n, nrhs, fac->plan.invp, dir);
             else k_permute_cols<T><<<(unsigned)std::min<i64>(n, 65536), NT, 0, st>>>((T *)B, ldb, Y, n, nrhs,
