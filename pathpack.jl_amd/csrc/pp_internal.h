@@ -55,7 +55,7 @@ constexpr int NB = 32;         // pivot block of the blocked front factorization
 constexpr int PANEL_W = 32;    // widest sweep panel
 constexpr int NCLASS = 8;      // sweep width classes 1, 2, 4, 8, 12, 16, 24, 32
 constexpr int TILE_ROWS = 64;    // rows per scatter / backward workgroup (one per lane, 4 waves)
-constexpr int SCATTER_T = 64;    // extension columns per scatter workgroup
+constexpr int SCATTER_T = 32;    // extension columns per scatter workgroup
 constexpr int BLK_W = 128;       // widest star block (the GEMM tile's column count)
 constexpr int BLK_K = 32;        // pack rows are padded to a multiple (of every k step of the block GEMMs)
 constexpr int BLK_CLS = NCLASS;  // list class of star blocks with bn = BLK_W (BLK_CLS + 1: bn = BLK_W / 2)
